@@ -1,0 +1,306 @@
+#!/usr/bin/env python3
+"""BFP8 W8A16 GEMV benchmark on one MI355X.
+
+Workload (default, --workload sweep): the synthetic 24-layer decode-token
+weight sweep at batch 1 -- per layer gate 3584x1024, up 3584x1024, down
+1024x3584, in-projection 6144x1024, out-projection 1024x2048 -- followed by
+the 65536x1024 lm_head with fused greedy argmax + top-40.  Mantissas uniform
+in [-127, 127], exponents uniform in [124, 130] ([122, 128] for the lm_head),
+a fresh N(0,1) activation per GEMV (silu(a)*b with 1% +-20 outliers for the
+down projection).  One step = quantize every activation (one launch) + one
+grouped GEMV launch over all 121 GEMVs and the lm_head, weights resident in
+HBM.  Weight copies rotate (2 sweeps = 1.08 GB) so the 256 MB Infinity Cache
+cannot serve repeats.
+
+value = algorithmic bytes per sweep (weights once + f32 x in + f32 y out; the
+fused lm_head writes no logits) / wall time per step, in GB/s.
+
+Extra workloads for the per-config numbers: --workload lm_head (65536x1024
+fused top-40), gemv (3584x1024), down (1024x3584), batch16 (B=16 x 3584x1024).
+
+    python bench.py [--steps K] [--warmup W] [--workload sweep] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import re
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+PKG = ROOT / "qwen35-ax7020-edge-llm_amd"
+sys.path.insert(0, str(PKG))
+
+PEAK_HBM_GBPS = 8000.0
+LAYER = [("gate", 3584, 1024), ("up", 3584, 1024), ("down", 1024, 3584), ("in_proj", 6144, 1024),
+         ("out_proj", 1024, 2048)]
+N_LAYERS = 24
+LM_HEAD = (65536, 1024)
+TOPK = 40
+
+
+def wbytes(M, K):
+    return M * K + M * (K // 64)
+
+
+def workload_items(name):
+    """[(tag, M, K, e_lo, e_hi, topk)] for one step of a workload."""
+    if name == "sweep":
+        items = [("lm_head", *LM_HEAD, 122, 128, TOPK)]
+        for layer in range(N_LAYERS):
+            items += [(f"l{layer}.{t}", M, K, 124, 130, 0) for t, M, K in LAYER]
+        return items
+    if name == "lm_head":
+        return [("lm_head", *LM_HEAD, 122, 128, TOPK)]
+    if name == "gemv":
+        return [("gemv", 3584, 1024, 124, 130, 0)]
+    if name == "down":
+        return [("down", 1024, 3584, 124, 130, 0)]
+    raise ValueError(name)
+
+
+def metric_bytes(items):
+    """Weights once + f32 activations in + f32 outputs (none for the fused lm_head)."""
+    return sum(wbytes(M, K) + 4 * K + (0 if tk else 4 * M) for _, M, K, _, _, tk in items)
+
+
+def kernel_bytes(items):
+    """Bytes the grouped GEMV kernel must move: weights, int16 activations
+    (split form, 2 B/element) + f32 block scales, f32 outputs."""
+    return sum(wbytes(M, K) + 2 * K + 4 * (K // 64) + (0 if tk else 4 * M) for _, M, K, _, _, tk in items)
+
+
+def read_traffic(workload):
+    """HBM bytes per dispatch from the committed rocprofv3 PMC summary, if any."""
+    p = ROOT / "profiles" / f"{workload}_gemv_pmc.md"
+    if not p.exists():
+        return None
+    m = re.search(r"traffic_bytes_per_dispatch:\s*([0-9.]+)", p.read_text())
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(items, seconds=10.0):
+    """The reference's host bfp8_gemv (float path, 04/qwen_kernels_opt.c:311-325)
+    built from its own sources (oracle/_ref), timed on this host over the same
+    synthetic GEMV list; falls back to the oracle's restatement of that path."""
+    import numpy as np
+
+    import qwen_kernels_gpu as qk
+
+    ref = ROOT / "oracle" / "_ref" / "libref_qwen_kernels.so"
+    port = ROOT / "oracle" / "liboracle.so"
+    if ref.exists():
+        lib = ctypes.CDLL(str(ref))
+        lib.init_kernels()
+        fn, kind = lib.bfp8_gemv, "reference"
+    elif port.exists():
+        lib = ctypes.CDLL(str(port))
+        fn, kind = lib.orc_gemv_float, "port"
+    else:
+        return None
+    fn.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int] * 2
+    fn.restype = None
+    host = []
+    for i, (tag, M, K, lo, hi, tk) in enumerate(items):
+        mant, exps = qk.synth_planes(M, K, 7_000 + i, lo, hi)
+        x = qk.synth_normal(K, 8_000 + i)
+        host.append((mant, exps, x, np.empty(M, dtype=np.float32), M, K))
+    nbytes = metric_bytes(items)
+    t0 = time.perf_counter()
+    sweeps = 0
+    while True:
+        for mant, exps, x, y, M, K in host:
+            fn(y.ctypes.data, x.ctypes.data, mant.ctypes.data, exps.ctypes.data, M, K)
+        sweeps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or sweeps >= 200:
+            break
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count()
+    return {"value": round(nbytes * sweeps / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
+            "sample": f"{sweeps} x the same GEMV list on host planes ({nbytes / 1e6:.1f} MB per pass), "
+                      f"float path with OpenMP over rows, {el:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="sweep", choices=["sweep", "lm_head", "gemv", "down", "batch16"])
+    ap.add_argument("--rotate-gb", type=float, default=1.0, help="rotating weight copies totalling >= this")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py: this build runs on one GPU; the path shards by rows across GPUs "
+              "(see DESIGN.md) but multi-GPU runs are not part of it", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import qwen_kernels_gpu as qk
+
+    torch.cuda.set_device(0)
+    lib = qk.load()
+    lib.init_kernels()
+    if args.workload == "batch16":
+        return bench_batch16(args, qk, torch, np)
+
+    items = workload_items(args.workload)
+    per_copy = sum(wbytes(M, K) for _, M, K, *_ in items)
+    copies = max(1, int(np.ceil(args.rotate_gb * 1e9 / per_copy)))
+    print(f"[bench] {args.workload}: {len(items)} GEMVs, {per_copy / 1e6:.1f} MB weights, {copies} copies",
+          file=sys.stderr, flush=True)
+    xs = []
+    for i, (tag, M, K, lo, hi, tk) in enumerate(items):
+        x = qk.synth_swiglu(K, 5_000 + i) if (K == 3584) else qk.synth_normal(K, 5_000 + i)
+        xs.append(torch.from_numpy(x).cuda())
+    plans, keep = [], []
+    for c in range(copies):
+        plan_items = []
+        for i, (tag, M, K, lo, hi, tk) in enumerate(items):
+            dm = qk.DeviceMatrix.synth(M, K, 1_000_003 * c + i, lo, hi)
+            it = {"mat": dm, "x": xs[i]}
+            if tk:
+                it["topk"] = tk
+            else:
+                it["y"] = torch.empty(M, dtype=torch.float32, device="cuda")
+            plan_items.append(it)
+        plans.append(qk.SweepPlan(plan_items))
+        keep.append(plan_items)
+    torch.cuda.synchronize()
+
+    # warmup, then the timed steps (one quantize + one grouped GEMV launch each)
+    for i in range(args.warmup):
+        plans[i % copies].run()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        plans[i % copies].run()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms_per_step = (t1 - t0) * 1e3 / args.steps
+    mbytes = metric_bytes(items)
+    value = mbytes / (ms_per_step * 1e-3) / 1e9
+    print(f"[bench] timed {args.steps} steps: {ms_per_step * 1e3:.1f} us/step", file=sys.stderr, flush=True)
+
+    # dominant kernel: the grouped GEMV launch alone, HIP events on its stream
+    stream = torch.cuda.current_stream()
+    evs = []
+    for i in range(args.steps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        plans[i % copies].run_gemv()
+        b.record(stream)
+        evs.append((a, b))
+    torch.cuda.synchronize()
+    kus = [a.elapsed_time(b) * 1e3 for a, b in evs]
+    kernel_us = float(np.mean(kus))
+    kbytes = kernel_bytes(items)
+    achieved = kbytes / (kernel_us * 1e-6) / 1e9
+
+    # quantize launch alone
+    qev = []
+    for i in range(min(args.steps, 20)):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        plans[i % copies].quantize()
+        b.record(stream)
+        qev.append((a, b))
+    torch.cuda.synchronize()
+    quant_us = float(np.mean([a.elapsed_time(b) * 1e3 for a, b in qev]))
+
+    # measured read-only ceiling over 1 GiB, and a copy of known size (the
+    # PMC counter calibration kernel)
+    buf = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    buf.fill_(1)
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    for _ in range(2):
+        qk.check(lib.bfp8_dev_read_probe(buf.data_ptr(), buf.numel(), sink.data_ptr(), stream.cuda_stream))
+    rev = []
+    for _ in range(10):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        qk.check(lib.bfp8_dev_read_probe(buf.data_ptr(), buf.numel(), sink.data_ptr(), stream.cuda_stream))
+        b.record(stream)
+        rev.append((a, b))
+    torch.cuda.synchronize()
+    ceiling = buf.numel() / (np.mean([a.elapsed_time(b) for a, b in rev]) * 1e-3) / 1e9
+    cpy = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+    qk.check(lib.bfp8_dev_copy_probe(cpy.data_ptr(), buf.data_ptr(), cpy.numel(), stream.cuda_stream))
+    torch.cuda.synchronize()
+    del buf, cpy
+
+    traffic = read_traffic(args.workload)
+    result = {
+        "metric": "BFP8 GEMV achieved HBM GB/s (% of peak); us per 24-layer decode sweep",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8xint16->int32, f32 epilogue",
+        "data": "synthetic (seeded counter-hash mantissas/exponents, Box-Muller activations)",
+        "config": {"workload": args.workload, "gemvs_per_step": len(items), "batch": 1,
+                   "weight_bytes_per_step": per_copy, "metric_bytes_per_step": mbytes,
+                   "rotating_copies": copies, "parallelism": "single GPU"},
+        "us_per_step": round(ms_per_step * 1e3, 2),
+        "pct_of_peak": round(100 * value / PEAK_HBM_GBPS, 2),
+        "kernel": {"name": "bfp8_gemv_grouped_kernel", "avg_us": round(kernel_us, 2),
+                   "min_us": round(min(kus), 2), "quantize_avg_us": round(quant_us, 2)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": traffic},
+        "hbm_read_ceiling_GBps": round(ceiling, 1),
+        "frac_of_measured_ceiling": round(achieved / ceiling, 4),
+    }
+    if not args.no_cpu:
+        print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = cpu_baseline(items)
+    print(json.dumps(result), flush=True)
+    for p in plans:
+        p.close()
+
+
+def bench_batch16(args, qk, torch, np):
+    M, K, B = 3584, 1024, 16
+    per_copy = wbytes(M, K)
+    copies = max(1, int(np.ceil(args.rotate_gb * 1e9 / per_copy)))
+    mats = [qk.DeviceMatrix.synth(M, K, 900 + c, 124, 130) for c in range(copies)]
+    X = torch.from_numpy(np.stack([qk.synth_normal(K, 950 + b) for b in range(B)])).cuda()
+    xsp = torch.empty(B * K // 64 * 32, dtype=torch.int32, device="cuda")
+    xsc = torch.empty(B * K // 64, dtype=torch.float32, device="cuda")
+    lib = qk.load()
+    for b in range(B):
+        qk.check(lib.bfp8_dev_quantize(None, xsc.data_ptr() + b * (K // 64) * 4, xsp.data_ptr() + b * (K // 64) * 128,
+                                       X[b].data_ptr(), K, torch.cuda.current_stream().cuda_stream))
+    Y = torch.empty((B, M), dtype=torch.float32, device="cuda")
+    for i in range(args.warmup):
+        qk.gemv_batch(mats[i % copies], xsp, xsc, B, Y)
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(s)
+    for i in range(args.steps):
+        qk.gemv_batch(mats[i % copies], xsp, xsc, B, Y)
+    b.record(s)
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) * 1e3 / args.steps
+    gbs = (per_copy + B * 4 * K + B * 4 * M) / (us * 1e-6) / 1e9
+    intops = 2.0 * M * K * B / (us * 1e-6) / 1e12
+    print(json.dumps({"metric": "BFP8 GEMV B=16 achieved GB/s and int Tops/s", "value": round(gbs, 2),
+                      "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+                      "us_per_step": round(us, 3), "int_tops": round(intops, 3), "higher_is_better": True,
+                      "config": {"workload": "batch16", "M": M, "K": K, "B": B}}))
+
+
+if __name__ == "__main__":
+    main()

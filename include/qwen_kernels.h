@@ -1,0 +1,204 @@
+/*
+ * qwen_kernels.h -- C ABI of libqwen_kernels.so, the MI355X (gfx950) drop-in
+ * for the reference's BFP8 GEMV operator library.
+ *
+ * Three groups of entry points:
+ *
+ *  1. Reference symbols, same names, signatures and meaning as the
+ *     reference's libqwen_kernels.so (bound by ctypes in
+ *     04/qwen_real_engine.py:656-725, :848-866).  Host pointers, synchronous:
+ *     y is fully written when the call returns.  The GPU does the work.
+ *
+ *  2. New host-pointer symbols for paths the reference has no entry for
+ *     (fused BFP8 lm_head with argmax / top-k, batched GEMV).  Conventions
+ *     follow 04/qwen_sampling.c:283-285: return a count, 0 on invalid
+ *     arguments.
+ *
+ *  3. Device-level symbols (prefix bfp8_dev_ / bfp8_plan_): device pointers,
+ *     an explicit HIP stream (hipStream_t passed as void*, NULL = the
+ *     library's stream), asynchronous; return 0 on success or a negative
+ *     BFP8_E* code.  These keep weights and activations resident in HBM.
+ *
+ * Failure behaviour: the reference's bfp8_gemv has no error channel
+ * (04/qwen_kernels_opt.c:207, void).  A void entry point of this library
+ * that cannot run on the GPU prints the HIP error to stderr and aborts the
+ * process: there is no silent CPU fallback.  Int-returning entry points
+ * return their error value instead; bfp8_last_error() gives the message.
+ *
+ * Numerics: identical to the reference's board build (-DUSE_NEON):
+ *   - K <= 4096: x quantized per 64-block to int16 (04/qwen_kernels_opt.c:182-205),
+ *     int32 residue-lane block sums, flush-to-zero float epilogue in the
+ *     reference's lane order (:226-277); an odd last row uses the scalar
+ *     order (:279-306).
+ *   - K > 4096: the reference's float path (:311-325).
+ */
+#ifndef QWEN_KERNELS_H
+#define QWEN_KERNELS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(__GNUC__)
+#pragma GCC visibility push(default)
+#endif
+
+/* ---- 1. reference symbols -------------------------------------------------- */
+
+/* Replaces init_kernels(), 04/qwen_kernels_opt.c:128-135.  Also selects the
+ * GPU (current HIP device) and creates the library's stream.  Idempotent. */
+void init_kernels(void);
+
+/* Replaces bfp8_gemv(), 04/qwen_kernels_opt.c:207-326.
+ * y[M] = BFP8 W[M][K] (mantissas int8 [M][K], row stride K; exps uint8
+ * [M][K/64]) times x[K].  Host pointers.  Weights that live in read-only
+ * memory (the engine's PROT_READ mmap, 04/qwen_real_engine.py:745-751) are
+ * converted to the GPU layout once and cached by (mantissas, exps, M, K);
+ * writable weight buffers are re-uploaded on every call. */
+void bfp8_gemv(float* y, const float* x, const int8_t* mantissas, const uint8_t* exps, int M, int K);
+
+/* Replace the stage profiler, 04/qwen_kernels_opt.c:87-91 (same 15 slots and
+ * names).  Slot 0 (bfp8_gemv) accumulates wall milliseconds of bfp8_gemv and
+ * bfp8_gemv_batch; slot 1 (lm_head_argmax) of the fused lm_head calls. */
+void qwen_prof_enable(int on);
+void qwen_prof_reset(void);
+int qwen_prof_count(void);
+double qwen_prof_get(int i);
+const char* qwen_prof_name(int i);
+
+/* ---- 2. new host-pointer symbols ------------------------------------------- */
+
+/* Fused BFP8 lm_head: logits = bfp8_gemv(h) over vocab rows (never
+ * materialised), then the top k by (score desc, id asc) among logits above
+ * -FLT_MAX, exactly the selection of lm_head_topk (04/qwen_sampling.c:283-353).
+ * Returns min(k, #candidates); 0 on invalid arguments (k < 1 or k > 64, odd
+ * vocab, vocab > 262144, hidden not in [64, 4096]). */
+int bfp8_lm_head_topk(const float* h, const int8_t* mantissas, const uint8_t* exps, int vocab,
+                      int hidden, int k, int* out_ids, float* out_scores);
+
+/* Fused BFP8 lm_head argmax with the rule of lm_head_argmax
+ * (04/qwen_kernels_opt.c:401-506): lowest id among the maximal logits above
+ * -1e30, else 0.  Returns -1 on invalid arguments (as bfp8_lm_head_topk). */
+int bfp8_lm_head_argmax(const float* h, const int8_t* mantissas, const uint8_t* exps, int vocab,
+                        int hidden);
+
+/* Y[b][M] = bfp8_gemv(X[b][K]) for b < B, weights read once per batch.  The
+ * reference's equivalent is B separate bfp8_gemv calls (it has no batched
+ * entry, 01/FINAL_REPORT.md:361); results are bit-identical to those. */
+void bfp8_gemv_batch(float* Y, const float* X, const int8_t* mantissas, const uint8_t* exps, int M,
+                     int K, int B);
+
+/* Message of the most recent failure of this library ("" if none). */
+const char* bfp8_last_error(void);
+
+/* Drops every cached device copy of read-only weights. */
+void bfp8_cache_clear(void);
+
+/* ---- 3. device-level symbols ------------------------------------------------ */
+
+#define BFP8_OK 0
+#define BFP8_EINVAL (-1)
+#define BFP8_EHIP (-2)
+#define BFP8_ENOMEM (-3)
+
+/* Bytes of the GPU planes of an M x K BFP8 matrix (bfp8_layout.h). */
+size_t bfp8_dev_mant_bytes(int M, int K);
+size_t bfp8_dev_exps_bytes(int M, int K);
+/* Bytes of the split activation of a K vector (K/64 * 128). */
+size_t bfp8_dev_xsplit_bytes(int K);
+
+/* Converter: the packer's SoA planes (05/bfp8_packer.py:53-86 as sliced by
+ * 04/qwen_real_engine.py:834-846: mantissas [M][K], exps [M][K/64]) to the
+ * GPU planes, and back.  All pointers on the device. */
+int bfp8_dev_pack(int8_t* mant_gpu, uint8_t* exps_gpu, const int8_t* mant_soa,
+                  const uint8_t* exps_soa, int M, int K, void* stream);
+int bfp8_dev_unpack(int8_t* mant_soa, uint8_t* exps_soa, const int8_t* mant_gpu,
+                    const uint8_t* exps_gpu, int M, int K, void* stream);
+
+/* Activation quantizer (04/qwen_kernels_opt.c:182-205) on the device:
+ * x[K] -> xq[K] (may be NULL), xscale[K/64], xsplit (bfp8_dev_xsplit_bytes). */
+int bfp8_dev_quantize(int16_t* xq, float* xscale, uint32_t* xsplit, const float* x, int K,
+                      void* stream);
+
+/* GEMV on quantized activations, K <= 4096.  y[M]; lane_sums (may be NULL)
+ * receives the int32 residue-lane block sums [M][K/64][4] (lane j of block b
+ * = sum over k = j mod 4 of w*xq, the reference's NEON accumulator lanes). */
+int bfp8_dev_gemv(float* y, const uint32_t* xsplit, const float* xscale, const int8_t* mant_gpu,
+                  const uint8_t* exps_gpu, int M, int K, int32_t* lane_sums, void* stream);
+
+/* The reference's float path (04/qwen_kernels_opt.c:311-325) on the device,
+ * unquantized x; the path bfp8_gemv takes for K > 4096. */
+int bfp8_dev_gemv_float(float* y, const float* x, const int8_t* mant_gpu, const uint8_t* exps_gpu,
+                        int M, int K, void* stream);
+
+/* Batched GEMV: Y[B][M]; xsplit is B consecutive split vectors
+ * (bfp8_dev_xsplit_bytes(K) each), xscale B x K/64.  B in 1..16. */
+int bfp8_dev_gemv_batch(float* Y, const uint32_t* xsplit, const float* xscale,
+                        const int8_t* mant_gpu, const uint8_t* exps_gpu, int M, int K, int B,
+                        void* stream);
+
+/* Fused lm_head on quantized activations: outputs on the device (ids[k],
+ * scores[k], count, argmax).  Uses a library-owned device workspace. */
+int bfp8_dev_lm_head_topk(int* out_ids, float* out_scores, int* out_count, int* out_argmax,
+                          const uint32_t* xsplit, const float* xscale, const int8_t* mant_gpu,
+                          const uint8_t* exps_gpu, int vocab, int hidden, int k, void* stream);
+
+/* A sweep plan: many independent GEMVs (and at most one fused lm_head)
+ * executed as one quantize launch plus one grouped GEMV launch.  Item i reads
+ * x (device, K floats) and writes y (device, M floats), or, for the lm_head
+ * item (topk > 0), the four top-k outputs.  Tiles of larger K are issued
+ * first; the lm_head's tiles lead so that its final merge overlaps the rest. */
+typedef struct bfp8_plan_item {
+    const float* x;
+    float* y;
+    const int8_t* mant_gpu;
+    const uint8_t* exps_gpu;
+    int M;
+    int K;
+    int topk;
+    int* out_ids;
+    float* out_scores;
+    int* out_count;
+    int* out_argmax;
+} bfp8_plan_item;
+
+void* bfp8_plan_create(const bfp8_plan_item* items, int n);
+int bfp8_plan_run(void* plan, void* stream);
+/* Only the grouped GEMV launch (activations already quantized by a previous
+ * bfp8_plan_run or bfp8_plan_quantize). */
+int bfp8_plan_run_gemv(void* plan, void* stream);
+int bfp8_plan_quantize(void* plan, void* stream);
+void bfp8_plan_destroy(void* plan);
+
+/* Synthetic reference-format planes on the device: mantissas uniform in
+ * [-127, 127], exponents uniform in [e_lo, e_hi], from a counter-based hash
+ * of (seed, index) -- bfp8_synth_planes_host gives the same bytes. */
+int bfp8_dev_synth_planes(int8_t* mant_soa, uint8_t* exps_soa, int M, int K, uint64_t seed,
+                          int e_lo, int e_hi, void* stream);
+void bfp8_synth_planes_host(int8_t* mant_soa, uint8_t* exps_soa, int M, int K, uint64_t seed,
+                            int e_lo, int e_hi);
+/* x ~ N(0,1) (Box-Muller over the same hash), float32. */
+void bfp8_synth_normal(float* out, int n, uint64_t seed);
+/* silu(a)*b with a, b ~ N(0,1), then a fraction of positions set to +-mag. */
+void bfp8_synth_swiglu(float* out, int n, uint64_t seed, double outlier_frac, float mag);
+
+/* Bandwidth probes for the roofline: a read-only sweep of `bytes` and a
+ * device-to-device copy (used to calibrate hardware byte counters). */
+int bfp8_dev_read_probe(const void* buf, size_t bytes, uint32_t* out, void* stream);
+int bfp8_dev_copy_probe(void* dst, const void* src, size_t bytes, void* stream);
+
+/* The library's HIP stream (hipStream_t as void*). */
+void* bfp8_stream(void);
+
+#if defined(__GNUC__)
+#pragma GCC visibility pop
+#endif
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QWEN_KERNELS_H */

@@ -1,0 +1,342 @@
+// bfp8_ieee.hip -- kernels whose float arithmetic restates the reference's
+// scalar (VFP) code, plus the integer-only kernels of the library.
+//
+// Compiled with IEEE f32 subnormals and -ffp-contract=off; every rounding
+// step below is spelled with __fmul_rn / __fadd_rn / __fdiv_rn so that each
+// C operation of the reference maps to one correctly rounded operation.
+#include <hip/hip_runtime.h>
+
+#include "bfp8_internal.h"
+
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// ---- activation quantizer, 04/qwen_kernels_opt.c:182-205 ------------------
+// One wavefront per 64-element block.
+//   amax = max |x| over the block (a NaN never wins `v > amax`)
+//   amax > 1e-20:  q = 16384/amax, xscale = amax/16384, xq = (int16)lrintf(x*q)
+//   otherwise:     xscale = 0, xq = 0
+// and the split xq = 256*xh + xl written in the residue-major record
+// (bfp8_layout.h) that the GEMV kernels read with scalar loads.
+__device__ __forceinline__ void quantize_block(const Bfp8QuantDesc& d, int b) {
+    const int nb = d.K >> 6;
+    if (b >= nb) return;
+    const int i = threadIdx.x;
+    const float xv = d.x[(size_t)b * 64 + i];
+    const float v = fabsf(xv);
+    float amax = (v > 0.0f) ? v : 0.0f;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        const float o = __shfl_xor(amax, m, 64);
+        amax = (o > amax) ? o : amax;
+    }
+    int xq = 0;
+    float xs = 0.0f;
+    if (amax > 1e-20f) {
+        const float q = __fdiv_rn(16384.0f, amax);
+        xs = __fdiv_rn(amax, 16384.0f);
+        const float p = __fmul_rn(xv, q);
+        // lrintf rounds half to even; a NaN product (x NaN, or inf*0) gives 0.
+        xq = (p == p) ? (int)__builtin_rintf(p) : 0;
+    }
+    if (d.xq) d.xq[(size_t)b * 64 + i] = (int16_t)xq;
+    if (i == 0) d.xscale[b] = xs;
+    const int xl = (int)(int8_t)(xq & 0xff);
+    const int xh = (xq - xl) >> 8;
+    const int res = i & 3, ii = i >> 2;
+    const int pos = res * 32 + (ii >> 2) * 4 + (ii & 3);
+    __shared__ uint32_t rec[32];
+    uint8_t* rb = reinterpret_cast<uint8_t*>(rec);
+    rb[pos] = (uint8_t)xh;
+    rb[pos + 16] = (uint8_t)xl;
+    __syncthreads();
+    if (i < 32) d.xsplit[(size_t)b * 32 + i] = rec[i];
+}
+
+// Residue sum from a 16-byte residue chunk and the split activation record.
+__device__ __forceinline__ int residue_sum_v(u32x4 w, const uint32_t* xb) {
+    int acc = __builtin_amdgcn_sdot4((int)w.x, (int)xb[0], 0, false);
+    acc = __builtin_amdgcn_sdot4((int)w.y, (int)xb[1], acc, false);
+    acc = __builtin_amdgcn_sdot4((int)w.z, (int)xb[2], acc, false);
+    acc = __builtin_amdgcn_sdot4((int)w.w, (int)xb[3], acc, false);
+    acc = (int)((uint32_t)acc << 8);
+    acc = __builtin_amdgcn_sdot4((int)w.x, (int)xb[4], acc, false);
+    acc = __builtin_amdgcn_sdot4((int)w.y, (int)xb[5], acc, false);
+    acc = __builtin_amdgcn_sdot4((int)w.z, (int)xb[6], acc, false);
+    acc = __builtin_amdgcn_sdot4((int)w.w, (int)xb[7], acc, false);
+    return acc;
+}
+
+__device__ __forceinline__ const u32x4* chunk_ptr(const uint8_t* mant, int nb, int row, int b, int q) {
+    const int t = row >> 6, r = row & 63;
+    return reinterpret_cast<const u32x4*>(mant + (((size_t)t * nb + b) * 4 + q) * 1024u + (size_t)r * 16u);
+}
+
+__device__ __forceinline__ uint32_t exp_byte(const uint8_t* exps, int nb, int row, int b) {
+    const int t = row >> 6, r = row & 63, nb4 = (nb + 3) >> 2;
+    return exps[(((size_t)t * nb4 + (b >> 2)) * 64 + r) * 4 + (b & 3)];
+}
+
+}  // namespace
+
+extern "C" __global__ __launch_bounds__(64) void bfp8_quantize_kernel(const Bfp8QuantDesc* __restrict__ descs) {
+    quantize_block(descs[blockIdx.y], blockIdx.x);
+}
+
+extern "C" __global__ __launch_bounds__(64) void bfp8_quantize1_kernel(Bfp8QuantDesc d) {
+    quantize_block(d, blockIdx.x);
+}
+
+// ---- odd-M last row, 04/qwen_kernels_opt.c:279-306 ---------------------------
+// Scalar VFP code: one int32 per block (lane sums added as integers), then
+//   sum = sum + ((float(s) * EXP_SCALE[e]) * xscale[b])   in block order,
+// IEEE subnormals (EXP_SCALE[e] is subnormal for e < 8).  K <= 4096 here.
+extern "C" __global__ __launch_bounds__(64) void bfp8_tail_row_kernel(
+    float* __restrict__ y, const uint32_t* __restrict__ xsplit, const float* __restrict__ xscale,
+    const uint8_t* __restrict__ mant, const uint8_t* __restrict__ exps, int M, int K) {
+    const int m = M - 1;
+    const int nb = K >> 6;
+    const int b = threadIdx.x;
+    __shared__ float prod[64];
+    float p = 0.0f;
+    if (b < nb) {
+        int s = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) s += residue_sum_v(*chunk_ptr(mant, nb, m, b, q), xsplit + ((size_t)b * 4 + q) * 8);
+        const float es = ldexpf(1.0f, (int)exp_byte(exps, nb, m, b) - 134);
+        p = __fmul_rn(__fmul_rn((float)s, es), xscale[b]);
+    }
+    prod[b] = p;
+    __syncthreads();
+    if (b == 0) {
+        float sum = 0.0f;
+        for (int j = 0; j < nb; ++j) sum = __fadd_rn(sum, prod[j]);
+        y[m] = sum;
+    }
+}
+
+// ---- float path, 04/qwen_kernels_opt.c:311-325 (K > 4096 on the board) ------
+// Unquantized x:  block_dot += (float)w * x  (64 sequential steps),
+//                 sum += block_dot * EXP_SCALE[e]  (block order).
+// One wavefront per row; lanes take blocks, lane 0 sums in order.
+extern "C" __global__ __launch_bounds__(64) void bfp8_gemv_float_kernel(
+    float* __restrict__ y, const float* __restrict__ x, const uint8_t* __restrict__ mant,
+    const uint8_t* __restrict__ exps, int M, int K) {
+    extern __shared__ float prods[];
+    const int m = blockIdx.x;
+    const int nb = K >> 6;
+    for (int b = threadIdx.x; b < nb; b += 64) {
+        u32x4 c[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) c[q] = *chunk_ptr(mant, nb, m, b, q);
+        const float* xb = x + (size_t)b * 64;
+        float dot = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 64; ++k) {
+            // element k sits in residue chunk k&3, byte k>>2
+            const int i = k >> 2;
+            const uint32_t word = c[k & 3][i >> 2];
+            const int w = (int)(int8_t)((word >> (8 * (i & 3))) & 0xffu);
+            dot = __fadd_rn(dot, __fmul_rn((float)w, xb[k]));
+        }
+        const float es = ldexpf(1.0f, (int)exp_byte(exps, nb, m, b) - 134);
+        prods[b] = __fmul_rn(dot, es);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float sum = 0.0f;
+        for (int b = 0; b < nb; ++b) sum = __fadd_rn(sum, prods[b]);
+        y[m] = sum;
+    }
+}
+
+// ---- layout converter: reference SoA planes <-> GPU planes --------------------
+// One thread per (row tile lane, block): reads the 64 mantissas of a block
+// (row stride K, as the engine slices them) and writes the four residue
+// chunks; rows past M are zero.
+extern "C" __global__ __launch_bounds__(256) void bfp8_pack_mant_kernel(
+    uint8_t* __restrict__ mg, const int8_t* __restrict__ ms, int M, int K) {
+    const int nb = K >> 6;
+    const size_t total = (size_t)bfp8_ntiles(M) * 64u * nb;
+    for (size_t g = (size_t)blockIdx.x * blockDim.x + threadIdx.x; g < total;
+         g += (size_t)gridDim.x * blockDim.x) {
+        const int r = (int)(g & 63);
+        const size_t tb = g >> 6;
+        const int b = (int)(tb % nb);
+        const int t = (int)(tb / nb);
+        const int row = t * 64 + r;
+        u32x4 out[4] = {u32x4(0u), u32x4(0u), u32x4(0u), u32x4(0u)};
+        if (row < M) {
+            const int8_t* src = ms + (size_t)row * K + (size_t)b * 64;
+            for (int k = 0; k < 64; ++k) {
+                const int q = k & 3, i = k >> 2;
+                out[q][i >> 2] |= ((uint32_t)(uint8_t)src[k]) << (8 * (i & 3));
+            }
+        }
+        for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<u32x4*>(mg + (((size_t)t * nb + b) * 4 + q) * 1024u + (size_t)r * 16u) = out[q];
+    }
+}
+
+extern "C" __global__ __launch_bounds__(256) void bfp8_pack_exps_kernel(
+    uint8_t* __restrict__ eg, const uint8_t* __restrict__ es, int M, int K) {
+    const int nb = K >> 6, nb4 = (nb + 3) >> 2;
+    const size_t total = (size_t)bfp8_ntiles(M) * nb4 * 64u;
+    for (size_t g = (size_t)blockIdx.x * blockDim.x + threadIdx.x; g < total;
+         g += (size_t)gridDim.x * blockDim.x) {
+        const int r = (int)(g & 63);
+        const size_t tg = g >> 6;
+        const int grp = (int)(tg % nb4);
+        const int t = (int)(tg / nb4);
+        const int row = t * 64 + r;
+        uint32_t word = 0;
+        for (int p = 0; p < 4; ++p) {
+            const int b = grp * 4 + p;
+            if (row < M && b < nb) word |= (uint32_t)es[(size_t)row * nb + b] << (8 * p);
+        }
+        reinterpret_cast<uint32_t*>(eg)[g] = word;
+    }
+}
+
+extern "C" __global__ __launch_bounds__(256) void bfp8_unpack_kernel(
+    int8_t* __restrict__ ms, uint8_t* __restrict__ es, const uint8_t* __restrict__ mg,
+    const uint8_t* __restrict__ eg, int M, int K) {
+    const int nb = K >> 6;
+    const size_t total = (size_t)M * nb;
+    for (size_t g = (size_t)blockIdx.x * blockDim.x + threadIdx.x; g < total;
+         g += (size_t)gridDim.x * blockDim.x) {
+        const int row = (int)(g / nb), b = (int)(g % nb);
+        u32x4 c[4];
+        for (int q = 0; q < 4; ++q) c[q] = *chunk_ptr(mg, nb, row, b, q);
+        int8_t* dst = ms + (size_t)row * K + (size_t)b * 64;
+        for (int k = 0; k < 64; ++k) {
+            const int i = k >> 2;
+            dst[k] = (int8_t)((c[k & 3][i >> 2] >> (8 * (i & 3))) & 0xffu);
+        }
+        es[(size_t)row * nb + b] = (uint8_t)exp_byte(eg, nb, row, b);
+    }
+}
+
+// ---- synthetic reference-format planes (counter-based, host-reproducible) ----
+extern "C" __global__ __launch_bounds__(256) void bfp8_synth_kernel(
+    int8_t* __restrict__ ms, uint8_t* __restrict__ es, size_t nm, size_t ne, uint64_t seed, int lo, int hi) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < nm; i += stride)
+        ms[i] = bfp8_synth_mant(seed, i);
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < ne; i += stride)
+        es[i] = bfp8_synth_exp(seed, i, lo, hi);
+}
+
+// ---- bandwidth probes -----------------------------------------------------------
+// Read-only ceiling: dwordx4 grid-stride reads folded into one word per thread
+// block (so the loads cannot be dropped).
+extern "C" __global__ __launch_bounds__(256) void bfp8_read_probe_kernel(
+    const u32x4* __restrict__ src, size_t n16, uint32_t* __restrict__ out) {
+    u32x4 acc = u32x4(0u);
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    for (; i + 3 * stride < n16; i += 4 * stride) {
+        u32x4 a = __builtin_nontemporal_load(src + i);
+        u32x4 b = __builtin_nontemporal_load(src + i + stride);
+        u32x4 c = __builtin_nontemporal_load(src + i + 2 * stride);
+        u32x4 d = __builtin_nontemporal_load(src + i + 3 * stride);
+        acc ^= a ^ b ^ c ^ d;
+    }
+    for (; i < n16; i += stride) acc ^= __builtin_nontemporal_load(src + i);
+    uint32_t v = acc.x ^ acc.y ^ acc.z ^ acc.w;
+    for (int m = 32; m >= 1; m >>= 1) v ^= (uint32_t)__shfl_xor((int)v, m, 64);
+    if ((threadIdx.x & 63) == 0) atomicXor(out, v);
+}
+
+extern "C" __global__ __launch_bounds__(256) void bfp8_copy_probe_kernel(
+    u32x4* __restrict__ dst, const u32x4* __restrict__ src, size_t n16) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) dst[i] = src[i];
+}
+
+// ---- launchers ----------------------------------------------------------------------
+static int grid_for(size_t work, int per_block) {
+    size_t g = (work + per_block - 1) / per_block;
+    if (g > 65536) g = 65536;
+    if (g < 1) g = 1;
+    return (int)g;
+}
+
+hipError_t bfp8_launch_quantize(const Bfp8QuantDesc* descs_dev, int ndesc, int max_nb, hipStream_t s) {
+    if (ndesc <= 0 || max_nb <= 0) return hipSuccess;
+    hipLaunchKernelGGL(bfp8_quantize_kernel, dim3(max_nb, ndesc), dim3(64), 0, s, descs_dev);
+    return hipGetLastError();
+}
+
+hipError_t bfp8_launch_quantize1(const Bfp8QuantDesc& d, hipStream_t s) {
+    const int nb = bfp8_nblocks(d.K);
+    if (nb <= 0) return hipSuccess;
+    hipLaunchKernelGGL(bfp8_quantize1_kernel, dim3(nb), dim3(64), 0, s, d);
+    return hipGetLastError();
+}
+
+hipError_t bfp8_launch_tail_row(float* y, const uint32_t* xsplit, const float* xscale,
+                                const uint8_t* mant, const uint8_t* exps, int M, int K, hipStream_t s) {
+    if (M <= 0 || !(M & 1)) return hipSuccess;
+    if (bfp8_nblocks(K) > 64) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(bfp8_tail_row_kernel, dim3(1), dim3(64), 0, s, y, xsplit, xscale, mant, exps, M, K);
+    return hipGetLastError();
+}
+
+hipError_t bfp8_launch_gemv_float(float* y, const float* x, const uint8_t* mant, const uint8_t* exps,
+                                  int M, int K, hipStream_t s) {
+    if (M <= 0) return hipSuccess;
+    const int nb = bfp8_nblocks(K);
+    if (nb > 16384) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(bfp8_gemv_float_kernel, dim3(M), dim3(64), (size_t)(nb > 0 ? nb : 1) * 4, s, y, x,
+                       mant, exps, M, K);
+    return hipGetLastError();
+}
+
+hipError_t bfp8_launch_pack(uint8_t* mant_gpu, uint8_t* exps_gpu, const int8_t* mant_soa,
+                            const uint8_t* exps_soa, int M, int K, hipStream_t s) {
+    const int nb = bfp8_nblocks(K);
+    if (M <= 0 || nb <= 0) return hipSuccess;
+    const size_t wm = (size_t)bfp8_ntiles(M) * 64u * nb;
+    hipLaunchKernelGGL(bfp8_pack_mant_kernel, dim3(grid_for(wm, 256)), dim3(256), 0, s, mant_gpu, mant_soa, M, K);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const size_t we = (size_t)bfp8_ntiles(M) * bfp8_nb4(nb) * 64u;
+    hipLaunchKernelGGL(bfp8_pack_exps_kernel, dim3(grid_for(we, 256)), dim3(256), 0, s, exps_gpu, exps_soa, M, K);
+    return hipGetLastError();
+}
+
+hipError_t bfp8_launch_unpack(int8_t* mant_soa, uint8_t* exps_soa, const uint8_t* mant_gpu,
+                              const uint8_t* exps_gpu, int M, int K, hipStream_t s) {
+    const int nb = bfp8_nblocks(K);
+    if (M <= 0 || nb <= 0) return hipSuccess;
+    const size_t w = (size_t)M * nb;
+    hipLaunchKernelGGL(bfp8_unpack_kernel, dim3(grid_for(w, 256)), dim3(256), 0, s, mant_soa, exps_soa, mant_gpu,
+                       exps_gpu, M, K);
+    return hipGetLastError();
+}
+
+hipError_t bfp8_launch_synth_planes(int8_t* mant_soa, uint8_t* exps_soa, int M, int K, uint64_t seed,
+                                    int e_lo, int e_hi, hipStream_t s) {
+    if (M <= 0 || K <= 0) return hipSuccess;
+    const size_t nm = (size_t)M * K, ne = (size_t)M * bfp8_nblocks(K);
+    hipLaunchKernelGGL(bfp8_synth_kernel, dim3(grid_for(nm, 256 * 16)), dim3(256), 0, s, mant_soa, exps_soa, nm,
+                       ne, seed, e_lo, e_hi);
+    return hipGetLastError();
+}
+
+hipError_t bfp8_launch_read_probe(const void* buf, size_t bytes, uint32_t* out, hipStream_t s) {
+    const size_t n16 = bytes / 16;
+    if (n16 == 0) return hipSuccess;
+    hipLaunchKernelGGL(bfp8_read_probe_kernel, dim3(256 * 16), dim3(256), 0, s, (const u32x4*)buf, n16, out);
+    return hipGetLastError();
+}
+
+hipError_t bfp8_launch_copy_probe(void* dst, const void* src, size_t bytes, hipStream_t s) {
+    const size_t n16 = bytes / 16;
+    if (n16 == 0) return hipSuccess;
+    hipLaunchKernelGGL(bfp8_copy_probe_kernel, dim3(grid_for(n16, 256 * 4)), dim3(256), 0, s, (u32x4*)dst,
+                       (const u32x4*)src, n16);
+    return hipGetLastError();
+}

@@ -1,0 +1,98 @@
+// bfp8_internal.h -- kernel descriptors and launchers shared by the two kernel
+// translation units and the C-ABI host code.  Not part of the public ABI.
+//
+//   bfp8_ftz.hip   kernels whose float arithmetic restates the reference's
+//                  Advanced SIMD code: compiled with f32 flush-to-zero, no
+//                  contraction (GEMV, grouped GEMV + fused lm_head top-k,
+//                  batched GEMV).
+//   bfp8_ieee.hip  kernels whose float arithmetic restates the reference's
+//                  scalar VFP code: IEEE subnormals, no contraction
+//                  (activation quantizer, odd-M last row, K > 4096 float
+//                  path), plus integer-only kernels (layout conversion,
+//                  synthetic planes, bandwidth probes).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "bfp8_layout.h"
+
+// One GEMV of a grouped launch (or the only one of a single launch).
+struct Bfp8GemvDesc {
+    const uint8_t* mant;     // GPU mantissa plane (bfp8_layout.h)
+    const uint8_t* exps;     // GPU exponent plane
+    const uint32_t* xsplit;  // split activation, NB*32 words
+    const float* xscale;     // NB per-block activation scales
+    float* y;                // M outputs (rows < pair_rows are written), may be null
+    int32_t* lanes;          // optional [M][NB][4] residue-lane sums (debug), may be null
+    int M, K;
+    int pair_rows;           // rows computed with the paired (NEON) epilogue: M & ~1
+    int topk;                // 0: plain GEMV; 1..64: fused lm_head top-k over the rows
+    uint64_t* partials;      // [ntiles][topk] per-tile sorted keys (topk > 0)
+    uint32_t* counter;       // tiles finished; zero between launches (topk > 0)
+    int* out_ids;            // [topk]
+    float* out_scores;       // [topk]
+    int* out_count;          // number of valid entries
+    int* out_argmax;         // lm_head_argmax-rule winner
+};
+
+// One activation vector to quantize.
+struct Bfp8QuantDesc {
+    const float* x;
+    int16_t* xq;       // K (may be null)
+    float* xscale;     // K/64
+    uint32_t* xsplit;  // K/64 * 32 words
+    int K;
+    int pad_;
+};
+
+// Grouped-launch work item: which descriptor and which row tile.
+struct Bfp8TileRef {
+    int desc;
+    int tile;
+};
+
+#define BFP8_TOPK_MAX 64
+#define BFP8_TOPK_MAX_TILES 4096
+#define BFP8_TOPK_LDS_BYTES (4096 * 8)
+
+// ---- bfp8_ftz.hip --------------------------------------------------------
+hipError_t bfp8_launch_gemv(const Bfp8GemvDesc& d, hipStream_t s);
+hipError_t bfp8_launch_gemv_grouped(const Bfp8GemvDesc* descs_dev, const Bfp8TileRef* tiles_dev,
+                                    int ntiles, bool any_topk, hipStream_t s);
+hipError_t bfp8_launch_gemv_batch(float* Y, const uint32_t* xsplit, const float* xscale,
+                                  const uint8_t* mant, const uint8_t* exps, int M, int K, int B,
+                                  hipStream_t s);
+
+// ---- bfp8_ieee.hip -------------------------------------------------------
+hipError_t bfp8_launch_quantize(const Bfp8QuantDesc* descs_dev, int ndesc, int max_nb, hipStream_t s);
+hipError_t bfp8_launch_quantize1(const Bfp8QuantDesc& d, hipStream_t s);
+hipError_t bfp8_launch_tail_row(float* y, const uint32_t* xsplit, const float* xscale,
+                                const uint8_t* mant, const uint8_t* exps, int M, int K, hipStream_t s);
+hipError_t bfp8_launch_gemv_float(float* y, const float* x, const uint8_t* mant, const uint8_t* exps,
+                                  int M, int K, hipStream_t s);
+hipError_t bfp8_launch_pack(uint8_t* mant_gpu, uint8_t* exps_gpu, const int8_t* mant_soa,
+                            const uint8_t* exps_soa, int M, int K, hipStream_t s);
+hipError_t bfp8_launch_unpack(int8_t* mant_soa, uint8_t* exps_soa, const uint8_t* mant_gpu,
+                              const uint8_t* exps_gpu, int M, int K, hipStream_t s);
+hipError_t bfp8_launch_synth_planes(int8_t* mant_soa, uint8_t* exps_soa, int M, int K, uint64_t seed,
+                                    int e_lo, int e_hi, hipStream_t s);
+hipError_t bfp8_launch_read_probe(const void* buf, size_t bytes, uint32_t* out, hipStream_t s);
+hipError_t bfp8_launch_copy_probe(void* dst, const void* src, size_t bytes, hipStream_t s);
+
+// ---- synthetic inputs (shared host/device integer hash) -------------------
+// splitmix64 finaliser over (seed, index): the same integers on host and GPU.
+BFP8_HD static inline uint64_t bfp8_hash64(uint64_t seed, uint64_t idx) {
+    uint64_t z = seed + (idx + 1u) * 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+// Mantissa of element i: uniform in [-127, 127].
+BFP8_HD static inline int8_t bfp8_synth_mant(uint64_t seed, uint64_t i) {
+    return (int8_t)((int)((bfp8_hash64(seed, i) >> 32) % 255u) - 127);
+}
+// Exponent of block i: uniform in [lo, hi].
+BFP8_HD static inline uint8_t bfp8_synth_exp(uint64_t seed, uint64_t i, int lo, int hi) {
+    uint64_t h = bfp8_hash64(seed ^ 0xE7E7E7E7E7E7E7E7ull, i);
+    return (uint8_t)(lo + (int)((h >> 32) % (uint64_t)(hi - lo + 1)));
+}

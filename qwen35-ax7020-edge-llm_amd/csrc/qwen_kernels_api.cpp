@@ -1,0 +1,813 @@
+// qwen_kernels_api.cpp -- host side of libqwen_kernels.so (C ABI in
+// include/qwen_kernels.h).  Owns the device, a HIP stream, device
+// workspaces, pinned staging buffers, the read-only weight cache and the
+// grouped-GEMV plans.  All arithmetic runs in the HIP kernels of bfp8_ftz.hip
+// and bfp8_ieee.hip; nothing here computes results on the CPU.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <ctime>
+#include <map>
+#include <mutex>
+#include <string>
+#include <tuple>
+#include <vector>
+
+#include "bfp8_internal.h"
+#include "qwen_kernels.h"
+
+namespace {
+
+// ---- errors ---------------------------------------------------------------------
+std::mutex g_err_mu;
+std::string g_err;
+
+void set_error(const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    std::lock_guard<std::mutex> lk(g_err_mu);
+    g_err = buf;
+}
+
+[[noreturn]] void fatal(const char* where) {
+    std::string msg;
+    {
+        std::lock_guard<std::mutex> lk(g_err_mu);
+        msg = g_err;
+    }
+    fprintf(stderr, "libqwen_kernels: %s failed on the GPU: %s (no CPU fallback; aborting)\n", where,
+            msg.c_str());
+    fflush(stderr);
+    abort();
+}
+
+#define HIP_OK(expr)                                                                   \
+    do {                                                                               \
+        hipError_t e_ = (expr);                                                        \
+        if (e_ != hipSuccess) {                                                        \
+            set_error("%s: %s (%s:%d)", #expr, hipGetErrorString(e_), __FILE__, __LINE__); \
+            return BFP8_EHIP;                                                          \
+        }                                                                              \
+    } while (0)
+
+// ---- profiler slots: names and order of 04/qwen_kernels_opt.c:66-78 ----------------
+enum { QP_GEMV = 0, QP_LMHEAD = 1, QP_N = 15 };
+const char* const kProfNames[QP_N] = {
+    "bfp8_gemv", "lm_head_argmax", "gdn_recurrent_step", "conv1d_silu", "swiglu", "rmsnorm",
+    "gdn_gates", "qk_l2norm", "rmsnorm_gated", "add_residual", "embed_lookup", "py_full_attn",
+    "forward_linear_layer", "forward_mlp", "forward_token_c"};
+int g_prof_on = 0;
+double g_prof_ms[QP_N];
+
+double now_ms() {
+    timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (double)ts.tv_sec * 1e3 + (double)ts.tv_nsec / 1e6;
+}
+
+struct ProfScope {
+    int slot;
+    double t0;
+    explicit ProfScope(int s) : slot(s), t0(g_prof_on ? now_ms() : 0.0) {}
+    ~ProfScope() {
+        if (g_prof_on) g_prof_ms[slot] += now_ms() - t0;
+    }
+};
+
+// ---- device buffers -------------------------------------------------------------------
+struct DevBuf {
+    void* p = nullptr;
+    size_t n = 0;
+    int reserve(size_t bytes) {
+        if (bytes <= n) return BFP8_OK;
+        if (p) HIP_OK(hipFree(p));
+        p = nullptr;
+        n = 0;
+        size_t want = std::max<size_t>(bytes, 256);
+        HIP_OK(hipMalloc(&p, want));
+        n = want;
+        return BFP8_OK;
+    }
+    void release() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        n = 0;
+    }
+    template <class T>
+    T* as() const {
+        return static_cast<T*>(p);
+    }
+};
+
+struct PinnedBuf {
+    void* p = nullptr;
+    size_t n = 0;
+    int reserve(size_t bytes) {
+        if (bytes <= n) return BFP8_OK;
+        if (p) HIP_OK(hipHostFree(p));
+        p = nullptr;
+        n = 0;
+        size_t want = std::max<size_t>(bytes, 4096);
+        HIP_OK(hipHostMalloc(&p, want, hipHostMallocDefault));
+        n = want;
+        return BFP8_OK;
+    }
+};
+
+struct CachedWeights {
+    DevBuf mant, exps;
+};
+
+using WeightKey = std::tuple<const void*, const void*, int, int>;
+
+struct State {
+    std::mutex mu;
+    bool ready = false;
+    int device = 0;
+    hipStream_t stream = nullptr;
+    PinnedBuf h_in, h_out;
+    DevBuf x, xq, xscale, xsplit, y;            // activation / output workspace
+    DevBuf soa_m, soa_e, gpu_m, gpu_e;          // per-call weight upload
+    DevBuf tk_partials, tk_counter, tk_out;     // fused lm_head workspace
+    std::map<WeightKey, CachedWeights> cache;
+    size_t cache_bytes = 0;
+};
+
+State g;
+constexpr size_t kCacheLimit = (size_t)200 << 30;
+
+int ensure_init_locked() {
+    if (g.ready) return BFP8_OK;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n <= 0) {
+        set_error("no HIP device available (%s)", hipGetErrorString(e));
+        return BFP8_EHIP;
+    }
+    HIP_OK(hipGetDevice(&g.device));
+    HIP_OK(hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking));
+    // tk_counter must start at zero; the fused lm_head's last workgroup
+    // resets it after every launch.
+    if (g.tk_counter.reserve(256) != BFP8_OK) return BFP8_EHIP;
+    HIP_OK(hipMemset(g.tk_counter.p, 0, g.tk_counter.n));
+    g.ready = true;
+    return BFP8_OK;
+}
+
+hipStream_t pick_stream(void* s) { return s ? static_cast<hipStream_t>(s) : g.stream; }
+
+// Is every page of [p, p+n) mapped without write permission?
+bool range_readonly(const void* p, size_t n) {
+    if (!p || n == 0) return false;
+    FILE* f = fopen("/proc/self/maps", "r");
+    if (!f) return false;
+    uintptr_t cur = (uintptr_t)p, end = cur + n;
+    char line[512];
+    bool ok = false;
+    while (fgets(line, sizeof line, f)) {
+        unsigned long lo = 0, hi = 0;
+        char perms[8] = {0};
+        if (sscanf(line, "%lx-%lx %7s", &lo, &hi, perms) != 3) continue;
+        if (hi <= cur) continue;
+        if (lo > cur || perms[1] == 'w') break;  // gap or writable
+        cur = hi;
+        if (cur >= end) {
+            ok = true;
+            break;
+        }
+    }
+    fclose(f);
+    return ok;
+}
+
+struct DevWeights {
+    const uint8_t* mant;
+    const uint8_t* exps;
+};
+
+// Device GPU-layout planes for host reference planes.
+int weights_for(const int8_t* mant, const uint8_t* exps, int M, int K, DevWeights* out) {
+    const int nb = bfp8_nblocks(K);
+    const size_t mbytes = (size_t)M * (size_t)K, ebytes = (size_t)M * (size_t)nb;
+    const WeightKey key{mant, exps, M, K};
+    auto it = g.cache.find(key);
+    if (it != g.cache.end()) {
+        out->mant = it->second.mant.as<uint8_t>();
+        out->exps = it->second.exps.as<uint8_t>();
+        return BFP8_OK;
+    }
+    int rc;
+    if ((rc = g.soa_m.reserve(mbytes)) || (rc = g.soa_e.reserve(ebytes))) return rc;
+    HIP_OK(hipMemcpyAsync(g.soa_m.p, mant, mbytes, hipMemcpyHostToDevice, g.stream));
+    HIP_OK(hipMemcpyAsync(g.soa_e.p, exps, ebytes, hipMemcpyHostToDevice, g.stream));
+    const size_t gm = bfp8_gpu_mant_bytes(M, K), ge = bfp8_gpu_exps_bytes(M, K);
+    const bool cacheable = g.cache_bytes + gm + ge <= kCacheLimit &&
+                           range_readonly(mant, mbytes) && range_readonly(exps, ebytes);
+    DevBuf* dm = &g.gpu_m;
+    DevBuf* de = &g.gpu_e;
+    CachedWeights cw;
+    if (cacheable) {
+        dm = &cw.mant;
+        de = &cw.exps;
+    }
+    if ((rc = dm->reserve(gm)) || (rc = de->reserve(ge))) return rc;
+    HIP_OK(bfp8_launch_pack(dm->as<uint8_t>(), de->as<uint8_t>(), g.soa_m.as<int8_t>(),
+                            g.soa_e.as<uint8_t>(), M, K, g.stream));
+    out->mant = dm->as<uint8_t>();
+    out->exps = de->as<uint8_t>();
+    if (cacheable) {
+        g.cache_bytes += cw.mant.n + cw.exps.n;
+        g.cache.emplace(key, cw);
+    }
+    return BFP8_OK;
+}
+
+int upload_x(const float* x, size_t nfloat) {
+    int rc;
+    if ((rc = g.h_in.reserve(nfloat * 4)) || (rc = g.x.reserve(nfloat * 4))) return rc;
+    memcpy(g.h_in.p, x, nfloat * 4);
+    HIP_OK(hipMemcpyAsync(g.x.p, g.h_in.p, nfloat * 4, hipMemcpyHostToDevice, g.stream));
+    return BFP8_OK;
+}
+
+int quantize_ws(int K, int B) {
+    int rc;
+    const int nb = bfp8_nblocks(K);
+    if ((rc = g.xq.reserve((size_t)B * nb * 64 * 2)) || (rc = g.xscale.reserve((size_t)B * nb * 4)) ||
+        (rc = g.xsplit.reserve((size_t)B * bfp8_xsplit_bytes(K))))
+        return rc;
+    for (int b = 0; b < B; ++b) {
+        Bfp8QuantDesc q{};
+        q.x = g.x.as<float>() + (size_t)b * nb * 64;
+        q.xq = g.xq.as<int16_t>() + (size_t)b * nb * 64;
+        q.xscale = g.xscale.as<float>() + (size_t)b * nb;
+        q.xsplit = g.xsplit.as<uint32_t>() + (size_t)b * nb * 32;
+        q.K = K;
+        HIP_OK(bfp8_launch_quantize1(q, g.stream));
+    }
+    return BFP8_OK;
+}
+
+Bfp8GemvDesc plain_desc(float* y, const uint32_t* xsplit, const float* xscale, const uint8_t* m,
+                        const uint8_t* e, int M, int K, int32_t* lanes) {
+    Bfp8GemvDesc d{};
+    d.mant = m;
+    d.exps = e;
+    d.xsplit = xsplit;
+    d.xscale = xscale;
+    d.y = y;
+    d.lanes = lanes;
+    d.M = M;
+    d.K = K;
+    d.pair_rows = M & ~1;
+    return d;
+}
+
+// Quantized GEMV on the device (K <= 4096): paired rows + odd last row.
+int gemv_q(float* y, const uint32_t* xsplit, const float* xscale, const uint8_t* m, const uint8_t* e,
+           int M, int K, int32_t* lanes, hipStream_t s) {
+    HIP_OK(bfp8_launch_gemv(plain_desc(y, xsplit, xscale, m, e, M, K, lanes), s));
+    HIP_OK(bfp8_launch_tail_row(y, xsplit, xscale, m, e, M, K, s));
+    return BFP8_OK;
+}
+
+int host_gemv(float* y, const float* x, const int8_t* mant, const uint8_t* exps, int M, int K) {
+    const int nb = bfp8_nblocks(K);
+    if (nb == 0) {  // no whole block: the reference's accumulators stay 0
+        memset(y, 0, (size_t)M * sizeof(float));
+        return BFP8_OK;
+    }
+    int rc;
+    DevWeights w;
+    if ((rc = weights_for(mant, exps, M, K, &w))) return rc;
+    if ((rc = upload_x(x, (size_t)nb * 64))) return rc;
+    if ((rc = g.y.reserve((size_t)M * 4)) || (rc = g.h_out.reserve((size_t)M * 4))) return rc;
+    if (K <= 4096) {
+        if ((rc = quantize_ws(K, 1))) return rc;
+        if ((rc = gemv_q(g.y.as<float>(), g.xsplit.as<uint32_t>(), g.xscale.as<float>(), w.mant, w.exps,
+                         M, K, nullptr, g.stream)))
+            return rc;
+    } else {
+        HIP_OK(bfp8_launch_gemv_float(g.y.as<float>(), g.x.as<float>(), w.mant, w.exps, M, K, g.stream));
+    }
+    HIP_OK(hipMemcpyAsync(g.h_out.p, g.y.p, (size_t)M * 4, hipMemcpyDeviceToHost, g.stream));
+    HIP_OK(hipStreamSynchronize(g.stream));
+    memcpy(y, g.h_out.p, (size_t)M * 4);
+    return BFP8_OK;
+}
+
+bool lm_head_args_ok(int vocab, int hidden, int k) {
+    return vocab > 0 && !(vocab & 1) && bfp8_ntiles(vocab) <= BFP8_TOPK_MAX_TILES && hidden >= 64 &&
+           hidden <= 4096 && k >= 1 && k <= BFP8_TOPK_MAX;
+}
+
+int lm_head_dev(int* ids, float* scores, int* count, int* argmax, const uint32_t* xsplit,
+                const float* xscale, const uint8_t* m, const uint8_t* e, int vocab, int hidden, int k,
+                hipStream_t s) {
+    const int kk = std::min(k, vocab);
+    int rc;
+    if ((rc = g.tk_partials.reserve((size_t)bfp8_ntiles(vocab) * kk * 8))) return rc;
+    Bfp8GemvDesc d = plain_desc(nullptr, xsplit, xscale, m, e, vocab, hidden, nullptr);
+    d.topk = kk;
+    d.partials = g.tk_partials.as<uint64_t>();
+    d.counter = g.tk_counter.as<uint32_t>();
+    d.out_ids = ids;
+    d.out_scores = scores;
+    d.out_count = count;
+    d.out_argmax = argmax;
+    HIP_OK(bfp8_launch_gemv(d, s));
+    return BFP8_OK;
+}
+
+int host_lm_head(const float* h, const int8_t* mant, const uint8_t* exps, int vocab, int hidden, int k,
+                 int* out_ids, float* out_scores, int* out_argmax) {
+    int rc;
+    DevWeights w;
+    if ((rc = weights_for(mant, exps, vocab, hidden, &w))) return rc;
+    const int nb = bfp8_nblocks(hidden);
+    if ((rc = upload_x(h, (size_t)nb * 64)) || (rc = quantize_ws(hidden, 1))) return rc;
+    const int kk = std::min(k, vocab);
+    if ((rc = g.tk_out.reserve((size_t)(2 * kk + 2) * 4)) || (rc = g.h_out.reserve((size_t)(2 * kk + 2) * 4)))
+        return rc;
+    int* d_ids = g.tk_out.as<int>();
+    float* d_scores = reinterpret_cast<float*>(d_ids + kk);
+    int* d_cnt = d_ids + 2 * kk;
+    if ((rc = lm_head_dev(d_ids, d_scores, d_cnt, d_cnt + 1, g.xsplit.as<uint32_t>(), g.xscale.as<float>(),
+                          w.mant, w.exps, vocab, hidden, kk, g.stream)))
+        return rc;
+    HIP_OK(hipMemcpyAsync(g.h_out.p, g.tk_out.p, (size_t)(2 * kk + 2) * 4, hipMemcpyDeviceToHost, g.stream));
+    HIP_OK(hipStreamSynchronize(g.stream));
+    const int* hi = static_cast<const int*>(g.h_out.p);
+    const int cnt = hi[2 * kk];
+    if (out_ids) memcpy(out_ids, hi, (size_t)cnt * 4);
+    if (out_scores) memcpy(out_scores, hi + kk, (size_t)cnt * 4);
+    if (out_argmax) *out_argmax = hi[2 * kk + 1];
+    return cnt;
+}
+
+// ---- synthetic inputs ----------------------------------------------------------------------
+double unit53(uint64_t h) { return (double)(h >> 11) * (1.0 / 9007199254740992.0); }
+
+double normal_at(uint64_t seed, uint64_t i) {
+    const double u1 = unit53(bfp8_hash64(seed, 2 * i)) + (1.0 / 9007199254740992.0);  // (0, 1]
+    const double u2 = unit53(bfp8_hash64(seed, 2 * i + 1));
+    return std::sqrt(-2.0 * std::log(u1)) * std::cos(6.283185307179586 * u2);
+}
+
+}  // namespace
+
+// =========================== C ABI ================================================
+extern "C" {
+
+void init_kernels(void) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (ensure_init_locked() != BFP8_OK) fatal("init_kernels");
+}
+
+void bfp8_gemv(float* y, const float* x, const int8_t* mantissas, const uint8_t* exps, int M, int K) {
+    ProfScope ps(QP_GEMV);
+    if (M <= 0) return;
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (ensure_init_locked() != BFP8_OK || host_gemv(y, x, mantissas, exps, M, K) != BFP8_OK)
+        fatal("bfp8_gemv");
+}
+
+void bfp8_gemv_batch(float* Y, const float* X, const int8_t* mantissas, const uint8_t* exps, int M, int K,
+                     int B) {
+    ProfScope ps(QP_GEMV);
+    if (M <= 0 || B <= 0) return;
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (ensure_init_locked() != BFP8_OK) fatal("bfp8_gemv_batch");
+    const int nb = bfp8_nblocks(K);
+    if (nb == 0 || K > 4096) {  // no batched kernel for these: per-vector calls
+        for (int b = 0; b < B; ++b)
+            if (host_gemv(Y + (size_t)b * M, X + (size_t)b * K, mantissas, exps, M, K) != BFP8_OK)
+                fatal("bfp8_gemv_batch");
+        return;
+    }
+    DevWeights w;
+    int rc = weights_for(mantissas, exps, M, K, &w);
+    // X rows have stride K; the quantizer reads the first nb*64 of each.
+    if (!rc) rc = g.h_in.reserve((size_t)B * nb * 64 * 4);
+    if (!rc) rc = g.x.reserve((size_t)B * nb * 64 * 4);
+    if (!rc) {
+        for (int b = 0; b < B; ++b)
+            memcpy(static_cast<float*>(g.h_in.p) + (size_t)b * nb * 64, X + (size_t)b * K, (size_t)nb * 64 * 4);
+        if (hipMemcpyAsync(g.x.p, g.h_in.p, (size_t)B * nb * 64 * 4, hipMemcpyHostToDevice, g.stream) !=
+            hipSuccess) {
+            set_error("hipMemcpyAsync of X failed");
+            rc = BFP8_EHIP;
+        }
+    }
+    if (!rc) rc = quantize_ws(K, B);
+    if (!rc) rc = g.y.reserve((size_t)B * M * 4);
+    if (!rc) rc = g.h_out.reserve((size_t)B * M * 4);
+    for (int b0 = 0; !rc && b0 < B; b0 += 16) {
+        const int bc = std::min(16, B - b0);
+        int done = 0;
+        while (!rc && done < bc) {
+            int step = 16;
+            while (step > bc - done) step >>= 1;
+            const int v0 = b0 + done;
+            hipError_t e = bfp8_launch_gemv_batch(g.y.as<float>() + (size_t)v0 * M,
+                                                  g.xsplit.as<uint32_t>() + (size_t)v0 * nb * 32,
+                                                  g.xscale.as<float>() + (size_t)v0 * nb, w.mant, w.exps, M, K,
+                                                  step, g.stream);
+            if (e != hipSuccess) {
+                set_error("batched GEMV launch: %s", hipGetErrorString(e));
+                rc = BFP8_EHIP;
+            }
+            done += step;
+        }
+    }
+    for (int b = 0; !rc && b < B && (M & 1); ++b) {
+        hipError_t e = bfp8_launch_tail_row(g.y.as<float>() + (size_t)b * M, g.xsplit.as<uint32_t>() + (size_t)b * nb * 32,
+                                            g.xscale.as<float>() + (size_t)b * nb, w.mant, w.exps, M, K, g.stream);
+        if (e != hipSuccess) {
+            set_error("tail row launch: %s", hipGetErrorString(e));
+            rc = BFP8_EHIP;
+        }
+    }
+    if (!rc) {
+        if (hipMemcpyAsync(g.h_out.p, g.y.p, (size_t)B * M * 4, hipMemcpyDeviceToHost, g.stream) != hipSuccess ||
+            hipStreamSynchronize(g.stream) != hipSuccess) {
+            set_error("batched GEMV readback failed");
+            rc = BFP8_EHIP;
+        }
+    }
+    if (rc) fatal("bfp8_gemv_batch");
+    memcpy(Y, g.h_out.p, (size_t)B * M * 4);
+}
+
+int bfp8_lm_head_topk(const float* h, const int8_t* mantissas, const uint8_t* exps, int vocab, int hidden,
+                      int k, int* out_ids, float* out_scores) {
+    ProfScope ps(QP_LMHEAD);
+    if (!h || !mantissas || !exps || !out_ids || !out_scores || !lm_head_args_ok(vocab, hidden, k)) return 0;
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (ensure_init_locked() != BFP8_OK) return 0;
+    const int n = host_lm_head(h, mantissas, exps, vocab, hidden, k, out_ids, out_scores, nullptr);
+    return n < 0 ? 0 : n;
+}
+
+int bfp8_lm_head_argmax(const float* h, const int8_t* mantissas, const uint8_t* exps, int vocab, int hidden) {
+    ProfScope ps(QP_LMHEAD);
+    if (!h || !mantissas || !exps || !lm_head_args_ok(vocab, hidden, 1)) return -1;
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (ensure_init_locked() != BFP8_OK) return -1;
+    int am = -1;
+    const int n = host_lm_head(h, mantissas, exps, vocab, hidden, 1, nullptr, nullptr, &am);
+    return n < 0 ? -1 : am;
+}
+
+const char* bfp8_last_error(void) {
+    static thread_local std::string copy;
+    std::lock_guard<std::mutex> lk(g_err_mu);
+    copy = g_err;
+    return copy.c_str();
+}
+
+void bfp8_cache_clear(void) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (g.ready) (void)hipStreamSynchronize(g.stream);
+    for (auto& kv : g.cache) {
+        kv.second.mant.release();
+        kv.second.exps.release();
+    }
+    g.cache.clear();
+    g.cache_bytes = 0;
+}
+
+void qwen_prof_enable(int on) { g_prof_on = on; }
+void qwen_prof_reset(void) {
+    for (int i = 0; i < QP_N; i++) g_prof_ms[i] = 0.0;
+}
+int qwen_prof_count(void) { return QP_N; }
+double qwen_prof_get(int i) { return (i >= 0 && i < QP_N) ? g_prof_ms[i] : 0.0; }
+const char* qwen_prof_name(int i) { return (i >= 0 && i < QP_N) ? kProfNames[i] : "?"; }
+
+// ---- device level ------------------------------------------------------------------------
+size_t bfp8_dev_mant_bytes(int M, int K) { return bfp8_gpu_mant_bytes(M, K); }
+size_t bfp8_dev_exps_bytes(int M, int K) { return bfp8_gpu_exps_bytes(M, K); }
+size_t bfp8_dev_xsplit_bytes(int K) { return bfp8_xsplit_bytes(K); }
+
+void* bfp8_stream(void) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (ensure_init_locked() != BFP8_OK) return nullptr;
+    return g.stream;
+}
+
+#define DEV_PROLOGUE()                                                 \
+    do {                                                               \
+        std::lock_guard<std::mutex> lk_(g.mu);                         \
+        if (ensure_init_locked() != BFP8_OK) return BFP8_EHIP;         \
+    } while (0)
+
+int bfp8_dev_pack(int8_t* mant_gpu, uint8_t* exps_gpu, const int8_t* mant_soa, const uint8_t* exps_soa, int M,
+                  int K, void* stream) {
+    if (M < 0 || K < 0 || (M > 0 && bfp8_nblocks(K) > 0 && (!mant_gpu || !exps_gpu || !mant_soa || !exps_soa)))
+        return BFP8_EINVAL;
+    DEV_PROLOGUE();
+    HIP_OK(bfp8_launch_pack((uint8_t*)mant_gpu, exps_gpu, mant_soa, exps_soa, M, K, pick_stream(stream)));
+    return BFP8_OK;
+}
+
+int bfp8_dev_unpack(int8_t* mant_soa, uint8_t* exps_soa, const int8_t* mant_gpu, const uint8_t* exps_gpu, int M,
+                    int K, void* stream) {
+    if (M < 0 || K < 0) return BFP8_EINVAL;
+    DEV_PROLOGUE();
+    HIP_OK(bfp8_launch_unpack(mant_soa, exps_soa, (const uint8_t*)mant_gpu, exps_gpu, M, K, pick_stream(stream)));
+    return BFP8_OK;
+}
+
+int bfp8_dev_quantize(int16_t* xq, float* xscale, uint32_t* xsplit, const float* x, int K, void* stream) {
+    if (K < 0 || K > 4096 || (bfp8_nblocks(K) > 0 && (!xscale || !xsplit || !x))) return BFP8_EINVAL;
+    DEV_PROLOGUE();
+    Bfp8QuantDesc q{};
+    q.x = x;
+    q.xq = xq;
+    q.xscale = xscale;
+    q.xsplit = xsplit;
+    q.K = K;
+    HIP_OK(bfp8_launch_quantize1(q, pick_stream(stream)));
+    return BFP8_OK;
+}
+
+int bfp8_dev_gemv(float* y, const uint32_t* xsplit, const float* xscale, const int8_t* mant_gpu,
+                  const uint8_t* exps_gpu, int M, int K, int32_t* lane_sums, void* stream) {
+    if (M < 0 || K < 0 || K > 4096) return BFP8_EINVAL;
+    if (M == 0) return BFP8_OK;
+    if (!y || (bfp8_nblocks(K) > 0 && (!xsplit || !xscale || !mant_gpu || !exps_gpu))) return BFP8_EINVAL;
+    DEV_PROLOGUE();
+    hipStream_t s = pick_stream(stream);
+    if (bfp8_nblocks(K) == 0) {
+        HIP_OK(hipMemsetAsync(y, 0, (size_t)M * 4, s));
+        return BFP8_OK;
+    }
+    return gemv_q(y, xsplit, xscale, (const uint8_t*)mant_gpu, exps_gpu, M, K, lane_sums, s);
+}
+
+int bfp8_dev_gemv_float(float* y, const float* x, const int8_t* mant_gpu, const uint8_t* exps_gpu, int M, int K,
+                        void* stream) {
+    if (M < 0 || K < 0 || bfp8_nblocks(K) > 16384) return BFP8_EINVAL;
+    if (M == 0) return BFP8_OK;
+    DEV_PROLOGUE();
+    HIP_OK(bfp8_launch_gemv_float(y, x, (const uint8_t*)mant_gpu, exps_gpu, M, K, pick_stream(stream)));
+    return BFP8_OK;
+}
+
+int bfp8_dev_gemv_batch(float* Y, const uint32_t* xsplit, const float* xscale, const int8_t* mant_gpu,
+                        const uint8_t* exps_gpu, int M, int K, int B, void* stream) {
+    if (M < 0 || K < 64 || K > 4096 || B < 1 || B > 16) return BFP8_EINVAL;
+    if (M == 0) return BFP8_OK;
+    DEV_PROLOGUE();
+    hipStream_t s = pick_stream(stream);
+    const int nb = bfp8_nblocks(K);
+    int done = 0;
+    while (done < B) {
+        int step = 16;
+        while (step > B - done) step >>= 1;
+        HIP_OK(bfp8_launch_gemv_batch(Y + (size_t)done * M, xsplit + (size_t)done * nb * 32,
+                                      xscale + (size_t)done * nb, (const uint8_t*)mant_gpu, exps_gpu, M, K, step, s));
+        done += step;
+    }
+    if (M & 1)
+        for (int b = 0; b < B; ++b)
+            HIP_OK(bfp8_launch_tail_row(Y + (size_t)b * M, xsplit + (size_t)b * nb * 32, xscale + (size_t)b * nb,
+                                        (const uint8_t*)mant_gpu, exps_gpu, M, K, s));
+    return BFP8_OK;
+}
+
+int bfp8_dev_lm_head_topk(int* out_ids, float* out_scores, int* out_count, int* out_argmax,
+                          const uint32_t* xsplit, const float* xscale, const int8_t* mant_gpu,
+                          const uint8_t* exps_gpu, int vocab, int hidden, int k, void* stream) {
+    if (!lm_head_args_ok(vocab, hidden, k) || !out_ids || !out_scores || !out_count || !out_argmax)
+        return BFP8_EINVAL;
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (ensure_init_locked() != BFP8_OK) return BFP8_EHIP;
+    return lm_head_dev(out_ids, out_scores, out_count, out_argmax, xsplit, xscale, (const uint8_t*)mant_gpu,
+                       exps_gpu, vocab, hidden, k, pick_stream(stream));
+}
+
+int bfp8_dev_synth_planes(int8_t* mant_soa, uint8_t* exps_soa, int M, int K, uint64_t seed, int e_lo, int e_hi,
+                          void* stream) {
+    if (M < 0 || K < 0 || e_lo < 0 || e_hi > 255 || e_lo > e_hi) return BFP8_EINVAL;
+    DEV_PROLOGUE();
+    HIP_OK(bfp8_launch_synth_planes(mant_soa, exps_soa, M, K, seed, e_lo, e_hi, pick_stream(stream)));
+    return BFP8_OK;
+}
+
+void bfp8_synth_planes_host(int8_t* mant_soa, uint8_t* exps_soa, int M, int K, uint64_t seed, int e_lo, int e_hi) {
+    const size_t nm = (size_t)M * K, ne = (size_t)M * bfp8_nblocks(K);
+    for (size_t i = 0; i < nm; ++i) mant_soa[i] = bfp8_synth_mant(seed, i);
+    for (size_t i = 0; i < ne; ++i) exps_soa[i] = bfp8_synth_exp(seed, i, e_lo, e_hi);
+}
+
+void bfp8_synth_normal(float* out, int n, uint64_t seed) {
+    for (int i = 0; i < n; ++i) out[i] = (float)normal_at(seed, (uint64_t)i);
+}
+
+void bfp8_synth_swiglu(float* out, int n, uint64_t seed, double outlier_frac, float mag) {
+    for (int i = 0; i < n; ++i) {
+        const double a = normal_at(seed, (uint64_t)i);
+        const double b = normal_at(seed ^ 0x5DEECE66Dull, (uint64_t)i);
+        double v = a / (1.0 + std::exp(-a)) * b;
+        const uint64_t h = bfp8_hash64(seed ^ 0xA5A5A5A5A5A5A5A5ull, (uint64_t)i);
+        if (unit53(h) < outlier_frac) v = (h & 1) ? (double)mag : -(double)mag;
+        out[i] = (float)v;
+    }
+}
+
+int bfp8_dev_read_probe(const void* buf, size_t bytes, uint32_t* out, void* stream) {
+    DEV_PROLOGUE();
+    HIP_OK(bfp8_launch_read_probe(buf, bytes, out, pick_stream(stream)));
+    return BFP8_OK;
+}
+
+int bfp8_dev_copy_probe(void* dst, const void* src, size_t bytes, void* stream) {
+    DEV_PROLOGUE();
+    HIP_OK(bfp8_launch_copy_probe(dst, src, bytes, pick_stream(stream)));
+    return BFP8_OK;
+}
+
+}  // extern "C"
+
+// =========================== plans ================================================
+namespace {
+
+struct Plan {
+    std::vector<bfp8_plan_item> items;
+    std::vector<int> odd_items;    // items needing the odd-row kernel
+    std::vector<int> float_items;  // K > 4096 items (float path, own launches)
+    DevBuf descs, tiles, qdescs, xq, xscale, xsplit, partials, counter;
+    int ntiles = 0, nq = 0, max_nb = 0;
+    bool any_topk = false;
+    std::vector<Bfp8GemvDesc> hdesc;
+};
+
+}  // namespace
+
+extern "C" {
+
+void* bfp8_plan_create(const bfp8_plan_item* items, int n) {
+    if (!items || n <= 0) {
+        set_error("bfp8_plan_create: no items");
+        return nullptr;
+    }
+    {
+        std::lock_guard<std::mutex> lk(g.mu);
+        if (ensure_init_locked() != BFP8_OK) return nullptr;
+    }
+    Plan* p = new Plan();
+    p->items.assign(items, items + n);
+    int ntopk = 0;
+    size_t xs_words = 0, xsc_floats = 0, xq_elems = 0;
+    for (int i = 0; i < n; ++i) {
+        const bfp8_plan_item& it = items[i];
+        if (it.M <= 0 || it.K < 64 || !it.x || !it.mant_gpu || !it.exps_gpu ||
+            (it.topk > 0 && (!lm_head_args_ok(it.M, it.K, it.topk) || !it.out_ids || !it.out_scores ||
+                             !it.out_count || !it.out_argmax)) ||
+            (it.topk <= 0 && !it.y) || (it.topk > 0 && it.K > 4096)) {
+            set_error("bfp8_plan_create: invalid item %d", i);
+            delete p;
+            return nullptr;
+        }
+        ntopk += it.topk > 0;
+        const int nb = bfp8_nblocks(it.K);
+        if (it.K <= 4096) {
+            xs_words += (size_t)nb * 32;
+            xsc_floats += nb;
+            xq_elems += (size_t)nb * 64;
+            p->max_nb = std::max(p->max_nb, nb);
+        }
+    }
+    if (ntopk > 1) {
+        set_error("bfp8_plan_create: at most one lm_head item");
+        delete p;
+        return nullptr;
+    }
+    int rc = 0;
+    rc = rc ? rc : p->xsplit.reserve(xs_words * 4);
+    rc = rc ? rc : p->xscale.reserve(xsc_floats * 4);
+    rc = rc ? rc : p->xq.reserve(xq_elems * 2);
+    std::vector<Bfp8QuantDesc> hq;
+    std::vector<std::pair<int, int>> order;  // (item, first tile)
+    size_t ow = 0, of = 0, oq = 0;
+    for (int i = 0; i < n && !rc; ++i) {
+        const bfp8_plan_item& it = items[i];
+        Bfp8GemvDesc d{};
+        if (it.K > 4096) {
+            p->float_items.push_back(i);
+            p->hdesc.push_back(d);
+            continue;
+        }
+        const int nb = bfp8_nblocks(it.K);
+        Bfp8QuantDesc q{};
+        q.x = it.x;
+        q.xq = p->xq.as<int16_t>() + oq;
+        q.xscale = p->xscale.as<float>() + of;
+        q.xsplit = p->xsplit.as<uint32_t>() + ow;
+        q.K = it.K;
+        hq.push_back(q);
+        d = plain_desc(it.y, q.xsplit, q.xscale, (const uint8_t*)it.mant_gpu, it.exps_gpu, it.M, it.K, nullptr);
+        if (it.topk > 0) {
+            if (it.M & 1) rc = BFP8_EINVAL;
+            d.topk = std::min(it.topk, it.M);
+            rc = rc ? rc : p->partials.reserve((size_t)bfp8_ntiles(it.M) * d.topk * 8);
+            rc = rc ? rc : p->counter.reserve(256);
+            if (!rc && hipMemset(p->counter.p, 0, 256) != hipSuccess) rc = BFP8_EHIP;
+            d.partials = p->partials.as<uint64_t>();
+            d.counter = p->counter.as<uint32_t>();
+            d.out_ids = it.out_ids;
+            d.out_scores = it.out_scores;
+            d.out_count = it.out_count;
+            d.out_argmax = it.out_argmax;
+            p->any_topk = true;
+        }
+        if ((it.M & 1) && it.topk <= 0) p->odd_items.push_back(i);
+        p->hdesc.push_back(d);
+        ow += (size_t)nb * 32;
+        of += nb;
+        oq += (size_t)nb * 64;
+    }
+    // Tile order: the lm_head first (its final merge then overlaps the
+    // rest), then larger K before smaller K (longer workgroups start first).
+    std::vector<int> idx;
+    for (int i = 0; i < n; ++i)
+        if (items[i].K <= 4096) idx.push_back(i);
+    std::stable_sort(idx.begin(), idx.end(), [&](int a, int b) {
+        const bool ta = items[a].topk > 0, tb = items[b].topk > 0;
+        if (ta != tb) return ta;
+        return items[a].K > items[b].K;
+    });
+    std::vector<Bfp8TileRef> tiles;
+    for (int i : idx)
+        for (int t = 0; t < bfp8_ntiles(items[i].M); ++t) tiles.push_back(Bfp8TileRef{i, t});
+    p->ntiles = (int)tiles.size();
+    p->nq = (int)hq.size();
+    rc = rc ? rc : p->descs.reserve(p->hdesc.size() * sizeof(Bfp8GemvDesc));
+    rc = rc ? rc : p->tiles.reserve(tiles.size() * sizeof(Bfp8TileRef));
+    rc = rc ? rc : p->qdescs.reserve(hq.size() * sizeof(Bfp8QuantDesc));
+    if (!rc && (hipMemcpy(p->descs.p, p->hdesc.data(), p->hdesc.size() * sizeof(Bfp8GemvDesc), hipMemcpyHostToDevice) != hipSuccess ||
+                (!tiles.empty() && hipMemcpy(p->tiles.p, tiles.data(), tiles.size() * sizeof(Bfp8TileRef), hipMemcpyHostToDevice) != hipSuccess) ||
+                (!hq.empty() && hipMemcpy(p->qdescs.p, hq.data(), hq.size() * sizeof(Bfp8QuantDesc), hipMemcpyHostToDevice) != hipSuccess)))
+        rc = BFP8_EHIP;
+    if (rc) {
+        set_error("bfp8_plan_create: allocation or upload failed (%d)", rc);
+        p->descs.release(); p->tiles.release(); p->qdescs.release(); p->xq.release();
+        p->xscale.release(); p->xsplit.release(); p->partials.release(); p->counter.release();
+        delete p;
+        return nullptr;
+    }
+    return p;
+}
+
+int bfp8_plan_quantize(void* plan, void* stream) {
+    Plan* p = static_cast<Plan*>(plan);
+    if (!p) return BFP8_EINVAL;
+    HIP_OK(bfp8_launch_quantize(p->qdescs.as<Bfp8QuantDesc>(), p->nq, p->max_nb, pick_stream(stream)));
+    return BFP8_OK;
+}
+
+int bfp8_plan_run_gemv(void* plan, void* stream) {
+    Plan* p = static_cast<Plan*>(plan);
+    if (!p) return BFP8_EINVAL;
+    hipStream_t s = pick_stream(stream);
+    HIP_OK(bfp8_launch_gemv_grouped(p->descs.as<Bfp8GemvDesc>(), p->tiles.as<Bfp8TileRef>(), p->ntiles,
+                                    p->any_topk, s));
+    for (int i : p->odd_items) {
+        const Bfp8GemvDesc& d = p->hdesc[i];
+        HIP_OK(bfp8_launch_tail_row(d.y, d.xsplit, d.xscale, d.mant, d.exps, d.M, d.K, s));
+    }
+    for (int i : p->float_items) {
+        const bfp8_plan_item& it = p->items[i];
+        HIP_OK(bfp8_launch_gemv_float(it.y, it.x, (const uint8_t*)it.mant_gpu, it.exps_gpu, it.M, it.K, s));
+    }
+    return BFP8_OK;
+}
+
+int bfp8_plan_run(void* plan, void* stream) {
+    int rc = bfp8_plan_quantize(plan, stream);
+    return rc ? rc : bfp8_plan_run_gemv(plan, stream);
+}
+
+void bfp8_plan_destroy(void* plan) {
+    Plan* p = static_cast<Plan*>(plan);
+    if (!p) return;
+    {
+        std::lock_guard<std::mutex> lk(g.mu);
+        if (g.ready) (void)hipDeviceSynchronize();
+    }
+    p->descs.release(); p->tiles.release(); p->qdescs.release(); p->xq.release();
+    p->xscale.release(); p->xsplit.release(); p->partials.release(); p->counter.release();
+    delete p;
+}
+
+}  // extern "C"

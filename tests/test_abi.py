@@ -1,0 +1,141 @@
+"""CPU checks of the C-ABI library: it loads, exports every symbol that
+include/qwen_kernels.h declares, binds like the reference engine, and its
+host-side logic (sizes, synthetic generators, failure reporting) behaves.
+No GPU compute is called here."""
+import ctypes
+import re
+import subprocess
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "qwen_kernels.h"
+LIB = ROOT / "qwen35-ax7020-edge-llm_amd" / "libqwen_kernels.so"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    text = "\n".join(l for l in text.splitlines() if not l.lstrip().startswith("#"))
+    names = re.findall(r"(?:^|;|\})\s*(?:const\s+)?[A-Za-z_][\w]*\s*\**\s*\b([a-z_][a-z0-9_]*)\s*\(", text, re.M)
+    return sorted(set(names) - {"struct", "typedef"})
+
+
+def exported_symbols():
+    out = subprocess.run(["nm", "-D", "--defined-only", str(LIB)], capture_output=True, text=True, check=True)
+    return {l.split()[-1] for l in out.stdout.splitlines() if " T " in l}
+
+
+def test_library_built_and_loads():
+    assert LIB.exists(), "run qwen35-ax7020-edge-llm_amd/build_lib.py"
+    ctypes.CDLL(str(LIB))
+
+
+def test_exports_every_declared_symbol():
+    decl = declared_functions()
+    assert len(decl) >= 34 and "bfp8_gemv" in decl and "bfp8_plan_create" in decl
+    missing = set(decl) - exported_symbols()
+    assert not missing, missing
+
+
+def test_exports_nothing_undeclared():
+    extra = exported_symbols() - set(declared_functions())
+    assert not extra, extra
+
+
+def test_reference_symbol_signatures_bind_like_the_engine():
+    import qwen_kernels_gpu as qk
+
+    lib = qk.load()
+    # 04/qwen_real_engine.py:680-685 / :864-866
+    assert lib.bfp8_gemv.argtypes == [ctypes.c_void_p] * 4 + [ctypes.c_int] * 2
+    assert lib.qwen_prof_count() == 15
+    names = [lib.qwen_prof_name(i).decode() for i in range(15)]
+    assert names[0] == "bfp8_gemv" and names[1] == "lm_head_argmax" and names[-1] == "forward_token_c"
+    assert lib.qwen_prof_name(99) == b"?" and lib.qwen_prof_get(-1) == 0.0
+
+
+def test_layout_sizes():
+    import qwen_kernels_gpu as qk
+
+    lib = qk.load()
+    # 3584 rows -> 56 tiles of 64; 16 blocks -> 4 exponent groups
+    assert lib.bfp8_dev_mant_bytes(3584, 1024) == 3584 * 1024
+    assert lib.bfp8_dev_exps_bytes(3584, 1024) == 56 * 4 * 256
+    assert lib.bfp8_dev_mant_bytes(65, 128) == 2 * 64 * 128  # padded to whole tiles
+    assert lib.bfp8_dev_exps_bytes(1024, 3584) == 16 * 14 * 256
+    assert lib.bfp8_dev_xsplit_bytes(3584) == 56 * 128
+    assert lib.bfp8_dev_mant_bytes(0, 1024) == 0 and lib.bfp8_dev_xsplit_bytes(63) == 0
+
+
+def _splitmix(seed, idx):
+    m = (1 << 64) - 1
+    z = (seed + (idx + 1) * 0x9E3779B97F4A7C15) & m
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & m
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & m
+    return z ^ (z >> 31)
+
+
+def test_synthetic_planes_follow_the_documented_hash():
+    import qwen_kernels_gpu as qk
+
+    mant, exps = qk.synth_planes(3, 128, 12345, 124, 130)
+    flat = mant.reshape(-1)
+    for i in (0, 1, 77, 383):
+        assert flat[i] == (_splitmix(12345, i) >> 32) % 255 - 127
+    ef = exps.reshape(-1)
+    for i in range(ef.size):
+        assert ef[i] == 124 + (_splitmix(12345 ^ 0xE7E7E7E7E7E7E7E7, i) >> 32) % 7
+    assert mant.min() >= -127 and mant.max() <= 127
+
+
+def test_synthetic_activation_statistics():
+    import qwen_kernels_gpu as qk
+
+    x = qk.synth_normal(200000, 9)
+    assert abs(float(x.mean())) < 0.01 and abs(float(x.std()) - 1) < 0.01
+    s = qk.synth_swiglu(100000, 9, 0.01, 20.0)
+    frac = float(np.mean(np.abs(s) == 20.0))
+    assert 0.008 < frac < 0.012
+    assert np.array_equal(qk.synth_normal(64, 5), qk.synth_normal(64, 5))
+
+
+def test_device_call_without_gpu_reports_error():
+    """On a host without a GPU the int entry points return an error code with
+    a message; nothing falls back to the CPU."""
+    import torch
+
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    import qwen_kernels_gpu as qk
+
+    lib = qk.load()
+    x = np.zeros(64, np.float32)
+    out = np.zeros(64, np.float32)
+    rc = lib.bfp8_dev_quantize(None, out.ctypes.data, out.ctypes.data, x.ctypes.data, 64, None)
+    assert rc == qk.BFP8_EHIP
+    assert b"no HIP device" in lib.bfp8_last_error()
+    assert lib.bfp8_lm_head_topk(x.ctypes.data, x.ctypes.data, x.ctypes.data, 64, 64, 0, x.ctypes.data,
+                                 x.ctypes.data) == 0  # invalid k: rejected before any GPU work
+
+
+def test_void_entry_point_fails_loudly_without_gpu():
+    """bfp8_gemv has no error channel (04/qwen_kernels_opt.c:207): without a GPU
+    the library aborts with a message instead of computing on the CPU."""
+    import torch
+
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    code = (
+        "import sys, numpy as np; sys.path.insert(0, %r)\n"
+        "import qwen_kernels_gpu as qk\n"
+        "k = qk.load(); y = np.zeros(2, np.float32); x = np.ones(64, np.float32)\n"
+        "m = np.ones((2, 64), np.int8); e = np.full((2, 1), 134, np.uint8)\n"
+        "k.bfp8_gemv(y.ctypes.data, x.ctypes.data, m.ctypes.data, e.ctypes.data, 2, 64)\n"
+        "print('RETURNED', y)\n" % str(ROOT / "qwen35-ax7020-edge-llm_amd"))
+    res = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120,
+                         env={"HIP_VISIBLE_DEVICES": "", "PATH": "/usr/bin:/bin"})
+    assert res.returncode != 0 and "RETURNED" not in res.stdout
+    assert "no CPU fallback" in res.stderr

@@ -1,0 +1,427 @@
+"""GPU parity: the HIP kernels against the CPU oracle, bit for bit.
+
+Shapes are the real ones (3584x1024, 1024x3584, 65536x1024, the 24-layer
+sweep, B=16); inputs come from the library's seeded generators and are fed
+identically to the GPU and to the oracle.  Floats are compared as bit
+patterns (NaN compared as NaN: the reference's NEON default-NaN payload is
+not reproduced)."""
+import os
+import sys
+import tempfile
+
+import numpy as np
+import pytest
+
+import oracle_lib as ol
+
+pytestmark = pytest.mark.gpu
+F32 = np.float32
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+def same_f32(a, b):
+    a = np.asarray(a, dtype=F32).reshape(-1)
+    b = np.asarray(b, dtype=F32).reshape(-1)
+    nan = np.isnan(a) & np.isnan(b)
+    return bool(np.all(nan | (a.view(np.uint32) == b.view(np.uint32))))
+
+
+def mismatch(a, b):
+    a = np.asarray(a, dtype=F32).reshape(-1)
+    b = np.asarray(b, dtype=F32).reshape(-1)
+    bad = np.nonzero(~((np.isnan(a) & np.isnan(b)) | (a.view(np.uint32) == b.view(np.uint32))))[0]
+    return f"{bad.size} mismatches, first {bad[:5]}: {a[bad[:5]]} vs {b[bad[:5]]}"
+
+
+def encode_xsplit(xq):
+    """The split-activation layout (bfp8_layout.h) built from int16 xq."""
+    xq = np.asarray(xq, dtype=np.int32)
+    nb = xq.size // 64
+    xl = ((xq & 0xFF) ^ 0x80) - 0x80
+    xh = (xq - xl) >> 8
+    out = np.zeros((nb, 4, 8), dtype=np.uint32)
+    for k in range(64):
+        q, i = k & 3, k >> 2
+        d, p = i >> 2, i & 3
+        out[:, q, d] |= (xh[k::64].astype(np.uint32) & 0xFF) << (8 * p)
+        out[:, q, 4 + d] |= (xl[k::64].astype(np.uint32) & 0xFF) << (8 * p)
+    return out.reshape(-1).view(np.int32)
+
+
+def decode_xsplit(words, nb):
+    w = np.asarray(words, dtype=np.int32).view(np.uint32)[: nb * 32].reshape(nb, 4, 8)
+    xq = np.zeros(nb * 64, dtype=np.int32)
+    for k in range(64):
+        q, i = k & 3, k >> 2
+        d, p = i >> 2, i & 3
+        h = ((w[:, q, d] >> (8 * p)) & 0xFF).astype(np.int32)
+        l = ((w[:, q, 4 + d] >> (8 * p)) & 0xFF).astype(np.int32)
+        h = (h ^ 0x80) - 0x80
+        l = (l ^ 0x80) - 0x80
+        xq[k::64] = 256 * h + l
+    return xq
+
+
+@pytest.fixture(scope="module")
+def torch_mod():
+    import torch
+
+    return torch
+
+
+def run_gemv_dev(qk, torch, mant, exps, x, lanes=True):
+    dm = qk.DeviceMatrix.from_soa(mant, exps)
+    xt = torch.from_numpy(np.ascontiguousarray(x, dtype=F32)).cuda()
+    xq, xs, xsp = qk.quantize(xt)
+    if lanes:
+        y, ln = qk.gemv(dm, xsp, xs, lane_sums=True)
+    else:
+        y, ln = qk.gemv(dm, xsp, xs), None
+    torch.cuda.synchronize()
+    return (y.cpu().numpy(), xq.cpu().numpy(), xs.cpu().numpy(), xsp.cpu().numpy(),
+            None if ln is None else ln.cpu().numpy())
+
+
+# ---- quantizer -------------------------------------------------------------------------------
+def test_quantize_bit_exact_with_special_values(gpu, torch_mod):
+    qk, torch = gpu, torch_mod
+    rng = np.random.default_rng(11)
+    K = 4096
+    x = (rng.standard_normal(K) * np.repeat(10.0 ** rng.uniform(-12, 12, K // 64), 64)).astype(F32)
+    x[0:64] = 0.0
+    x[64:128] = F32(1e-20)
+    x[128:192] = np.nextafter(F32(0), F32(1)) * np.arange(64, dtype=F32)  # subnormals only
+    x[192] = 16384.0
+    x[193:200] = [2.5, 3.5, -2.5, -3.5, 0.5, 1.5, 16383.5]
+    x[260] = np.nan
+    x[330] = np.inf
+    x[400] = -np.inf
+    x[470:480] = -F32(0.0)
+    x[600] = F32(1.5e-38)  # subnormal next to normals
+    say("quantize K=4096 specials")
+    xt = torch.from_numpy(x).cuda()
+    xq, xs, xsp = qk.quantize(xt)
+    torch.cuda.synchronize()
+    xq_ref, xs_ref = ol.quant_x(x)
+    assert np.array_equal(xq.cpu().numpy(), xq_ref)
+    assert same_f32(xs.cpu().numpy(), xs_ref)
+    assert np.array_equal(decode_xsplit(xsp.cpu().numpy(), K // 64), xq_ref.astype(np.int32))
+
+
+@pytest.mark.parametrize("K", [64, 1024, 2048, 3584])
+def test_quantize_random_scales(gpu, torch_mod, K):
+    qk, torch = gpu, torch_mod
+    rng = np.random.default_rng(K)
+    for trial in range(20):
+        x = (rng.standard_normal(K) * 10.0 ** rng.uniform(-30, 30)).astype(F32)
+        xq, xs, _ = qk.quantize(torch.from_numpy(x).cuda())
+        xq_ref, xs_ref = ol.quant_x(x)
+        assert np.array_equal(xq.cpu().numpy(), xq_ref), trial
+        assert same_f32(xs.cpu().numpy(), xs_ref), trial
+
+
+# ---- layout converter -------------------------------------------------------------------------
+@pytest.mark.parametrize("M,K", [(1, 64), (65, 192), (3584, 1024), (1024, 3584), (3, 100)])
+def test_pack_unpack_round_trip(gpu, torch_mod, M, K):
+    qk, torch = gpu, torch_mod
+    mant, exps = qk.synth_planes(M, K, 1000 + M, 0, 255)
+    say("pack/unpack", M, K)
+    dm = qk.DeviceMatrix.from_soa(mant, exps)
+    ms, es = dm.unpack()
+    torch.cuda.synchronize()
+    nb = K // 64
+    assert np.array_equal(es.cpu().numpy(), exps[:, :nb])
+    back = ms.cpu().numpy()
+    assert np.array_equal(back[:, : nb * 64], mant[:, : nb * 64])
+
+
+def test_gpu_synth_matches_host_synth(gpu, torch_mod):
+    qk, torch = gpu, torch_mod
+    M, K = 1000, 1024
+    say("synth planes")
+    dm = qk.DeviceMatrix.synth(M, K, 77, 124, 130)
+    ms, es = dm.unpack()
+    mant, exps = qk.synth_planes(M, K, 77, 124, 130)
+    assert np.array_equal(ms.cpu().numpy(), mant) and np.array_equal(es.cpu().numpy(), exps)
+
+
+# ---- GEMV at the configured shapes -----------------------------------------------------------------
+def test_known_answer_279616_on_gpu(gpu, torch_mod):
+    """All-0x01 weights and xq = 0x1111: every block sums to 279616."""
+    qk, torch = gpu, torch_mod
+    M, K = 3584, 1024
+    mant = np.ones((M, K), dtype=np.int8)
+    exps = np.full((M, K // 64), 134, dtype=np.uint8)
+    say("KAT 279616")
+    dm = qk.DeviceMatrix.from_soa(mant, exps)
+    xsp = torch.from_numpy(encode_xsplit(np.full(K, 0x1111, dtype=np.int16))).cuda()
+    xs = torch.ones(K // 64, dtype=torch.float32, device="cuda")
+    y, lanes = qk.gemv(dm, xsp, xs, lane_sums=True)
+    ln = lanes.cpu().numpy()
+    assert (ln == 16 * 0x1111).all() and (ln.sum(-1) == 279616).all()
+    assert (y.cpu().numpy() == F32(279616 * 16)).all()
+
+
+@pytest.mark.parametrize("M,K,elo,ehi,seed", [
+    (3584, 1024, 124, 130, 1),   # single GEMV, batch 1
+    (1024, 3584, 124, 130, 2),   # down projection
+    (6144, 1024, 124, 130, 3),   # in-projection stand-in
+    (1024, 2048, 124, 130, 4),   # out-projection stand-in
+])
+def test_gemv_configured_shapes(gpu, torch_mod, M, K, elo, ehi, seed):
+    qk, torch = gpu, torch_mod
+    mant, exps = qk.synth_planes(M, K, seed, elo, ehi)
+    x = qk.synth_swiglu(K, seed + 50) if K == 3584 else qk.synth_normal(K, seed + 50)
+    say("gemv", M, K)
+    y, xq, xs, _, lanes = run_gemv_dev(qk, torch, mant, exps, x)
+    y_ref, xq_ref, xs_ref, lanes_ref = ol.gemv_neon(x, mant, exps)
+    assert np.array_equal(xq, xq_ref) and same_f32(xs, xs_ref)
+    assert np.array_equal(lanes, lanes_ref)
+    assert same_f32(y, y_ref), mismatch(y, y_ref)
+
+
+def test_gate_up_down_chain(gpu, torch_mod):
+    """Down projection chained after gate+up: three GEMVs on one stream."""
+    qk, torch = gpu, torch_mod
+    gate = qk.synth_planes(3584, 1024, 21, 124, 130)
+    up = qk.synth_planes(3584, 1024, 22, 124, 130)
+    down = qk.synth_planes(1024, 3584, 23, 124, 130)
+    xh = qk.synth_normal(1024, 24)
+    xd = qk.synth_swiglu(3584, 25, 0.01, 20.0)
+    say("gate/up/down chain")
+    kk = qk.Bfp8Kernels()
+    for (m, e), x in ((gate, xh), (up, xh), (down, xd)):
+        y = kk.gemv_bfp8(x, m, e, m.shape[0], m.shape[1])
+        y_ref, *_ = ol.gemv_neon(x, m, e)
+        assert same_f32(y, y_ref), mismatch(y, y_ref)
+
+
+@pytest.mark.parametrize("M,K", [(1, 64), (7, 64), (65, 1024), (129, 3584), (3, 100), (5, 1000), (2, 63), (9, 4096)])
+def test_odd_rows_ragged_k_and_flushed_exponents(gpu, torch_mod, M, K):
+    qk, torch = gpu, torch_mod
+    rng = np.random.default_rng(M * 7919 + K)
+    mant = rng.integers(-128, 128, size=(M, K), dtype=np.int8)
+    exps = rng.integers(0, 256, size=(M, max(K // 64, 0)), dtype=np.uint8)
+    if exps.size:
+        exps[:, 0] = rng.integers(0, 8, size=M)  # subnormal EXP_SCALE
+    x = (rng.standard_normal(K) * 1e-3).astype(F32)
+    if K >= 128:
+        x[64:128] = 0.0
+    say("odd/ragged", M, K)
+    y = qk.Bfp8Kernels().gemv_bfp8(x, mant, exps, M, K)
+    y_ref, *_ = ol.gemv_neon(x, mant, exps)
+    assert same_f32(y, y_ref), mismatch(y, y_ref)
+
+
+@pytest.mark.parametrize("case", ["m5_k4160"])
+def test_float_path_above_4096_matches_reference_build(gpu, torch_mod, case):
+    """K > 4096 takes the reference's float path; the fixture holds the output
+    of the reference's own host build."""
+    qk = gpu
+    d = np.load(os.path.join(os.path.dirname(__file__), "golden", "ref_float_path.npz"))
+    x, mant, exps, y_fix = (d[f"{case}_{k}"] for k in ("x", "mant", "exps", "y"))
+    say("float path", mant.shape)
+    y = qk.Bfp8Kernels().gemv_bfp8(x, mant, exps, *mant.shape)
+    assert same_f32(y, y_fix), mismatch(y, y_fix)
+    mant2, exps2 = qk.synth_planes(33, 8192, 5, 0, 255)
+    x2 = qk.synth_normal(8192, 6)
+    y2 = qk.Bfp8Kernels().gemv_bfp8(x2, mant2, exps2, 33, 8192)
+    assert same_f32(y2, ol.gemv_float(x2, mant2, exps2))
+
+
+def test_nan_and_inf_activations(gpu, torch_mod):
+    qk, torch = gpu, torch_mod
+    M, K = 64, 256
+    mant, exps = qk.synth_planes(M + 1, K, 31, 124, 130)
+    x = qk.synth_normal(K, 32)
+    x[5] = np.nan
+    x[70] = np.inf
+    say("nan/inf")
+    y = qk.Bfp8Kernels().gemv_bfp8(x, mant, exps, M + 1, K)
+    y_ref, *_ = ol.gemv_neon(x, mant, exps)
+    assert same_f32(y, y_ref), mismatch(y, y_ref)
+
+
+# ---- host-pointer boundary -------------------------------------------------------------------------
+def test_writable_weights_follow_their_contents(gpu, torch_mod):
+    qk = gpu
+    M, K = 256, 1024
+    mant, exps = qk.synth_planes(M, K, 41, 124, 130)
+    x = qk.synth_normal(K, 42)
+    kk = qk.Bfp8Kernels()
+    say("writable weights")
+    y1 = kk.gemv_bfp8(x, mant, exps, M, K)
+    mant[:, :] = np.roll(mant, 1, axis=0)
+    y2 = kk.gemv_bfp8(x, mant, exps, M, K)
+    assert same_f32(y2, ol.gemv_neon(x, mant, exps)[0]) and not same_f32(y1, y2)
+
+
+def test_read_only_mapped_weights_are_cached(gpu, torch_mod):
+    """The engine's weights are a PROT_READ mmap (04/qwen_real_engine.py:745-751)."""
+    qk = gpu
+    M, K = 3584, 1024
+    mant, exps = qk.synth_planes(M, K, 43, 124, 130)
+    with tempfile.TemporaryDirectory() as td:
+        path = os.path.join(td, "w.bin")
+        with open(path, "wb") as f:
+            f.write(mant.tobytes())
+            f.write(exps.tobytes())
+        raw = np.memmap(path, dtype=np.uint8, mode="r")
+        mm = raw[: M * K].view(np.int8)
+        ee = raw[M * K: M * K + M * K // 64]
+        kk = qk.Bfp8Kernels()
+        say("read-only mmap weights")
+        for seed in (44, 45, 46):
+            x = qk.synth_normal(K, seed)
+            y = kk.gemv_bfp8(x, mm, ee, M, K)
+            assert same_f32(y, ol.gemv_neon(x, mant, exps)[0])
+        del raw, mm, ee
+    kk.lib.bfp8_cache_clear()
+
+
+def test_profiler_slot_accumulates(gpu, torch_mod):
+    qk = gpu
+    kk = qk.Bfp8Kernels()
+    lib = kk.lib
+    lib.qwen_prof_reset()
+    lib.qwen_prof_enable(1)
+    mant, exps = qk.synth_planes(128, 1024, 47, 124, 130)
+    kk.gemv_bfp8(qk.synth_normal(1024, 48), mant, exps, 128, 1024)
+    lib.qwen_prof_enable(0)
+    assert lib.qwen_prof_get(0) > 0.0 and lib.qwen_prof_get(2) == 0.0
+
+
+# ---- fused lm_head -------------------------------------------------------------------------------
+@pytest.fixture(scope="module")
+def lm_head_case(gpu):
+    qk = gpu
+    V, H = 65536, 1024
+    mant, exps = qk.synth_planes(V, H, 500, 122, 128)
+    x = qk.synth_normal(H, 501)
+    y_ref, *_ = ol.gemv_neon(x, mant, exps)
+    return mant, exps, x, y_ref
+
+
+@pytest.mark.parametrize("k", [1, 40, 64])
+def test_lm_head_topk_fused(gpu, torch_mod, lm_head_case, k):
+    qk, torch = gpu, torch_mod
+    mant, exps, x, y_ref = lm_head_case
+    say("lm_head fused top-k", k)
+    dm = qk.DeviceMatrix.from_soa(mant, exps)
+    _, xs, xsp = qk.quantize(torch.from_numpy(x).cuda())
+    for rep in range(3):  # the last-workgroup counter must reset between launches
+        ids, sc, cnt, am = qk.lm_head_topk(dm, xsp, xs, k)
+        torch.cuda.synchronize()
+        ids_ref, sc_ref = ol.topk(y_ref, k)
+        n = int(cnt.item())
+        assert n == ids_ref.size
+        assert np.array_equal(ids.cpu().numpy()[:n], ids_ref), rep
+        assert same_f32(sc.cpu().numpy()[:n], sc_ref)
+        assert int(am.item()) == ol.argmax(y_ref)
+
+
+def test_lm_head_host_api_and_ties(gpu, torch_mod, lm_head_case):
+    qk = gpu
+    mant, exps, x, y_ref = lm_head_case
+    mant = mant.copy()
+    exps = exps.copy()
+    top = np.argsort(-y_ref, kind="stable")[:50]
+    # duplicate the best rows elsewhere (both lower and higher ids): equal logits
+    for j, src in enumerate(top[:20]):
+        for dst in (int(src) ^ 0x8000, (int(src) + 12345) % 65536):
+            mant[dst] = mant[src]
+            exps[dst] = exps[src]
+    y2, *_ = ol.gemv_neon(x, mant, exps)
+    assert len(np.unique(y2[np.argsort(-y2, kind="stable")[:40]])) < 40  # ties present
+    kk = qk.Bfp8Kernels()
+    say("lm_head host api with ties")
+    for k in (40, 64):
+        ids, sc = kk.lm_head_topk(x, mant, exps, 65536, 1024, k)
+        ids_ref, sc_ref = ol.topk(y2, k)
+        assert np.array_equal(ids, ids_ref) and same_f32(sc, sc_ref)
+    assert kk.lm_head_argmax(x, mant, exps, 65536, 1024) == ol.argmax(y2)
+
+
+def test_lm_head_small_vocab_and_invalid_arguments(gpu, torch_mod):
+    qk = gpu
+    kk = qk.Bfp8Kernels()
+    mant, exps = qk.synth_planes(100, 128, 60, 124, 130)
+    x = qk.synth_normal(128, 61)
+    y_ref, *_ = ol.gemv_neon(x, mant, exps)
+    say("lm_head small vocab")
+    ids, sc = kk.lm_head_topk(x, mant, exps, 100, 128, 64)
+    ids_ref, sc_ref = ol.topk(y_ref, 64)
+    assert np.array_equal(ids, ids_ref) and same_f32(sc, sc_ref)
+    ids, _ = kk.lm_head_topk(x, mant, exps, 30, 128, 64)  # k > vocab -> min(k, vocab)
+    assert np.array_equal(ids, ol.topk(y_ref[:30], 64)[0])
+    assert kk.lm_head_topk(x, mant, exps, 99, 128, 40)[0].size == 0  # odd vocab rejected
+    assert kk.lm_head_topk(x, mant, exps, 100, 128, 65)[0].size == 0
+    assert kk.lm_head_topk(x, mant, exps, 100, 128, 0)[0].size == 0
+    assert kk.lm_head_argmax(x, mant, exps, 99, 128) == -1
+
+
+# ---- batch and sweep ---------------------------------------------------------------------------------
+@pytest.mark.parametrize("M", [3584, 65536])
+def test_batch16_matches_sixteen_single_calls(gpu, torch_mod, M):
+    qk, torch = gpu, torch_mod
+    K, B = 1024, 16
+    mant, exps = qk.synth_planes(M, K, 70 + M, 124, 130)
+    X = np.stack([qk.synth_normal(K, 700 + b) for b in range(B)])
+    say("batch16", M)
+    Y = qk.Bfp8Kernels().gemv_batch(X, mant, exps, M, K)
+    for b in range(B):
+        y_ref, *_ = ol.gemv_neon(X[b], mant, exps)
+        assert same_f32(Y[b], y_ref), (b, mismatch(Y[b], y_ref))
+
+
+def test_batch_odd_sizes(gpu, torch_mod):
+    qk = gpu
+    M, K, B = 129, 2048, 5
+    mant, exps = qk.synth_planes(M, K, 80, 124, 130)
+    X = np.stack([qk.synth_normal(K, 800 + b) for b in range(B)])
+    say("batch5 odd M")
+    Y = qk.Bfp8Kernels().gemv_batch(X, mant, exps, M, K)
+    for b in range(B):
+        assert same_f32(Y[b], ol.gemv_neon(X[b], mant, exps)[0]), b
+
+
+def test_sweep_plan_24_layers_and_lm_head(gpu, torch_mod):
+    """The full synthetic decode sweep in one plan: 24 x {gate, up, down, in, out}
+    plus the fused lm_head, every output bit-exact, twice in a row."""
+    qk, torch = gpu, torch_mod
+    shapes = [(3584, 1024), (3584, 1024), (1024, 3584), (6144, 1024), (1024, 2048)]
+    items, refs = [], []
+    say("sweep plan build")
+    for layer in range(24):
+        for j, (M, K) in enumerate(shapes):
+            seed = 10_000 + layer * 10 + j
+            dm = qk.DeviceMatrix.synth(M, K, seed, 124, 130)
+            x = qk.synth_swiglu(K, seed + 5) if K == 3584 else qk.synth_normal(K, seed + 5)
+            items.append({"mat": dm, "x": torch.from_numpy(x).cuda(),
+                          "y": torch.empty(M, dtype=torch.float32, device="cuda")})
+            refs.append((M, K, seed, x))
+    lm = qk.DeviceMatrix.synth(65536, 1024, 99_999, 122, 128)
+    xl = qk.synth_normal(1024, 99_998)
+    items.insert(0, {"mat": lm, "x": torch.from_numpy(xl).cuda(), "topk": 40})
+    plan = qk.SweepPlan(items)
+    for rep in range(2):
+        say("sweep plan run", rep)
+        for it in items[1:]:
+            it["y"].fill_(np.nan)
+        plan.run()
+        torch.cuda.synchronize()
+        for it, (M, K, seed, x) in zip(items[1:], refs):
+            mant, exps = qk.synth_planes(M, K, seed, 124, 130)
+            y_ref, *_ = ol.gemv_neon(x, mant, exps)
+            assert same_f32(it["y"].cpu().numpy(), y_ref), (M, K, seed)
+        mant, exps = qk.synth_planes(65536, 1024, 99_999, 122, 128)
+        y_ref, *_ = ol.gemv_neon(xl, mant, exps)
+        ids, sc, cnt = plan.topk_out
+        ids_ref, sc_ref = ol.topk(y_ref, 40)
+        assert int(cnt[0].item()) == 40 and int(cnt[1].item()) == ol.argmax(y_ref)
+        assert np.array_equal(ids.cpu().numpy(), ids_ref) and same_f32(sc.cpu().numpy(), sc_ref)
+    plan.close()

@@ -1,0 +1,270 @@
+"""Pins the CPU oracle (oracle/bfp8_oracle.c) against the reference.
+
+Each check is independent of the oracle's own formulas: the reference's
+host build and its RTL testbench stimulus (tests/golden), closed forms whose
+answer follows from the arithmetic, ARM ARM flush-to-zero rules, and brute
+force on small inputs.
+"""
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle_lib as ol
+
+GOLD = Path(__file__).resolve().parent / "golden"
+F32 = np.float32
+
+
+# ---- EXP_SCALE (04/qwen_kernels_opt.c:126-135) ------------------------------------
+def test_exp_scale_is_power_of_two_for_every_byte():
+    for e in range(256):
+        want = math.ldexp(1.0, e - 134)
+        if want > np.finfo(np.float32).max:
+            want = math.inf
+        assert ol.oracle().orc_exp_scale(e) == F32(want), e
+
+
+# ---- integer block sums ---------------------------------------------------------------
+def test_known_answer_279616():
+    """All-0x01 weights, x all 0x1111: every block sums to 64*4369 = 279616
+    (01/FINAL_REPORT.md:226, 57 344 blocks of a 3584x1024 matrix)."""
+    M, K = 3584, 1024
+    mant = np.ones((M, K), dtype=np.int8)
+    xq = np.full(K, 0x1111, dtype=np.int16)
+    lanes = ol.lane_sums(mant, xq)
+    assert lanes.shape == (M, 16, 4)
+    assert (lanes.sum(-1) == 279616).all()
+    assert (lanes == 16 * 0x1111).all()
+
+
+@pytest.mark.parametrize("case", ["k128_m3", "k1024_m8"])
+def test_tb_gemv_core_legacy_block_dots(case):
+    """02/tb_gemv_core.v legacy cases: raw int32 block dots must be bit-exact."""
+    d = np.load(GOLD / "tb_gemv_core_legacy.npz")
+    lanes = ol.lane_sums(d[f"{case}_wq"], d[f"{case}_xq"])
+    assert np.array_equal(lanes.sum(-1).astype(np.int64), d[f"{case}_dots"])
+
+
+def test_lane_sums_brute_force_residues():
+    rng = np.random.default_rng(1)
+    M, K = 5, 320
+    mant = rng.integers(-128, 128, size=(M, K), dtype=np.int8)
+    xq = rng.integers(-16384, 16385, size=K).astype(np.int16)
+    lanes = ol.lane_sums(mant, xq)
+    prod = mant.astype(np.int64).reshape(M, K // 64, 16, 4) * xq.astype(np.int64).reshape(K // 64, 16, 4)
+    assert np.array_equal(lanes, prod.sum(axis=2))
+    # bound of the reference's accumulator lanes: |S_j| <= 16*128*16384 = 2^25
+    assert np.abs(lanes).max() <= 2 ** 25
+
+
+# ---- quantizer (04/qwen_kernels_opt.c:182-205) ------------------------------------------
+def test_quant_amax_element_maps_to_16384():
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal(256).astype(F32)
+    xq, xs = ol.quant_x(x)
+    for b in range(4):
+        blk = x[b * 64:(b + 1) * 64]
+        i = int(np.argmax(np.abs(blk)))
+        assert xq[b * 64 + i] == (16384 if blk[i] > 0 else -16384)
+        assert xs[b] == F32(np.abs(blk).max() / F32(16384))  # exact: division by 2^14
+    assert np.abs(xq.astype(np.int32)).max() <= 16384
+
+
+def test_quant_rounds_half_to_even():
+    """amax = 16384 makes q exactly 1, so xq = lrintf(x): ties go to even."""
+    x = np.zeros(64, dtype=F32)
+    x[0] = 16384.0
+    x[1:9] = [2.5, 3.5, -2.5, -3.5, 0.5, 1.5, -0.5, 16383.5]
+    xq, xs = ol.quant_x(x)
+    assert xs[0] == 1.0
+    assert list(xq[:9]) == [16384, 2, 4, -2, -4, 0, 2, 0, 16384]
+
+
+def test_quant_zero_tiny_nan_inf_blocks():
+    x = np.zeros(6 * 64, dtype=F32)
+    x[64:128] = F32(1e-20)                     # amax == 1e-20: not > 1e-20 -> zero block
+    x[128] = np.nextafter(F32(1e-20), F32(1))  # just above: quantized
+    x[192:256] = np.linspace(-1, 1, 64, dtype=F32)
+    x[200] = np.nan                             # NaN never wins the max; its xq is 0
+    x[256:320] = 1.0
+    x[300] = np.inf                             # amax = inf: q = 0, xscale = inf, xq = 0
+    x[320:384] = -F32(0.0)
+    xq, xs = ol.quant_x(x)
+    assert xs[0] == 0 and not xq[:64].any()
+    assert xs[1] == 0 and not xq[64:128].any()
+    assert xs[2] > 0 and xq[128] == 16384 and not xq[129:192].any()
+    assert xs[3] == F32(1.0) / F32(16384) and xq[200] == 0 and xq[255] == 16384 and xq[192] == -16384
+    assert math.isinf(xs[4]) and not xq[256:320].any()
+    assert xs[5] == 0 and not xq[320:].any()
+
+
+def test_quant_error_bound():
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal(4096) * np.repeat(10.0 ** rng.uniform(-8, 8, 64), 64)).astype(F32)
+    xq, xs = ol.quant_x(x)
+    recon = xq.astype(np.float64) / (16384.0 / np.repeat(xs.astype(np.float64) * 16384, 64))
+    err = np.abs(recon - x) / np.repeat(xs.astype(np.float64), 64)
+    assert err.max() <= 0.5 + 1e-3  # half an int16 step (plus the rounding of q)
+
+
+# ---- Advanced SIMD float model (ARM ARM FPRound with FPSCR.FZ = 1) ----------------------
+def test_neon_flush_to_zero_rules():
+    tiny = F32(2.0 ** -130)  # subnormal operand reads as zero
+    assert ol.neon_mul(tiny, F32(2.0 ** 10)) == 0.0
+    assert ol.neon_add(tiny, F32(0.0)) == 0.0
+    # subnormal result is written as (signed) zero
+    assert ol.neon_add(F32(1.5 * 2.0 ** -126), F32(-(2.0 ** -126))) == 0.0
+    # (a subnormal operand is itself read as zero: 2^-126 + (-2^-127) = 2^-126)
+    assert ol.neon_add(F32(2.0 ** -126), F32(-(2.0 ** -127))) == F32(2.0 ** -126)
+    r = ol.neon_mul(F32(-(2.0 ** -100)), F32(2.0 ** -30))
+    assert r == 0.0 and math.copysign(1.0, r) < 0
+    # tininess is decided before rounding: (1 - 2^-24) * 2^-126 would round up
+    # to FLT_MIN in IEEE arithmetic but is tiny, so it flushes
+    assert F32(1 - 2.0 ** -24) * F32(2.0 ** -126) == F32(2.0 ** -126)
+    assert ol.neon_mul(F32(1 - 2.0 ** -24), F32(2.0 ** -126)) == 0.0
+    # normal range: one rounding, as IEEE
+    a, b = F32(1.1), F32(3.3)
+    assert ol.neon_mul(a, b) == a * b and ol.neon_add(a, b) == a + b
+
+
+# ---- board-build GEMV closed forms --------------------------------------------------------
+def _block_inputs(res_w, res_xq):
+    """One 64-block from per-residue (w, xq) lists of 16; x = xq with a 16384
+    amax somewhere so that q = 1 and xscale = 1 exactly."""
+    w = np.zeros(64, dtype=np.int8)
+    xq = np.zeros(64, dtype=np.int32)
+    for j in range(4):
+        w[j::4] = res_w[j]
+        xq[j::4] = res_xq[j]
+    assert np.abs(xq).max() == 16384
+    return w, xq.astype(F32)
+
+
+def _gemv_single_block(w, x, M=2, e=134):
+    mant = np.tile(w, (M, 1))
+    exps = np.full((M, 1), e, dtype=np.uint8)
+    return ol.gemv_neon(x, mant, exps)
+
+
+def test_gemv_exact_small_case():
+    """With xscale = 1 and EXP_SCALE = 1 and small sums nothing rounds:
+    y equals the exact integer dot product."""
+    rng = np.random.default_rng(4)
+    M, K = 6, 256
+    mant = rng.integers(-3, 4, size=(M, K), dtype=np.int8)
+    x = rng.integers(-50, 51, size=K).astype(F32)
+    x[::64] = 16384.0
+    mant[:, ::64] = 0
+    exps = np.full((M, K // 64), 134, dtype=np.uint8)
+    y, xq, xs, lanes = ol.gemv_neon(x, mant, exps)
+    assert (xs == 1.0).all() and np.array_equal(xq, x.astype(np.int16))
+    assert np.array_equal(y.astype(np.int64), mant.astype(np.int64) @ x.astype(np.int64))
+    # exponent e scales by 2^(e-134) exactly
+    y2, *_ = ol.gemv_neon(x, mant, exps + 3)
+    assert np.array_equal(y2, y * 8)
+
+
+def test_gemv_lane_order_is_fs0_plus_fs2_then_fs1_plus_fs3():
+    """S = (2^24, 1, -2^24, 1): (fs0+fs2)+(fs1+fs3) = 2, whereas the sequential
+    lane order or (fs0+fs1)+(fs2+fs3) round 2^24+1 down and give 1."""
+    w, x = _block_inputs([[64] * 16, [1] + [0] * 15, [-64] * 16, [1] + [0] * 15],
+                         [[16384] * 16, [1] + [0] * 15, [16384] * 16, [1] + [0] * 15])
+    y, xq, xs, lanes = _gemv_single_block(w, x)
+    assert list(lanes[0, 0]) == [2 ** 24, 1, -(2 ** 24), 1]
+    assert list(y) == [2.0, 2.0]
+
+
+def test_gemv_converts_each_lane_before_summing():
+    """S_0 = 2^24+1 converts to 2^24 (ties-to-even) and cancels S_2 = -2^24, so
+    y = 0; converting the block total (= 1) first would give 1."""
+    r0w = [64] * 14 + [127, 5]
+    r0x = [16384] * 14 + [16384, 3277]
+    w, x = _block_inputs([r0w, [0] * 16, [-64] * 16, [0] * 16], [r0x, [0] * 16, [16384] * 16, [0] * 16])
+    y, _, _, lanes = _gemv_single_block(w, x)
+    assert lanes[0, 0, 0] == 2 ** 24 + 1
+    assert list(y) == [0.0, 0.0]
+
+
+def test_gemv_odd_last_row_uses_block_total_and_ieee():
+    """Odd M: the last row converts the block total (04/qwen_kernels_opt.c:299-303)
+    and runs on IEEE scalar floats, where EXP_SCALE[0] = 2^-134 is a subnormal
+    that the paired (flush-to-zero) rows read as 0."""
+    r0w = [64] * 14 + [127, 5]
+    r0x = [16384] * 14 + [16384, 3277]
+    w, x = _block_inputs([r0w, [0] * 16, [-64] * 16, [0] * 16], [r0x, [0] * 16, [16384] * 16, [0] * 16])
+    y, *_ = _gemv_single_block(w, x, M=3)
+    assert list(y) == [0.0, 0.0, 1.0]
+    w2, x2 = _block_inputs([[64] * 16, [0] * 16, [0] * 16, [0] * 16], [[16384] * 16, [0] * 16, [0] * 16, [0] * 16])
+    y0, *_ = _gemv_single_block(w2, x2, M=3, e=0)
+    assert y0[0] == 0.0 and y0[1] == 0.0
+    assert y0[2] == F32(2.0 ** 24 * 2.0 ** -134)  # 2^-110: normal, exact
+
+
+def test_gemv_against_float64_testbench_model():
+    """02/tb_gemv_core.v's golden model sums sum_b dots*2^(e-134)*xscale in
+    double; the float32 result stays within float rounding of it."""
+    rng = np.random.default_rng(5)
+    for K, M in ((128, 3), (1024, 8), (3584, 16)):
+        mant = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+        exps = rng.integers(118, 131, size=(M, K // 64), dtype=np.uint8)
+        x = rng.standard_normal(K).astype(F32) * np.repeat(2.0 ** rng.integers(0, 5, K // 64), 64).astype(F32)
+        y, xq, xs, lanes = ol.gemv_neon(x, mant, exps)
+        yd = ol.gemv_f64(mant, exps, xq, xs)
+        scale = (np.abs(lanes).sum(-1) * np.ldexp(1.0, exps.astype(int) - 134) * xs).sum(-1)
+        assert np.all(np.abs(y - yd) <= 4 * (K // 64 + 2) * 2.0 ** -24 * scale)
+
+
+# ---- the reference's host build (oracle/_ref) -----------------------------------------------
+@pytest.mark.parametrize("case", ["m6_k128", "m7_k192", "m64_k1024", "m5_k4160", "m3_k100"])
+def test_float_path_matches_reference_build(case):
+    d = np.load(GOLD / "ref_float_path.npz")
+    x, mant, exps, y = (d[f"{case}_{k}"] for k in ("x", "mant", "exps", "y"))
+    assert np.array_equal(ol.gemv_float(x, mant, exps).view(np.uint32), y.view(np.uint32))
+    if mant.shape[1] > 4096:  # the board build takes the float path there too
+        yn, *_ = ol.gemv_neon(x, mant, exps)
+        assert np.array_equal(yn.view(np.uint32), y.view(np.uint32))
+
+
+@pytest.mark.skipif(not ol.ref_available(), reason="oracle/_ref needs the reference sources")
+def test_float_path_matches_reference_build_live():
+    rng = np.random.default_rng(6)
+    for M, K in ((9, 64), (130, 640), (4, 8192)):
+        mant = rng.integers(-128, 128, size=(M, K), dtype=np.int8)
+        exps = rng.integers(0, 256, size=(M, K // 64), dtype=np.uint8)
+        x = rng.standard_normal(K).astype(F32)
+        assert np.array_equal(ol.gemv_float(x, mant, exps).view(np.uint32),
+                              ol.ref_gemv_float(x, mant, exps).view(np.uint32))
+
+
+TOPK_CASES = ["ties1000", "special1001", "vocab65536", "allnan64", "hugeneg128", "eqmax256"]
+
+
+def _brute_topk(v, k):
+    idx = [i for i in range(v.size) if v[i] > -np.finfo(np.float32).max]
+    idx.sort(key=lambda i: (-float(v[i]), i))
+    idx = idx[:k]
+    return np.array(idx, dtype=np.int32), v[idx]
+
+
+@pytest.mark.parametrize("case", TOPK_CASES)
+def test_topk_and_argmax_match_reference_build(case):
+    d = np.load(GOLD / "ref_topk.npz")
+    v = ol.bf16_to_f32(d[f"{case}_bits"])
+    assert ol.argmax(v) == int(d[f"{case}_argmax"])
+    for k in (1, 40, 64):
+        ids, sc = ol.topk(v, k)
+        assert np.array_equal(ids, d[f"{case}_k{k}_ids"])
+        assert np.array_equal(sc.view(np.uint32), d[f"{case}_k{k}_scores"].view(np.uint32))
+        bi, bs = _brute_topk(v, k)
+        assert np.array_equal(ids, bi)
+
+
+def test_oracle_regression_vectors():
+    d = np.load(GOLD / "oracle_neon.npz")
+    for case in ("m6_k128", "m7_k256", "m64_k1024"):
+        y, xq, xs, lanes = ol.gemv_neon(d[f"{case}_x"], d[f"{case}_mant"], d[f"{case}_exps"])
+        assert np.array_equal(y.view(np.uint32), d[f"{case}_y"].view(np.uint32))
+        assert np.array_equal(xq, d[f"{case}_xq"]) and np.array_equal(lanes, d[f"{case}_lanes"])
+        assert np.array_equal(xs.view(np.uint32), d[f"{case}_xscale"].view(np.uint32))
