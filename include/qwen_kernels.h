@@ -15,8 +15,8 @@
  *     arguments.
  *
  *  3. Device-level symbols (prefix bfp8_dev_ / bfp8_plan_): device pointers,
- *     an explicit HIP stream (hipStream_t passed as void*, NULL = the
- *     library's stream), asynchronous; return 0 on success or a negative
+ *     an explicit HIP stream (hipStream_t passed as void*; NULL is the HIP
+ *     default stream, bfp8_stream() the library's own), asynchronous; return 0 on success or a negative
  *     BFP8_E* code.  These keep weights and activations resident in HBM.
  *
  * Failure behaviour: the reference's bfp8_gemv has no error channel

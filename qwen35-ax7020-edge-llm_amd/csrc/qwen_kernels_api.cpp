@@ -162,7 +162,9 @@ int ensure_init_locked() {
     return BFP8_OK;
 }
 
-hipStream_t pick_stream(void* s) { return s ? static_cast<hipStream_t>(s) : g.stream; }
+// Device-level entry points run on the caller's stream; NULL is the HIP
+// default (null) stream, as everywhere in HIP.
+hipStream_t pick_stream(void* s) { return static_cast<hipStream_t>(s); }
 
 // Is every page of [p, p+n) mapped without write permission?
 bool range_readonly(const void* p, size_t n) {
