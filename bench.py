@@ -54,8 +54,12 @@ def workload_items(name):
         for layer in range(N_LAYERS):
             items += [(f"l{layer}.{t}", M, K, 124, 130, 0) for t, M, K in LAYER]
         return items
+    if name == "layers":  # the sweep without the lm_head
+        return [it for it in workload_items("sweep") if it[0] != "lm_head"]
     if name == "lm_head":
         return [("lm_head", *LM_HEAD, 122, 128, TOPK)]
+    if name == "lm_head_plain":  # the lm_head GEMV without the fused top-k
+        return [("lm_head", *LM_HEAD, 122, 128, 0)]
     if name == "gemv":
         return [("gemv", 3584, 1024, 124, 130, 0)]
     if name == "down":
@@ -130,7 +134,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="sweep", choices=["sweep", "lm_head", "gemv", "down", "batch16"])
+    ap.add_argument("--workload", default="sweep", choices=["sweep", "layers", "lm_head", "lm_head_plain", "gemv", "down", "batch16"])
     ap.add_argument("--rotate-gb", type=float, default=1.0, help="rotating weight copies totalling >= this")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     args = ap.parse_args()

@@ -14,9 +14,11 @@
 //
 // Work mapping: a workgroup of 4 wavefronts owns a tile of 64 rows; wavefront
 // q computes residue lane q of all 64 rows (lane = row), streaming one 1 KiB
-// contiguous dwordx4 load per block.  The residue's activation dwords are
-// wave-uniform and live in SGPRs (scalar loads), so the inner loop is
-// 8 x v_dot4_i32_i8 + 1 shift per 16 weight bytes per lane, no LDS traffic.
+// contiguous non-temporal dwordx4 load per block (the four wavefronts together
+// read 4 KiB contiguous per block step).  The GEMV's split activation is
+// staged once per workgroup in LDS and read with wave-uniform (broadcast) LDS
+// reads, so the inner loop is 8 x v_dot4_i32_i8 + 1 shift per 16 weight bytes
+// per lane with no scalar-load round trips.
 // The per-block float epilogue runs in block order inside each lane, which is
 // exactly the reference's per-lane accumulation order.  No MFMA: batch-1 is a
 // bandwidth-bound matrix-vector product.
@@ -39,26 +41,14 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
                                              kBufDword3);
 }
 
+// Weights are streamed once: non-temporal loads (cache policy bit nt).
+constexpr int kNonTemporal = 2;
 __device__ __forceinline__ u32x4 load_w(__amdgpu_buffer_rsrc_t rs, int voff, int soff) {
-    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, 0));
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, kNonTemporal));
 }
 
 __device__ __forceinline__ uint32_t load_e(__amdgpu_buffer_rsrc_t rs, int voff, int soff) {
     return __builtin_amdgcn_raw_buffer_load_b32(rs, voff, soff, 0);
-}
-
-// Exact S_q of one (row, block, residue): xq = 256*xh + xl.
-__device__ __forceinline__ int residue_sum(u32x4 w, sgpr_u32_ptr xb) {
-    int acc = __builtin_amdgcn_sdot4((int)w.x, (int)xb[0], 0, false);
-    acc = __builtin_amdgcn_sdot4((int)w.y, (int)xb[1], acc, false);
-    acc = __builtin_amdgcn_sdot4((int)w.z, (int)xb[2], acc, false);
-    acc = __builtin_amdgcn_sdot4((int)w.w, (int)xb[3], acc, false);
-    acc = (int)((uint32_t)acc << 8);
-    acc = __builtin_amdgcn_sdot4((int)w.x, (int)xb[4], acc, false);
-    acc = __builtin_amdgcn_sdot4((int)w.y, (int)xb[5], acc, false);
-    acc = __builtin_amdgcn_sdot4((int)w.z, (int)xb[6], acc, false);
-    acc = __builtin_amdgcn_sdot4((int)w.w, (int)xb[7], acc, false);
-    return acc;
 }
 
 // EXP_SCALE[e] under flush-to-zero: 2^(e-134) for e >= 8, else +0.
@@ -112,208 +102,335 @@ __device__ __forceinline__ uint64_t wave_sort_desc(uint64_t key, int lane) {
     return key;
 }
 
-// Bitonic sort of n (power of two) keys in LDS, descending; whole workgroup.
-__device__ void lds_sort_desc(uint64_t* s, int n) {
-    for (int k = 2; k <= n; k <<= 1) {
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            for (int i = threadIdx.x; i < (n >> 1); i += blockDim.x) {
-                int a = 2 * i - (i & (j - 1));
-                int c = a + j;
-                uint64_t x = s[a], y = s[c];
-                bool desc = (a & k) == 0;
-                if (desc ? (x < y) : (x > y)) {
-                    s[a] = y;
-                    s[c] = x;
-                }
-            }
-            __syncthreads();
-        }
+// Two descending lists of 64 keys (one per lane) -> the 64 largest of both,
+// descending: max(a[i], b[63-i]) is bitonic and holds them; six half-cleaner
+// stages sort it.
+__device__ __forceinline__ uint64_t wave_merge_desc(uint64_t a, uint64_t b_reversed, int lane) {
+    uint64_t c = a > b_reversed ? a : b_reversed;
+#pragma unroll
+    for (int j = 32; j > 0; j >>= 1) {
+        const uint64_t o = shfl_xor64(c, j);
+        const uint64_t mx = c > o ? c : o, mn = c > o ? o : c;
+        c = ((lane & j) == 0) ? mx : mn;
     }
+    return c;
 }
 
-__device__ __forceinline__ int pow2_ceil(int v) {
-    int p = 1;
-    while (p < v) p <<= 1;
-    return p;
+// The final merge runs as one workgroup of kMergeWaves wavefronts; each
+// wavefront keeps a running sorted top-64 in registers and the wavefronts are
+// reduced pairwise through LDS (log2(kMergeWaves) levels).
+constexpr int kMergeWaves = 16;
+constexpr int kMergeThreads = kMergeWaves * 64;
+
+struct MergeLds {
+    uint64_t xch[kMergeWaves][64];
+    int list[BFP8_TOPK_MAX];
+};
+
+// Tree-reduces every wavefront's sorted list into wavefront 0's.
+__device__ __forceinline__ uint64_t reduce_waves(uint64_t v, int w, int lane, MergeLds& L) {
+#pragma unroll
+    for (int step = 1; step < kMergeWaves; step <<= 1) {
+        if ((w & (2 * step - 1)) == step) L.xch[w][lane] = v;
+        __syncthreads();
+        if ((w & (2 * step - 1)) == 0) v = wave_merge_desc(v, L.xch[w + step][63 - lane], lane);
+        __syncthreads();
+    }
+    return v;
 }
 
-// Final merge of the per-tile top-k lists, run by the last workgroup.
-// Keys are unique (they carry the row), so an entry at position i of a list
-// whose head ranks h-th among all heads has at least h+i better keys: only
-// i < kk - h can reach the top kk, at most kk(kk+1)/2 candidates.
-__device__ void topk_merge(const Bfp8GemvDesc& d, int ntiles, uint64_t* s) {
+// Final merge of the per-tile top-k lists.  Keys are unique (they carry the
+// row), so an entry at position i of a list whose head ranks h-th among all
+// heads has at least h+i better keys: only the lists of the kk best heads, and
+// in them only i < kk - h, can reach the top kk.
+__device__ void topk_merge(const Bfp8GemvDesc& d, int ntiles, MergeLds& L) {
     const int kk = d.topk;
-    __shared__ int s_list[BFP8_TOPK_MAX];
-    const int np = pow2_ceil(ntiles);
-    for (int i = threadIdx.x; i < np; i += blockDim.x)
-        s[i] = (i < ntiles) ? __builtin_nontemporal_load(&d.partials[(size_t)i * kk]) : 0ull;
-    __syncthreads();
-    lds_sort_desc(s, np);
-    if ((int)threadIdx.x < kk) {
-        uint64_t h = ((int)threadIdx.x < np) ? s[threadIdx.x] : 0ull;
-        s_list[threadIdx.x] = h ? (key_id(h) / BFP8_TILE_ROWS) : -1;
+    const uint64_t* parts = d.partials;
+    const int lane = threadIdx.x & 63;
+    const int w = threadIdx.x >> 6;
+    // 1. the 64 best list heads
+    uint64_t v = 0;
+    for (int base = w * 64; base < ntiles; base += kMergeThreads) {
+        const int i = base + lane;
+        uint64_t h = i < ntiles ? __builtin_nontemporal_load(&parts[(size_t)i * kk]) : 0ull;
+        h = wave_sort_desc(h, lane);
+        v = wave_merge_desc(v, shfl_xor64(h, 63), lane);
     }
+    v = reduce_waves(v, w, lane, L);
+    if (w == 0 && lane < kk) L.list[lane] = v ? key_id(v) / BFP8_TILE_ROWS : -1;
     __syncthreads();
-    const int ncand = kk * (kk + 1) / 2;
-    const int nc = pow2_ceil(ncand);
-    for (int i = threadIdx.x; i < nc; i += blockDim.x) {
-        uint64_t v = 0;
-        if (i < ncand) {
-            int h = 0, off = 0;
-            while (off + (kk - h) <= i) {
-                off += kk - h;
-                ++h;
-            }
-            int list = s_list[h];
-            if (list >= 0) v = __builtin_nontemporal_load(&d.partials[(size_t)list * kk + (i - off)]);
-        }
-        s[i] = v;
+    // 2. merge those lists, list h cut after kk - h entries
+    v = 0;
+    for (int h = w; h < kk; h += kMergeWaves) {
+        const int list = L.list[h];
+        if (list < 0) continue;
+        const uint64_t e = lane < kk - h ? __builtin_nontemporal_load(&parts[(size_t)list * kk + lane]) : 0ull;
+        v = wave_merge_desc(v, shfl_xor64(e, 63), lane);
     }
-    __syncthreads();
-    lds_sort_desc(s, nc);
-    if (threadIdx.x < 64) {
-        int lane = threadIdx.x;
-        uint64_t v = (lane < kk) ? s[lane] : 0ull;
-        unsigned long long valid = __ballot(v != 0);
-        int cnt = __popcll(valid);
+    v = reduce_waves(v, w, lane, L);
+    if (w == 0) {
+        const uint64_t t = lane < kk ? v : 0ull;
+        const int cnt = __popcll(__ballot(t != 0));
         if (lane < kk) {
-            d.out_ids[lane] = v ? key_id(v) : -1;
-            d.out_scores[lane] = v ? key_score(v) : 0.0f;
+            d.out_ids[lane] = t ? key_id(t) : -1;
+            d.out_scores[lane] = t ? key_score(t) : 0.0f;
         }
         if (lane == 0) {
             *d.out_count = cnt;
             // lm_head_argmax: lowest id among maxima above -1e30, else 0
             // (04/qwen_kernels_opt.c:402-403, :483-490)
-            *d.out_argmax = (v && key_score(v) > -1e30f) ? key_id(v) : 0;
+            *d.out_argmax = (t && key_score(t) > -1e30f) ? key_id(t) : 0;
         }
     }
 }
 
-// ---- one 64-row tile --------------------------------------------------------
-// Returns y of row 64t+lane in wavefront 0 (unspecified in the others).
-__device__ __forceinline__ float gemv_tile(const Bfp8GemvDesc& d, int t, float* red) {
-    const int q = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
-    const int r = threadIdx.x & 63;
-    const int nb = d.K >> 6;
-    const int nb4 = (nb + 3) >> 2;
-    const uint8_t* mtile = d.mant + (size_t)t * nb * 4096u;
-    const uint8_t* etile = d.exps + (size_t)t * nb4 * 256u;
-    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(mtile, (uint32_t)nb * 4096u);
-    const __amdgpu_buffer_rsrc_t ers = make_rsrc(etile, (uint32_t)nb4 * 256u);
-    const int wv = q * 1024 + r * 16;
-    const int ev = r * 4;
-    const sgpr_u32_ptr xs = (sgpr_u32_ptr)(d.xsplit) + q * 8;
-    const sgpr_f32_ptr xsc = (sgpr_f32_ptr)(d.xscale);
-    const int row = t * BFP8_TILE_ROWS + r;
-    int32_t* lanes = d.lanes;
+// ---- persistent streaming GEMV ------------------------------------------------
+// A workgroup of 4 wavefronts owns one 64-row tile at a time; wavefront q
+// computes residue lane q of the tile's rows (lane = row).  Each workgroup
+// walks a list of tiles -- a host-built, byte-balanced slice of a tile table
+// (plans) or every gridDim-th tile of one GEMV -- and streams their weights as
+// chunks of kChunk blocks (8 KiB per wavefront).  The next chunk, including the
+// first chunk of the next tile, is always in flight while the current chunk is
+// reduced, so no workgroup stalls on a cold start between tiles.
 
-    float fs = 0.0f;
-    int b = 0;
-    const int nfull = nb & ~(kChunk - 1);
-    if (nfull > 0) {
-        u32x4 wa[kChunk], wb[kChunk];
-        uint32_t ea0, ea1, eb0, eb1;
-#pragma unroll
-        for (int u = 0; u < kChunk; ++u) wa[u] = load_w(wrs, wv, u * 4096);
-        ea0 = load_e(ers, ev, 0);
-        ea1 = load_e(ers, ev, 256);
-        for (;;) {
-            const bool more_a = b + kChunk < nfull;
-            if (more_a) {
-#pragma unroll
-                for (int u = 0; u < kChunk; ++u) wb[u] = load_w(wrs, wv, (b + kChunk + u) * 4096);
-                eb0 = load_e(ers, ev, ((b + kChunk) >> 2) * 256);
-                eb1 = load_e(ers, ev, ((b + kChunk) >> 2) * 256 + 256);
-            }
-#pragma unroll
-            for (int u = 0; u < kChunk; ++u) {
-                int S = residue_sum(wa[u], xs + (b + u) * 32);
-                uint32_t e = ((u < 4 ? ea0 : ea1) >> (8 * (u & 3))) & 0xffu;
-                fs = epilogue(fs, S, e, xsc[b + u]);
-                if (lanes && row < d.M) lanes[((size_t)row * nb + b + u) * 4 + q] = S;
-            }
-            b += kChunk;
-            if (!more_a) break;
-            const bool more_b = b + kChunk < nfull;
-            if (more_b) {
-#pragma unroll
-                for (int u = 0; u < kChunk; ++u) wa[u] = load_w(wrs, wv, (b + kChunk + u) * 4096);
-                ea0 = load_e(ers, ev, ((b + kChunk) >> 2) * 256);
-                ea1 = load_e(ers, ev, ((b + kChunk) >> 2) * 256 + 256);
-            }
-#pragma unroll
-            for (int u = 0; u < kChunk; ++u) {
-                int S = residue_sum(wb[u], xs + (b + u) * 32);
-                uint32_t e = ((u < 4 ? eb0 : eb1) >> (8 * (u & 3))) & 0xffu;
-                fs = epilogue(fs, S, e, xsc[b + u]);
-                if (lanes && row < d.M) lanes[((size_t)row * nb + b + u) * 4 + q] = S;
-            }
-            b += kChunk;
-            if (!more_b) break;
-        }
-    }
-    for (; b < nb; ++b) {  // remainder blocks (K/64 not a multiple of 8)
-        u32x4 w = load_w(wrs, wv, b * 4096);
-        uint32_t e = (load_e(ers, ev, (b >> 2) * 256) >> (8 * (b & 3))) & 0xffu;
-        int S = residue_sum(w, xs + b * 32);
-        fs = epilogue(fs, S, e, xsc[b]);
-        if (lanes && row < d.M) lanes[((size_t)row * nb + b) * 4 + q] = S;
-    }
+struct WBuf {  // one chunk: 8 residue chunks of 16 B and two exponent words
+    u32x4 w[kChunk];
+    uint32_t e0, e1;
+};
 
-    red[q * 64 + r] = fs;
-    __syncthreads();
-    float y = 0.0f;
-    if (q == 0) {
-        // vadd_f32(low, high) then vpadd_f32: (fs0 + fs2) + (fs1 + fs3)
-        y = (red[r] + red[128 + r]) + (red[64 + r] + red[192 + r]);
-        if (d.y && row < d.pair_rows) d.y[row] = y;
-    }
-    return y;
+struct Tile {  // the tile being streamed; every field is wave-uniform
+    const uint8_t* mant;  // this tile's mantissas (nb * 4 KiB)
+    const uint8_t* exps;  // this tile's exponent words (nb4 * 256 B)
+    const uint32_t* xsplit;
+    const float* xscale;
+    int nb, desc, tile;
+};
+
+struct StreamLds {
+    float red[2][256];  // cross-wave reduction, double-buffered by tile parity
+};
+
+__device__ __forceinline__ int nchunks(const Tile& T) { return (T.nb + kChunk - 1) / kChunk; }
+
+__device__ __forceinline__ void open_tile(Tile& T, const Bfp8GemvDesc& d, int desc, int t) {
+    const int nb = d.K >> 6, nb4 = (nb + 3) >> 2;
+    T.mant = d.mant + (size_t)t * nb * 4096u;
+    T.exps = d.exps + (size_t)t * nb4 * 256u;
+    T.xsplit = d.xsplit;
+    T.xscale = d.xscale;
+    T.nb = nb;
+    T.desc = desc;
+    T.tile = t;
 }
 
-__device__ __forceinline__ void run_tile(const Bfp8GemvDesc& d, int t, float* red, uint64_t* sbuf) {
-    const float y = gemv_tile(d, t, red);
-    if (d.topk <= 0) return;
-    const int ntiles = (d.M + BFP8_TILE_ROWS - 1) / BFP8_TILE_ROWS;
-    const int lane = threadIdx.x & 63;
+// wv[u]: this lane's byte offset of block u of a chunk (q*1 KiB + lane*16 +
+// u*4 KiB); the chunk itself is one scalar offset.
+__device__ __forceinline__ void issue(WBuf& B, const Tile& T, int c, const int* wv, int ev) {
+    const int b0 = c * kChunk;
+    const int cn = min(kChunk, T.nb - b0);
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(T.mant, (uint32_t)T.nb * 4096u);
+    const __amdgpu_buffer_rsrc_t ers = make_rsrc(T.exps, (uint32_t)((T.nb + 3) >> 2) * 256u);
+    if (cn == kChunk) {
+#pragma unroll
+        for (int u = 0; u < kChunk; ++u) B.w[u] = load_w(wrs, wv[u], b0 * 4096);
+    } else {
+#pragma unroll
+        for (int u = 0; u < kChunk; ++u)
+            if (u < cn) B.w[u] = load_w(wrs, wv[u], b0 * 4096);
+    }
+    B.e0 = load_e(ers, ev, (b0 >> 2) * 256);
+    B.e1 = (cn > 4) ? load_e(ers, ev, ((b0 >> 2) + 1) * 256) : 0u;
+}
+
+// Exact S_q of one (row, block, residue) from the scalar-loaded split activation.
+__device__ __forceinline__ int residue_sum(u32x4 w, sgpr_u32_ptr xb) {
+    int acc = __builtin_amdgcn_sdot4((int)w.x, (int)xb[0], 0, false);
+    acc = __builtin_amdgcn_sdot4((int)w.y, (int)xb[1], acc, false);
+    acc = __builtin_amdgcn_sdot4((int)w.z, (int)xb[2], acc, false);
+    acc = __builtin_amdgcn_sdot4((int)w.w, (int)xb[3], acc, false);
+    acc = (int)((uint32_t)acc << 8);
+    acc = __builtin_amdgcn_sdot4((int)w.x, (int)xb[4], acc, false);
+    acc = __builtin_amdgcn_sdot4((int)w.y, (int)xb[5], acc, false);
+    acc = __builtin_amdgcn_sdot4((int)w.z, (int)xb[6], acc, false);
+    acc = __builtin_amdgcn_sdot4((int)w.w, (int)xb[7], acc, false);
+    return acc;
+}
+
+// lanes_row: this lane's row of the optional [M][nb][4] residue-lane output.
+template <bool kLanes>
+__device__ __forceinline__ float reduce_block(float fs, const WBuf& B, int u, const Tile& T, int b, int q,
+                                              int32_t* lanes_row) {
+    const int S = residue_sum(B.w[u], (sgpr_u32_ptr)T.xsplit + (b * 4 + q) * 8);
+    const uint32_t e = ((u < 4 ? B.e0 : B.e1) >> (8 * (u & 3))) & 0xffu;
+    if (kLanes && lanes_row) lanes_row[b * 4 + q] = S;
+    return epilogue(fs, S, e, ((sgpr_f32_ptr)T.xscale)[b]);
+}
+
+template <bool kLanes>
+__device__ __forceinline__ float reduce_chunk(float fs, const WBuf& B, const Tile& T, int c, int q,
+                                              int32_t* lanes_row) {
+    const int b0 = c * kChunk;
+    const int cn = min(kChunk, T.nb - b0);
+    if (cn == kChunk) {
+#pragma unroll
+        for (int u = 0; u < kChunk; ++u) fs = reduce_block<kLanes>(fs, B, u, T, b0 + u, q, lanes_row);
+    } else {
+#pragma unroll
+        for (int u = 0; u < kChunk; ++u)
+            if (u < cn) fs = reduce_block<kLanes>(fs, B, u, T, b0 + u, q, lanes_row);
+    }
+    return fs;
+}
+
+// Per-tile top-k partial: the tile's keys sorted in wavefront 0, the best
+// `topk` stored.  Plain stores: the merge runs as the next kernel on the
+// stream, so the kernel boundary makes them visible -- no cross-workgroup
+// fence (an L2 write-back on this GPU) per tile.
+__device__ __noinline__ void topk_partial(const Bfp8GemvDesc& d, int t, float y) {
     if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
         const int row = t * BFP8_TILE_ROWS + lane;
         uint64_t key = (row < d.pair_rows) ? topk_key(y, row) : 0ull;
         key = wave_sort_desc(key, lane);
         if (lane < d.topk) d.partials[(size_t)t * d.topk + lane] = key;
     }
-    __threadfence();
+}
+
+// Cross-wave combine of a finished tile: vadd_f32(low, high) then vpadd_f32,
+// i.e. y = (fs0 + fs2) + (fs1 + fs3).
+__device__ __forceinline__ void finish_tile(const Bfp8GemvDesc& d, const Tile& T, float fs, int q, int r,
+                                            int parity, StreamLds& L) {
+    float* red = L.red[parity];
+    red[q * 64 + r] = fs;
     __syncthreads();
-    __shared__ int s_last;
-    if (threadIdx.x == 0) {
-        unsigned prev = atomicAdd(d.counter, 1u);
-        s_last = (prev == (unsigned)(ntiles - 1));
+    float y = 0.0f;
+    if (q == 0) {
+        y = (red[r] + red[128 + r]) + (red[64 + r] + red[192 + r]);
+        const int row = T.tile * BFP8_TILE_ROWS + r;
+        if (d.y && row < d.pair_rows) d.y[row] = y;
     }
-    __syncthreads();
-    if (s_last) {
-        __threadfence();
-        topk_merge(d, ntiles, sbuf);
-        if (threadIdx.x == 0) atomicExch(d.counter, 0u);
+    if (d.topk > 0) topk_partial(d, T.tile, y);
+}
+
+// Tile lists: a slice of a tile table, or a strided walk over one GEMV.
+struct TableTiles {
+    const Bfp8GemvDesc* descs;
+    const Bfp8TileRef* tiles;
+    int beg, cnt;
+    __device__ int count() const { return cnt; }
+    __device__ void get(int i, int& desc, int& tile) const {
+        const Bfp8TileRef tr = tiles[beg + i];
+        desc = tr.desc;
+        tile = tr.tile;
+    }
+    __device__ const Bfp8GemvDesc& desc(int i) const { return descs[i]; }
+};
+
+struct StridedTiles {
+    const Bfp8GemvDesc* d;
+    int ntiles;
+    __device__ int count() const {
+        return (int)blockIdx.x < ntiles ? (ntiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x : 0;
+    }
+    __device__ void get(int i, int& desc, int& tile) const {
+        desc = 0;
+        tile = (int)blockIdx.x + i * (int)gridDim.x;
+    }
+    __device__ const Bfp8GemvDesc& desc(int) const { return *d; }
+};
+
+// One half of the double-buffered stream: reduce `cur` (chunk `c` of tile
+// `Tc`) while the following chunk goes out into `nxt` / `Tn`.  Returns false
+// after the last chunk of the list.
+template <bool kLanes, class Src>
+__device__ __forceinline__ bool stream_step(const Src& src, WBuf& cur, WBuf& nxt, Tile& Tc, Tile& Tn, int& i,
+                                            int& c, float& fs, int& parity, int q, int r, const int* wv,
+                                            int ev, StreamLds& L) {
+    const int n = src.count();
+    int ni = i, nc = c + 1;
+    bool more = true;
+    if (nc == nchunks(Tc)) {
+        ni = i + 1;
+        nc = 0;
+        more = ni < n;
+        if (more) {
+            int di, ti;
+            src.get(ni, di, ti);
+            open_tile(Tn, src.desc(di), di, ti);
+        }
+    } else {
+        Tn = Tc;
+    }
+    if (more) issue(nxt, Tn, nc, wv, ev);
+    int32_t* lanes_row = nullptr;
+    if (kLanes) {
+        const Bfp8GemvDesc& dc = src.desc(Tc.desc);
+        const int row = Tc.tile * BFP8_TILE_ROWS + r;
+        if (dc.lanes && row < dc.M) lanes_row = dc.lanes + (size_t)row * Tc.nb * 4;
+    }
+    fs = reduce_chunk<kLanes>(fs, cur, Tc, c, q, lanes_row);
+    if (nc == 0 || !more) {
+        finish_tile(src.desc(Tc.desc), Tc, fs, q, r, parity, L);
+        fs = 0.0f;
+        parity ^= 1;
+    }
+    i = ni;
+    c = nc;
+    return more;
+}
+
+template <bool kLanes, class Src>
+__device__ __forceinline__ void stream_tiles(const Src& src, StreamLds& L) {
+    const int n = src.count();
+    if (n <= 0) return;
+    const int q = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int r = threadIdx.x & 63;
+    int wv[kChunk];
+#pragma unroll
+    for (int u = 0; u < kChunk; ++u) wv[u] = q * 1024 + r * 16 + u * 4096;
+    const int ev = r * 4;
+    Tile TA, TB;
+    WBuf A, B;
+    {
+        int di, ti;
+        src.get(0, di, ti);
+        open_tile(TA, src.desc(di), di, ti);
+    }
+    issue(A, TA, 0, wv, ev);
+    int i = 0, c = 0, parity = 0;
+    float fs = 0.0f;
+    for (;;) {
+        if (!stream_step<kLanes>(src, A, B, TA, TB, i, c, fs, parity, q, r, wv, ev, L)) break;
+        if (!stream_step<kLanes>(src, B, A, TB, TA, i, c, fs, parity, q, r, wv, ev, L)) break;
     }
 }
 
 }  // namespace
 
-// Single GEMV: grid = ntiles(M) workgroups of 256.
-extern "C" __global__ __launch_bounds__(256) void bfp8_gemv_kernel(Bfp8GemvDesc d) {
-    __shared__ float red[256];
-    extern __shared__ uint64_t sbuf[];
-    run_tile(d, blockIdx.x, red, sbuf);
+// Single GEMV, persistent: workgroup w takes tiles w, w + gridDim, ...
+// kLanes also writes the int32 residue-lane block sums.
+template <bool kLanes>
+__global__ __launch_bounds__(256) void bfp8_gemv_kernel(Bfp8GemvDesc d) {
+    __shared__ StreamLds L;
+    StridedTiles src{&d, (d.M + BFP8_TILE_ROWS - 1) / BFP8_TILE_ROWS};
+    stream_tiles<kLanes>(src, L);
 }
 
-// Grouped GEMV: one workgroup per (GEMV, tile) entry of the tile table.
+// Final top-k merge of one fused lm_head (one workgroup), launched right after
+// the GEMV kernel that wrote the per-tile partials.
+extern "C" __global__ __launch_bounds__(kMergeThreads) void bfp8_topk_merge_kernel(Bfp8GemvDesc d) {
+    __shared__ MergeLds L;
+    topk_merge(d, (d.M + BFP8_TILE_ROWS - 1) / BFP8_TILE_ROWS, L);
+}
+
+// Grouped GEMV, persistent: workgroup w walks tiles[wg_off[w] .. wg_off[w+1]).
 extern "C" __global__ __launch_bounds__(256) void bfp8_gemv_grouped_kernel(
-    const Bfp8GemvDesc* __restrict__ descs, const Bfp8TileRef* __restrict__ tiles) {
-    __shared__ float red[256];
-    extern __shared__ uint64_t sbuf[];
-    const Bfp8TileRef tr = tiles[blockIdx.x];
-    const Bfp8GemvDesc d = descs[tr.desc];
-    run_tile(d, tr.tile, red, sbuf);
+    const Bfp8GemvDesc* __restrict__ descs, const Bfp8TileRef* __restrict__ tiles,
+    const int* __restrict__ wg_off) {
+    __shared__ StreamLds L;
+    const int beg = wg_off[blockIdx.x];
+    TableTiles src{descs, tiles, beg, wg_off[blockIdx.x + 1] - beg};
+    stream_tiles<false>(src, L);
 }
 
 // Batched GEMV: B activation vectors against one weight matrix, weights read
@@ -397,20 +514,49 @@ __global__ __launch_bounds__(256) void bfp8_gemv_batch_kernel(float* __restrict_
 }
 
 // ---- launchers ---------------------------------------------------------------
+// Workgroups a persistent kernel keeps resident: all CUs times the kernel's
+// occupancy (capped at BFP8_STREAM_WG_PER_CU), queried once per kernel.
+static int resident_grid(const void* kernel) {
+    int dev = 0, cus = 256, occ = 0;
+    if (hipGetDevice(&dev) == hipSuccess) {
+        hipDeviceProp_t p;
+        if (hipGetDeviceProperties(&p, dev) == hipSuccess) cus = p.multiProcessorCount;
+    }
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, 256, 0) != hipSuccess || occ <= 0) occ = 1;
+    return cus * (occ < BFP8_STREAM_WG_PER_CU ? occ : BFP8_STREAM_WG_PER_CU);
+}
+
+int bfp8_stream_grid() {
+    static const int grid = resident_grid(reinterpret_cast<const void*>(bfp8_gemv_grouped_kernel));
+    return grid;
+}
+
 hipError_t bfp8_launch_gemv(const Bfp8GemvDesc& d, hipStream_t s) {
     const int nt = bfp8_ntiles(d.M);
     if (nt == 0) return hipSuccess;
-    const size_t lds = d.topk > 0 ? BFP8_TOPK_LDS_BYTES : 0;
-    hipLaunchKernelGGL(bfp8_gemv_kernel, dim3(nt), dim3(256), lds, s, d);
+    static const int g_plain = resident_grid(reinterpret_cast<const void*>(bfp8_gemv_kernel<false>));
+    static const int g_lanes = resident_grid(reinterpret_cast<const void*>(bfp8_gemv_kernel<true>));
+    const int cap = d.lanes ? g_lanes : g_plain;
+    const int grid = nt < cap ? nt : cap;
+    if (d.lanes)
+        hipLaunchKernelGGL(bfp8_gemv_kernel<true>, dim3(grid), dim3(256), 0, s, d);
+    else
+        hipLaunchKernelGGL(bfp8_gemv_kernel<false>, dim3(grid), dim3(256), 0, s, d);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || d.topk <= 0) return e;
+    return bfp8_launch_topk_merge(d, s);
+}
+
+hipError_t bfp8_launch_topk_merge(const Bfp8GemvDesc& d, hipStream_t s) {
+    hipLaunchKernelGGL(bfp8_topk_merge_kernel, dim3(1), dim3(kMergeThreads), 0, s, d);
     return hipGetLastError();
 }
 
 hipError_t bfp8_launch_gemv_grouped(const Bfp8GemvDesc* descs_dev, const Bfp8TileRef* tiles_dev,
-                                    int ntiles, bool any_topk, hipStream_t s) {
-    if (ntiles <= 0) return hipSuccess;
-    const size_t lds = any_topk ? BFP8_TOPK_LDS_BYTES : 0;
-    hipLaunchKernelGGL(bfp8_gemv_grouped_kernel, dim3(ntiles), dim3(256), lds, s, descs_dev,
-                       tiles_dev);
+                                    const int* wg_off_dev, int nwg, hipStream_t s) {
+    if (nwg <= 0) return hipSuccess;
+    hipLaunchKernelGGL(bfp8_gemv_grouped_kernel, dim3(nwg), dim3(256), 0, s, descs_dev, tiles_dev,
+                       wg_off_dev);
     return hipGetLastError();
 }
 

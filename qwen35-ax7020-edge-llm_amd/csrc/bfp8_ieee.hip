@@ -229,24 +229,26 @@ extern "C" __global__ __launch_bounds__(256) void bfp8_synth_kernel(
 }
 
 // ---- bandwidth probes -----------------------------------------------------------
-// Read-only ceiling: dwordx4 grid-stride reads folded into one word per thread
-// block (so the loads cannot be dropped).
+// Read-only ceiling: each workgroup streams one contiguous chunk with eight
+// non-temporal dwordx4 loads in flight per thread; the folded value is stored
+// only if it hits a magic constant, which keeps the loads live without any
+// atomic traffic.
 extern "C" __global__ __launch_bounds__(256) void bfp8_read_probe_kernel(
-    const u32x4* __restrict__ src, size_t n16, uint32_t* __restrict__ out) {
+    const u32x4* __restrict__ src, size_t n16, size_t chunk16, uint32_t* __restrict__ out) {
     u32x4 acc = u32x4(0u);
-    const size_t stride = (size_t)gridDim.x * blockDim.x;
-    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    for (; i + 3 * stride < n16; i += 4 * stride) {
-        u32x4 a = __builtin_nontemporal_load(src + i);
-        u32x4 b = __builtin_nontemporal_load(src + i + stride);
-        u32x4 c = __builtin_nontemporal_load(src + i + 2 * stride);
-        u32x4 d = __builtin_nontemporal_load(src + i + 3 * stride);
-        acc ^= a ^ b ^ c ^ d;
+    const size_t beg = (size_t)blockIdx.x * chunk16;
+    const size_t end = beg + chunk16 < n16 ? beg + chunk16 : n16;
+    size_t i = beg + threadIdx.x;
+    for (; i + 7 * 256 < end; i += 8 * 256) {
+        u32x4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = __builtin_nontemporal_load(src + i + u * 256);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc ^= v[u];
     }
-    for (; i < n16; i += stride) acc ^= __builtin_nontemporal_load(src + i);
-    uint32_t v = acc.x ^ acc.y ^ acc.z ^ acc.w;
-    for (int m = 32; m >= 1; m >>= 1) v ^= (uint32_t)__shfl_xor((int)v, m, 64);
-    if ((threadIdx.x & 63) == 0) atomicXor(out, v);
+    for (; i < end; i += 256) acc ^= __builtin_nontemporal_load(src + i);
+    const uint32_t v = acc.x ^ acc.y ^ acc.z ^ acc.w;
+    if (v == 0x9E3779B9u) out[0] = v;
 }
 
 extern "C" __global__ __launch_bounds__(256) void bfp8_copy_probe_kernel(
@@ -329,7 +331,9 @@ hipError_t bfp8_launch_synth_planes(int8_t* mant_soa, uint8_t* exps_soa, int M, 
 hipError_t bfp8_launch_read_probe(const void* buf, size_t bytes, uint32_t* out, hipStream_t s) {
     const size_t n16 = bytes / 16;
     if (n16 == 0) return hipSuccess;
-    hipLaunchKernelGGL(bfp8_read_probe_kernel, dim3(256 * 16), dim3(256), 0, s, (const u32x4*)buf, n16, out);
+    const int grid = 4096;
+    const size_t chunk16 = (n16 + grid - 1) / grid;
+    hipLaunchKernelGGL(bfp8_read_probe_kernel, dim3(grid), dim3(256), 0, s, (const u32x4*)buf, n16, chunk16, out);
     return hipGetLastError();
 }
 

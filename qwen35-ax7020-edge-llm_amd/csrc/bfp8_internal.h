@@ -28,7 +28,6 @@ struct Bfp8GemvDesc {
     int pair_rows;           // rows computed with the paired (NEON) epilogue: M & ~1
     int topk;                // 0: plain GEMV; 1..64: fused lm_head top-k over the rows
     uint64_t* partials;      // [ntiles][topk] per-tile sorted keys (topk > 0)
-    uint32_t* counter;       // tiles finished; zero between launches (topk > 0)
     int* out_ids;            // [topk]
     float* out_scores;       // [topk]
     int* out_count;          // number of valid entries
@@ -53,12 +52,19 @@ struct Bfp8TileRef {
 
 #define BFP8_TOPK_MAX 64
 #define BFP8_TOPK_MAX_TILES 4096
-#define BFP8_TOPK_LDS_BYTES (4096 * 8)
+#define BFP8_STREAM_WG_PER_CU 4
 
 // ---- bfp8_ftz.hip --------------------------------------------------------
+// Single GEMV (and, for topk > 0, the merge kernel after it).
 hipError_t bfp8_launch_gemv(const Bfp8GemvDesc& d, hipStream_t s);
+// Final top-k merge of a fused lm_head whose partials a GEMV kernel wrote.
+hipError_t bfp8_launch_topk_merge(const Bfp8GemvDesc& d, hipStream_t s);
+// Persistent grouped launch: workgroup w walks tiles_dev[wg_off_dev[w] ..
+// wg_off_dev[w+1]); nwg <= bfp8_stream_grid().
 hipError_t bfp8_launch_gemv_grouped(const Bfp8GemvDesc* descs_dev, const Bfp8TileRef* tiles_dev,
-                                    int ntiles, bool any_topk, hipStream_t s);
+                                    const int* wg_off_dev, int nwg, hipStream_t s);
+// Number of workgroups the persistent GEMV kernels keep resident.
+int bfp8_stream_grid();
 hipError_t bfp8_launch_gemv_batch(float* Y, const uint32_t* xsplit, const float* xscale,
                                   const uint8_t* mant, const uint8_t* exps, int M, int K, int B,
                                   hipStream_t s);

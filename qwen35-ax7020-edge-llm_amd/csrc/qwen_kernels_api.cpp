@@ -14,6 +14,7 @@
 #include <ctime>
 #include <map>
 #include <mutex>
+#include <queue>
 #include <string>
 #include <tuple>
 #include <vector>
@@ -136,7 +137,7 @@ struct State {
     PinnedBuf h_in, h_out;
     DevBuf x, xq, xscale, xsplit, y;            // activation / output workspace
     DevBuf soa_m, soa_e, gpu_m, gpu_e;          // per-call weight upload
-    DevBuf tk_partials, tk_counter, tk_out;     // fused lm_head workspace
+    DevBuf tk_partials, tk_out;                 // fused lm_head workspace
     std::map<WeightKey, CachedWeights> cache;
     size_t cache_bytes = 0;
 };
@@ -154,10 +155,6 @@ int ensure_init_locked() {
     }
     HIP_OK(hipGetDevice(&g.device));
     HIP_OK(hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking));
-    // tk_counter must start at zero; the fused lm_head's last workgroup
-    // resets it after every launch.
-    if (g.tk_counter.reserve(256) != BFP8_OK) return BFP8_EHIP;
-    HIP_OK(hipMemset(g.tk_counter.p, 0, g.tk_counter.n));
     g.ready = true;
     return BFP8_OK;
 }
@@ -320,7 +317,6 @@ int lm_head_dev(int* ids, float* scores, int* count, int* argmax, const uint32_t
     Bfp8GemvDesc d = plain_desc(nullptr, xsplit, xscale, m, e, vocab, hidden, nullptr);
     d.topk = kk;
     d.partials = g.tk_partials.as<uint64_t>();
-    d.counter = g.tk_counter.as<uint32_t>();
     d.out_ids = ids;
     d.out_scores = scores;
     d.out_count = count;
@@ -648,8 +644,8 @@ struct Plan {
     std::vector<bfp8_plan_item> items;
     std::vector<int> odd_items;    // items needing the odd-row kernel
     std::vector<int> float_items;  // K > 4096 items (float path, own launches)
-    DevBuf descs, tiles, qdescs, xq, xscale, xsplit, partials, counter;
-    int ntiles = 0, nq = 0, max_nb = 0;
+    DevBuf descs, tiles, qdescs, xq, xscale, xsplit, partials, wg_off;
+    int ntiles = 0, nq = 0, max_nb = 0, nwg = 0;
     bool any_topk = false;
     std::vector<Bfp8GemvDesc> hdesc;
 };
@@ -700,7 +696,6 @@ void* bfp8_plan_create(const bfp8_plan_item* items, int n) {
     rc = rc ? rc : p->xscale.reserve(xsc_floats * 4);
     rc = rc ? rc : p->xq.reserve(xq_elems * 2);
     std::vector<Bfp8QuantDesc> hq;
-    std::vector<std::pair<int, int>> order;  // (item, first tile)
     size_t ow = 0, of = 0, oq = 0;
     for (int i = 0; i < n && !rc; ++i) {
         const bfp8_plan_item& it = items[i];
@@ -723,10 +718,7 @@ void* bfp8_plan_create(const bfp8_plan_item* items, int n) {
             if (it.M & 1) rc = BFP8_EINVAL;
             d.topk = std::min(it.topk, it.M);
             rc = rc ? rc : p->partials.reserve((size_t)bfp8_ntiles(it.M) * d.topk * 8);
-            rc = rc ? rc : p->counter.reserve(256);
-            if (!rc && hipMemset(p->counter.p, 0, 256) != hipSuccess) rc = BFP8_EHIP;
             d.partials = p->partials.as<uint64_t>();
-            d.counter = p->counter.as<uint32_t>();
             d.out_ids = it.out_ids;
             d.out_scores = it.out_scores;
             d.out_count = it.out_count;
@@ -740,7 +732,9 @@ void* bfp8_plan_create(const bfp8_plan_item* items, int n) {
         oq += (size_t)nb * 64;
     }
     // Tile order: the lm_head first (its final merge then overlaps the
-    // rest), then larger K before smaller K (longer workgroups start first).
+    // rest), then larger K before smaller K.  Tiles are dealt to the
+    // persistent kernel's workgroups longest-first onto the least-loaded
+    // workgroup (bytes), and each workgroup walks its tiles in dealing order.
     std::vector<int> idx;
     for (int i = 0; i < n; ++i)
         if (items[i].K <= 4096) idx.push_back(i);
@@ -749,22 +743,46 @@ void* bfp8_plan_create(const bfp8_plan_item* items, int n) {
         if (ta != tb) return ta;
         return items[a].K > items[b].K;
     });
-    std::vector<Bfp8TileRef> tiles;
+    std::vector<Bfp8TileRef> order;
     for (int i : idx)
-        for (int t = 0; t < bfp8_ntiles(items[i].M); ++t) tiles.push_back(Bfp8TileRef{i, t});
+        for (int t = 0; t < bfp8_ntiles(items[i].M); ++t) order.push_back(Bfp8TileRef{i, t});
+    const int nwg = std::min<int>((int)order.size(), bfp8_stream_grid());
+    std::vector<std::vector<Bfp8TileRef>> per(nwg);
+    {
+        using Load = std::pair<long long, int>;
+        std::priority_queue<Load, std::vector<Load>, std::greater<Load>> heap;
+        for (int w = 0; w < nwg; ++w) heap.push({0LL, w});
+        for (const Bfp8TileRef& tr : order) {
+            Load l = heap.top();
+            heap.pop();
+            per[l.second].push_back(tr);
+            l.first += (long long)bfp8_nblocks(items[tr.desc].K) * 4160;
+            heap.push(l);
+        }
+    }
+    std::vector<Bfp8TileRef> tiles;
+    std::vector<int> wg_off(1, 0);
+    for (const auto& v : per) {
+        tiles.insert(tiles.end(), v.begin(), v.end());
+        wg_off.push_back((int)tiles.size());
+    }
     p->ntiles = (int)tiles.size();
+    p->nwg = nwg;
     p->nq = (int)hq.size();
     rc = rc ? rc : p->descs.reserve(p->hdesc.size() * sizeof(Bfp8GemvDesc));
     rc = rc ? rc : p->tiles.reserve(tiles.size() * sizeof(Bfp8TileRef));
     rc = rc ? rc : p->qdescs.reserve(hq.size() * sizeof(Bfp8QuantDesc));
+    rc = rc ? rc : p->wg_off.reserve(wg_off.size() * sizeof(int));
     if (!rc && (hipMemcpy(p->descs.p, p->hdesc.data(), p->hdesc.size() * sizeof(Bfp8GemvDesc), hipMemcpyHostToDevice) != hipSuccess ||
                 (!tiles.empty() && hipMemcpy(p->tiles.p, tiles.data(), tiles.size() * sizeof(Bfp8TileRef), hipMemcpyHostToDevice) != hipSuccess) ||
-                (!hq.empty() && hipMemcpy(p->qdescs.p, hq.data(), hq.size() * sizeof(Bfp8QuantDesc), hipMemcpyHostToDevice) != hipSuccess)))
+                (!hq.empty() && hipMemcpy(p->qdescs.p, hq.data(), hq.size() * sizeof(Bfp8QuantDesc), hipMemcpyHostToDevice) != hipSuccess) ||
+                hipMemcpy(p->wg_off.p, wg_off.data(), wg_off.size() * sizeof(int), hipMemcpyHostToDevice) != hipSuccess))
         rc = BFP8_EHIP;
     if (rc) {
         set_error("bfp8_plan_create: allocation or upload failed (%d)", rc);
         p->descs.release(); p->tiles.release(); p->qdescs.release(); p->xq.release();
-        p->xscale.release(); p->xsplit.release(); p->partials.release(); p->counter.release();
+        p->xscale.release(); p->xsplit.release(); p->partials.release();
+        p->wg_off.release();
         delete p;
         return nullptr;
     }
@@ -782,8 +800,10 @@ int bfp8_plan_run_gemv(void* plan, void* stream) {
     Plan* p = static_cast<Plan*>(plan);
     if (!p) return BFP8_EINVAL;
     hipStream_t s = pick_stream(stream);
-    HIP_OK(bfp8_launch_gemv_grouped(p->descs.as<Bfp8GemvDesc>(), p->tiles.as<Bfp8TileRef>(), p->ntiles,
-                                    p->any_topk, s));
+    HIP_OK(bfp8_launch_gemv_grouped(p->descs.as<Bfp8GemvDesc>(), p->tiles.as<Bfp8TileRef>(),
+                                    p->wg_off.as<int>(), p->nwg, s));
+    for (const Bfp8GemvDesc& d : p->hdesc)
+        if (d.topk > 0) HIP_OK(bfp8_launch_topk_merge(d, s));
     for (int i : p->odd_items) {
         const Bfp8GemvDesc& d = p->hdesc[i];
         HIP_OK(bfp8_launch_tail_row(d.y, d.xsplit, d.xscale, d.mant, d.exps, d.M, d.K, s));
@@ -808,7 +828,8 @@ void bfp8_plan_destroy(void* plan) {
         if (g.ready) (void)hipDeviceSynchronize();
     }
     p->descs.release(); p->tiles.release(); p->qdescs.release(); p->xq.release();
-    p->xscale.release(); p->xsplit.release(); p->partials.release(); p->counter.release();
+    p->xscale.release(); p->xsplit.release(); p->partials.release();
+    p->wg_off.release();
     delete p;
 }
 
