@@ -15,13 +15,14 @@
 // Work mapping: a workgroup of 4 wavefronts owns a tile of 64 rows; wavefront
 // q computes residue lane q of all 64 rows (lane = row), streaming one 1 KiB
 // contiguous non-temporal dwordx4 load per block (the four wavefronts together
-// read 4 KiB contiguous per block step).  The GEMV's split activation is
-// staged once per workgroup in LDS and read with wave-uniform (broadcast) LDS
-// reads, so the inner loop is 8 x v_dot4_i32_i8 + 1 shift per 16 weight bytes
-// per lane with no scalar-load round trips.
-// The per-block float epilogue runs in block order inside each lane, which is
-// exactly the reference's per-lane accumulation order.  No MFMA: batch-1 is a
-// bandwidth-bound matrix-vector product.
+// read 4 KiB contiguous per block step).  The split activation (xq = 256*xh +
+// xl, four bytes per dword) is read with scalar loads straight into SGPRs, so
+// the inner loop is 8 x v_dot4_i32_i8 with SGPR operands + 1 shift per 16
+// weight bytes per lane.  The GEMV kernels are persistent: a resident grid of
+// workgroups streams a list of tiles each with the next chunk always in
+// flight.  The per-block float epilogue runs in block order inside each lane,
+// which is exactly the reference's per-lane accumulation order.  No MFMA:
+// batch-1 is a bandwidth-bound matrix-vector product.
 #include <float.h>
 #include <hip/hip_runtime.h>
 
@@ -33,7 +34,9 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef const __attribute__((address_space(4))) uint32_t* sgpr_u32_ptr;
 typedef const __attribute__((address_space(4))) float* sgpr_f32_ptr;
 
-constexpr int kChunk = 8;              // blocks per load batch (8 KiB per wave)
+constexpr int kChunk = 4;       // streamed blocks per load batch (4 KiB per wavefront)
+constexpr int kBatchChunk = 8;  // blocks per LDS-staged step of the batched kernel
+static_assert(kChunk == 4 || kChunk == 8, "a chunk spans one or two exponent words");
 constexpr int kBufDword3 = 0x00020000;  // gfx9 raw buffer descriptor word 3
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
@@ -80,94 +83,175 @@ __device__ __forceinline__ float key_score(uint64_t k) {
 }
 __device__ __forceinline__ int key_id(uint64_t k) { return (int)~(uint32_t)k; }
 
-__device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int m) {
-    int lo = __shfl_xor((int)(uint32_t)v, m, 64);
-    int hi = __shfl_xor((int)(uint32_t)(v >> 32), m, 64);
-    return ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
+// ---- wavefront exchange ----------------------------------------------------
+// Lane i receives lane i^j.  j = 1, 2: DPP quad permutes; j = 4, 8, 16:
+// ds_swizzle bit-mask mode (and 0x1f, xor j, within 32 lanes); j = 32, 63:
+// ds_bpermute.  Always called with j a constant after unrolling.
+__device__ __forceinline__ uint32_t xor_lane32(uint32_t v, int j) {
+    switch (j) {
+        case 1: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);
+        case 2: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);
+        case 4: return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x1F | (4 << 10));
+        case 8: return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x1F | (8 << 10));
+        case 16: return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x1F | (16 << 10));
+        default: return (uint32_t)__shfl_xor((int)v, j, 64);
+    }
+}
+__device__ __forceinline__ uint64_t xor_lane(uint64_t v, int j) {
+    const uint32_t lo = xor_lane32((uint32_t)v, j);
+    const uint32_t hi = xor_lane32((uint32_t)(v >> 32), j);
+    return ((uint64_t)hi << 32) | lo;
 }
 
-// Bitonic sort of one key per lane, descending by lane (wave64).
-__device__ __forceinline__ uint64_t wave_sort_desc(uint64_t key, int lane) {
+// Bitonic sort of N independent columns (one key per lane each), column n
+// descending by lane when desc[n], else ascending; the N compare-exchange
+// chains interleave.  A compare-exchange keeps the partner's key when
+// (partner > own) equals "this lane keeps the larger" -- one 64-bit compare
+// and one select.
+template <int N>
+__device__ __forceinline__ void wave_sort(uint64_t (&key)[N], const bool (&desc)[N], int lane) {
 #pragma unroll
     for (int k = 2; k <= 64; k <<= 1) {
 #pragma unroll
         for (int j = k >> 1; j > 0; j >>= 1) {
-            uint64_t o = shfl_xor64(key, j);
-            bool take_max = ((lane & j) == 0) == ((lane & k) == 0);
-            uint64_t mx = key > o ? key : o;
-            uint64_t mn = key > o ? o : key;
-            key = take_max ? mx : mn;
+            const bool up = ((lane & j) == 0) == ((lane & k) == 0);
+#pragma unroll
+            for (int n = 0; n < N; ++n) {
+                const uint64_t o = xor_lane(key[n], j);
+                key[n] = ((o > key[n]) == (up == desc[n])) ? o : key[n];
+            }
         }
     }
-    return key;
 }
 
-// Two descending lists of 64 keys (one per lane) -> the 64 largest of both,
-// descending: max(a[i], b[63-i]) is bitonic and holds them; six half-cleaner
-// stages sort it.
-__device__ __forceinline__ uint64_t wave_merge_desc(uint64_t a, uint64_t b_reversed, int lane) {
-    uint64_t c = a > b_reversed ? a : b_reversed;
+// a and b sorted in opposite directions -> the 64 largest keys of both,
+// sorted descending (kDesc) or ascending: max(a[i], b[i]) holds them as a
+// bitonic sequence, six half-cleaner stages sort it.
+template <bool kDesc>
+__device__ __forceinline__ uint64_t wave_merge(uint64_t a, uint64_t b, int lane) {
+    uint64_t c = a > b ? a : b;
 #pragma unroll
     for (int j = 32; j > 0; j >>= 1) {
-        const uint64_t o = shfl_xor64(c, j);
-        const uint64_t mx = c > o ? c : o, mn = c > o ? o : c;
-        c = ((lane & j) == 0) ? mx : mn;
+        const uint64_t o = xor_lane(c, j);
+        c = ((o > c) == (((lane & j) == 0) == kDesc)) ? o : c;
     }
     return c;
 }
 
-// The final merge runs as one workgroup of kMergeWaves wavefronts; each
-// wavefront keeps a running sorted top-64 in registers and the wavefronts are
-// reduced pairwise through LDS (log2(kMergeWaves) levels).
-constexpr int kMergeWaves = 16;
-constexpr int kMergeThreads = kMergeWaves * 64;
+// Pairwise tree merge of N (power of two) lists held as even = descending,
+// odd = ascending; the result is descending.
+template <int N>
+__device__ __forceinline__ uint64_t wave_merge_tree(uint64_t (&v)[N], int lane) {
+#pragma unroll
+    for (int s = 1; s < N; s <<= 1) {
+#pragma unroll
+        for (int i = 0; i < N; i += 2 * s) {
+            if ((i / (2 * s)) % 2 == 0)
+                v[i] = wave_merge<true>(v[i], v[i + s], lane);
+            else
+                v[i] = wave_merge<false>(v[i], v[i + s], lane);
+        }
+    }
+    return v[0];
+}
 
+// ---- top-k final merge ---------------------------------------------------------
+// The per-tile partials ([ntiles][topk] sorted keys) are written by one
+// streaming launch and merged by a later launch on the same stream: the
+// kernel boundary makes them visible, so no cross-workgroup fence or atomic
+// is needed.  The merge runs as its own 16-wavefront kernel, or folded into
+// workgroup 0 of the next grouped launch (4 wavefronts).
+
+// What the merge needs of a descriptor, by value so that non-inlined code
+// never takes the address of a kernel argument.
+struct TopkArgs {
+    const uint64_t* partials;
+    int* out_ids;
+    float* out_scores;
+    int* out_count;
+    int* out_argmax;
+    int topk, ntiles;
+};
+
+__device__ __forceinline__ TopkArgs topk_args(const Bfp8GemvDesc& d) {
+    return TopkArgs{d.partials, d.out_ids, d.out_scores, d.out_count, d.out_argmax, d.topk, bfp8_ntiles(d.M)};
+}
+
+template <int W>
 struct MergeLds {
-    uint64_t xch[kMergeWaves][64];
+    uint64_t xch[W][64];
     int list[BFP8_TOPK_MAX];
 };
 
-// Tree-reduces every wavefront's sorted list into wavefront 0's.
-__device__ __forceinline__ uint64_t reduce_waves(uint64_t v, int w, int lane, MergeLds& L) {
+// Tree-reduces the W wavefronts' descending lists into wavefront 0's (the
+// partner's list is read reversed, i.e. ascending).
+template <int W>
+__device__ __forceinline__ uint64_t reduce_waves(uint64_t v, int w, int lane, MergeLds<W>& L) {
 #pragma unroll
-    for (int step = 1; step < kMergeWaves; step <<= 1) {
+    for (int step = 1; step < W; step <<= 1) {
         if ((w & (2 * step - 1)) == step) L.xch[w][lane] = v;
         __syncthreads();
-        if ((w & (2 * step - 1)) == 0) v = wave_merge_desc(v, L.xch[w + step][63 - lane], lane);
+        if ((w & (2 * step - 1)) == 0) v = wave_merge<true>(v, L.xch[w + step][63 - lane], lane);
         __syncthreads();
     }
     return v;
 }
 
-// Final merge of the per-tile top-k lists.  Keys are unique (they carry the
-// row), so an entry at position i of a list whose head ranks h-th among all
-// heads has at least h+i better keys: only the lists of the kk best heads, and
-// in them only i < kk - h, can reach the top kk.
-__device__ void topk_merge(const Bfp8GemvDesc& d, int ntiles, MergeLds& L) {
+// Final merge by one workgroup of W wavefronts, H list heads per lane per
+// pass.  Keys are unique (they carry the row), so an entry at position i of a
+// list whose head ranks h-th among all heads has at least h+i better keys:
+// only the lists of the kk best heads, and in them only i < kk - h, can reach
+// the top kk.
+template <int W, int H>
+__device__ __forceinline__ void topk_merge(const TopkArgs& d, MergeLds<W>& L) {
     const int kk = d.topk;
+    const int ntiles = d.ntiles;
     const uint64_t* parts = d.partials;
     const int lane = threadIdx.x & 63;
     const int w = threadIdx.x >> 6;
     // 1. the 64 best list heads
     uint64_t v = 0;
-    for (int base = w * 64; base < ntiles; base += kMergeThreads) {
-        const int i = base + lane;
-        uint64_t h = i < ntiles ? __builtin_nontemporal_load(&parts[(size_t)i * kk]) : 0ull;
-        h = wave_sort_desc(h, lane);
-        v = wave_merge_desc(v, shfl_xor64(h, 63), lane);
+    for (int base = w * 64 * H; base < ntiles; base += W * 64 * H) {
+        uint64_t h[H];
+        bool desc[H];
+#pragma unroll
+        for (int u = 0; u < H; ++u) {
+            const int i = base + u * 64 + lane;
+            h[u] = i < ntiles ? __builtin_nontemporal_load(&parts[(size_t)i * kk]) : 0ull;
+            desc[u] = (H > 1) && (u % 2 == 0);  // the last tree level must come out ascending
+        }
+        wave_sort<H>(h, desc, lane);
+#pragma unroll
+        for (int s = 1; s < H; s <<= 1) {
+#pragma unroll
+            for (int i = 0; i < H; i += 2 * s) {
+                if ((i / (2 * s)) % 2 == 0 && 2 * s < H)
+                    h[i] = wave_merge<true>(h[i], h[i + s], lane);
+                else
+                    h[i] = wave_merge<false>(h[i], h[i + s], lane);
+            }
+        }
+        v = wave_merge<true>(v, h[0], lane);
     }
-    v = reduce_waves(v, w, lane, L);
+    v = reduce_waves<W>(v, w, lane, L);
     if (w == 0 && lane < kk) L.list[lane] = v ? key_id(v) / BFP8_TILE_ROWS : -1;
     __syncthreads();
-    // 2. merge those lists, list h cut after kk - h entries
-    v = 0;
-    for (int h = w; h < kk; h += kMergeWaves) {
-        const int list = L.list[h];
-        if (list < 0) continue;
-        const uint64_t e = lane < kk - h ? __builtin_nontemporal_load(&parts[(size_t)list * kk + lane]) : 0ull;
-        v = wave_merge_desc(v, shfl_xor64(e, 63), lane);
+    // 2. wavefront w merges lists h = w, w + W, ... (list h cut after kk - h
+    // entries); odd slots are loaded reversed (ascending) for the tree.
+    constexpr int kSlots = BFP8_TOPK_MAX / W;
+    uint64_t e[kSlots];
+#pragma unroll
+    for (int sl = 0; sl < kSlots; ++sl) {
+        const int hh = w + sl * W;
+        const int list = hh < kk ? L.list[hh] : -1;
+        const int idx = (sl & 1) ? 63 - lane : lane;
+        e[sl] = (list >= 0 && idx < kk - hh) ? __builtin_nontemporal_load(&parts[(size_t)list * kk + idx]) : 0ull;
     }
-    v = reduce_waves(v, w, lane, L);
+    if (kSlots > 1)
+        v = wave_merge_tree<kSlots>(e, lane);
+    else
+        v = e[0];
+    v = reduce_waves<W>(v, w, lane, L);
     if (w == 0) {
         const uint64_t t = lane < kk ? v : 0ull;
         const int cnt = __popcll(__ballot(t != 0));
@@ -184,16 +268,38 @@ __device__ void topk_merge(const Bfp8GemvDesc& d, int ntiles, MergeLds& L) {
     }
 }
 
+constexpr int kWaves = 4;        // wavefronts per GEMV workgroup
+constexpr int kMergeWaves = 16;  // wavefronts of the stand-alone merge kernel
+
+// Folded merge for workgroup 0 of a grouped launch.
+__device__ __noinline__ void topk_merge_folded(TopkArgs d, MergeLds<kWaves>& L) {
+    topk_merge<kWaves, 4>(d, L);
+    __syncthreads();  // L is reused by the streaming code
+}
+
+// Per-tile top-k partial: the tile's keys sorted in wavefront 0, the best
+// `topk` stored.  Plain stores: the merge runs in a later launch.
+__device__ __noinline__ void topk_partial(uint64_t* partials, int topk, int pair_rows, int t, float y) {
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        const int row = t * BFP8_TILE_ROWS + lane;
+        uint64_t key[1] = {(row < pair_rows) ? topk_key(y, row) : 0ull};
+        const bool desc[1] = {true};
+        wave_sort<1>(key, desc, lane);
+        if (lane < topk) partials[(size_t)t * topk + lane] = key[0];
+    }
+}
+
 // ---- persistent streaming GEMV ------------------------------------------------
 // A workgroup of 4 wavefronts owns one 64-row tile at a time; wavefront q
 // computes residue lane q of the tile's rows (lane = row).  Each workgroup
 // walks a list of tiles -- a host-built, byte-balanced slice of a tile table
 // (plans) or every gridDim-th tile of one GEMV -- and streams their weights as
-// chunks of kChunk blocks (8 KiB per wavefront).  The next chunk, including the
+// chunks of kChunk blocks (1 KiB per block per wavefront).  The next chunk, including the
 // first chunk of the next tile, is always in flight while the current chunk is
 // reduced, so no workgroup stalls on a cold start between tiles.
 
-struct WBuf {  // one chunk: 8 residue chunks of 16 B and two exponent words
+struct WBuf {  // one chunk: kChunk residue slices of 16 B and its exponent word(s)
     u32x4 w[kChunk];
     uint32_t e0, e1;
 };
@@ -207,7 +313,8 @@ struct Tile {  // the tile being streamed; every field is wave-uniform
 };
 
 struct StreamLds {
-    float red[2][256];  // cross-wave reduction, double-buffered by tile parity
+    float red[2][256];        // cross-wave reduction, double-buffered by tile parity
+    MergeLds<kWaves> merge;   // folded top-k merge (workgroup 0 only)
 };
 
 __device__ __forceinline__ int nchunks(const Tile& T) { return (T.nb + kChunk - 1) / kChunk; }
@@ -239,7 +346,7 @@ __device__ __forceinline__ void issue(WBuf& B, const Tile& T, int c, const int* 
             if (u < cn) B.w[u] = load_w(wrs, wv[u], b0 * 4096);
     }
     B.e0 = load_e(ers, ev, (b0 >> 2) * 256);
-    B.e1 = (cn > 4) ? load_e(ers, ev, ((b0 >> 2) + 1) * 256) : 0u;
+    B.e1 = (kChunk > 4 && cn > 4) ? load_e(ers, ev, ((b0 >> 2) + 1) * 256) : 0u;
 }
 
 // Exact S_q of one (row, block, residue) from the scalar-loaded split activation.
@@ -282,20 +389,6 @@ __device__ __forceinline__ float reduce_chunk(float fs, const WBuf& B, const Til
     return fs;
 }
 
-// Per-tile top-k partial: the tile's keys sorted in wavefront 0, the best
-// `topk` stored.  Plain stores: the merge runs as the next kernel on the
-// stream, so the kernel boundary makes them visible -- no cross-workgroup
-// fence (an L2 write-back on this GPU) per tile.
-__device__ __noinline__ void topk_partial(const Bfp8GemvDesc& d, int t, float y) {
-    if (threadIdx.x < 64) {
-        const int lane = threadIdx.x;
-        const int row = t * BFP8_TILE_ROWS + lane;
-        uint64_t key = (row < d.pair_rows) ? topk_key(y, row) : 0ull;
-        key = wave_sort_desc(key, lane);
-        if (lane < d.topk) d.partials[(size_t)t * d.topk + lane] = key;
-    }
-}
-
 // Cross-wave combine of a finished tile: vadd_f32(low, high) then vpadd_f32,
 // i.e. y = (fs0 + fs2) + (fs1 + fs3).
 __device__ __forceinline__ void finish_tile(const Bfp8GemvDesc& d, const Tile& T, float fs, int q, int r,
@@ -309,7 +402,7 @@ __device__ __forceinline__ void finish_tile(const Bfp8GemvDesc& d, const Tile& T
         const int row = T.tile * BFP8_TILE_ROWS + r;
         if (d.y && row < d.pair_rows) d.y[row] = y;
     }
-    if (d.topk > 0) topk_partial(d, T.tile, y);
+    if (d.topk > 0) topk_partial(d.partials, d.topk, d.pair_rows, T.tile, y);
 }
 
 // Tile lists: a slice of a tile table, or a strided walk over one GEMV.
@@ -416,21 +509,23 @@ __global__ __launch_bounds__(256) void bfp8_gemv_kernel(Bfp8GemvDesc d) {
     stream_tiles<kLanes>(src, L);
 }
 
-// Final top-k merge of one fused lm_head (one workgroup), launched right after
-// the GEMV kernel that wrote the per-tile partials.
-extern "C" __global__ __launch_bounds__(kMergeThreads) void bfp8_topk_merge_kernel(Bfp8GemvDesc d) {
-    __shared__ MergeLds L;
-    topk_merge(d, (d.M + BFP8_TILE_ROWS - 1) / BFP8_TILE_ROWS, L);
-}
-
 // Grouped GEMV, persistent: workgroup w walks tiles[wg_off[w] .. wg_off[w+1]).
+// With merge_desc >= 0, workgroup 0 first merges that descriptor's top-k
+// partials, written by an earlier launch on the stream.
 extern "C" __global__ __launch_bounds__(256) void bfp8_gemv_grouped_kernel(
     const Bfp8GemvDesc* __restrict__ descs, const Bfp8TileRef* __restrict__ tiles,
-    const int* __restrict__ wg_off) {
+    const int* __restrict__ wg_off, int merge_desc) {
     __shared__ StreamLds L;
+    if (merge_desc >= 0 && blockIdx.x == 0) topk_merge_folded(topk_args(descs[merge_desc]), L.merge);
     const int beg = wg_off[blockIdx.x];
     TableTiles src{descs, tiles, beg, wg_off[blockIdx.x + 1] - beg};
     stream_tiles<false>(src, L);
+}
+
+// Stand-alone final top-k merge (one workgroup of 16 wavefronts).
+extern "C" __global__ __launch_bounds__(kMergeWaves * 64) void bfp8_topk_merge_kernel(Bfp8GemvDesc d) {
+    __shared__ MergeLds<kMergeWaves> L;
+    topk_merge<kMergeWaves, 1>(topk_args(d), L);
 }
 
 // Batched GEMV: B activation vectors against one weight matrix, weights read
@@ -443,7 +538,7 @@ __global__ __launch_bounds__(256) void bfp8_gemv_batch_kernel(float* __restrict_
                                                               const uint8_t* __restrict__ mant,
                                                               const uint8_t* __restrict__ exps, int M,
                                                               int K) {
-    __shared__ uint32_t xl[B * kChunk * 32];
+    __shared__ uint32_t xl[B * kBatchChunk * 32];
     __shared__ float red[4 * 64 * B];
     const int q = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int r = threadIdx.x & 63;
@@ -460,29 +555,29 @@ __global__ __launch_bounds__(256) void bfp8_gemv_batch_kernel(float* __restrict_
 #pragma unroll
     for (int v = 0; v < B; ++v) fs[v] = 0.0f;
 
-    for (int b0 = 0; b0 < nb; b0 += kChunk) {
-        const int nbc = min(kChunk, nb - b0);
-        u32x4 w[kChunk];
+    for (int b0 = 0; b0 < nb; b0 += kBatchChunk) {
+        const int nbc = min(kBatchChunk, nb - b0);
+        u32x4 w[kBatchChunk];
         uint32_t ew[2] = {0u, 0u};
 #pragma unroll
-        for (int u = 0; u < kChunk; ++u)
+        for (int u = 0; u < kBatchChunk; ++u)
             if (u < nbc) w[u] = load_w(wrs, wv, (b0 + u) * 4096);
         ew[0] = load_e(ers, r * 4, (b0 >> 2) * 256);
         if (nbc > 4) ew[1] = load_e(ers, r * 4, (b0 >> 2) * 256 + 256);
         __syncthreads();  // previous chunk's LDS reads are done
         for (int i = threadIdx.x; i < B * nbc * 32; i += 256) {
             int v = i / (nbc * 32), o = i - v * nbc * 32;
-            xl[v * kChunk * 32 + o] = xsplit[(size_t)v * xwords + b0 * 32 + o];
+            xl[v * kBatchChunk * 32 + o] = xsplit[(size_t)v * xwords + b0 * 32 + o];
         }
         __syncthreads();
 #pragma unroll
-        for (int u = 0; u < kChunk; ++u) {
+        for (int u = 0; u < kBatchChunk; ++u) {
             if (u >= nbc) break;
             const uint32_t e = (ew[u >> 2] >> (8 * (u & 3))) & 0xffu;
             const float sc = exp_scale_ftz(e);
 #pragma unroll
             for (int v = 0; v < B; ++v) {
-                const uint32_t* xb = xl + (v * kChunk + u) * 32 + q * 8;
+                const uint32_t* xb = xl + (v * kBatchChunk + u) * 32 + q * 8;
                 const uint4 h = *reinterpret_cast<const uint4*>(xb);
                 const uint4 l = *reinterpret_cast<const uint4*>(xb + 4);
                 int acc = __builtin_amdgcn_sdot4((int)w[u].x, (int)h.x, 0, false);
@@ -548,15 +643,15 @@ hipError_t bfp8_launch_gemv(const Bfp8GemvDesc& d, hipStream_t s) {
 }
 
 hipError_t bfp8_launch_topk_merge(const Bfp8GemvDesc& d, hipStream_t s) {
-    hipLaunchKernelGGL(bfp8_topk_merge_kernel, dim3(1), dim3(kMergeThreads), 0, s, d);
+    hipLaunchKernelGGL(bfp8_topk_merge_kernel, dim3(1), dim3(kMergeWaves * 64), 0, s, d);
     return hipGetLastError();
 }
 
 hipError_t bfp8_launch_gemv_grouped(const Bfp8GemvDesc* descs_dev, const Bfp8TileRef* tiles_dev,
-                                    const int* wg_off_dev, int nwg, hipStream_t s) {
+                                    const int* wg_off_dev, int nwg, int merge_desc, hipStream_t s) {
     if (nwg <= 0) return hipSuccess;
     hipLaunchKernelGGL(bfp8_gemv_grouped_kernel, dim3(nwg), dim3(256), 0, s, descs_dev, tiles_dev,
-                       wg_off_dev);
+                       wg_off_dev, merge_desc);
     return hipGetLastError();
 }
 

@@ -55,14 +55,19 @@ struct Bfp8TileRef {
 #define BFP8_STREAM_WG_PER_CU 4
 
 // ---- bfp8_ftz.hip --------------------------------------------------------
-// Single GEMV (and, for topk > 0, the merge kernel after it).
+// Single GEMV (for topk > 0 followed by the stand-alone merge kernel).
 hipError_t bfp8_launch_gemv(const Bfp8GemvDesc& d, hipStream_t s);
-// Final top-k merge of a fused lm_head whose partials a GEMV kernel wrote.
+// Stand-alone final top-k merge of partials an earlier launch wrote.
 hipError_t bfp8_launch_topk_merge(const Bfp8GemvDesc& d, hipStream_t s);
 // Persistent grouped launch: workgroup w walks tiles_dev[wg_off_dev[w] ..
-// wg_off_dev[w+1]); nwg <= bfp8_stream_grid().
+// wg_off_dev[w+1]); nwg <= bfp8_stream_grid().  merge_desc >= 0: workgroup 0
+// first merges the top-k partials of descs_dev[merge_desc] (written by an
+// earlier launch on the stream).
 hipError_t bfp8_launch_gemv_grouped(const Bfp8GemvDesc* descs_dev, const Bfp8TileRef* tiles_dev,
-                                    const int* wg_off_dev, int nwg, hipStream_t s);
+                                    const int* wg_off_dev, int nwg, int merge_desc, hipStream_t s);
+// Extra load, in blocks of the byte-balanced dealing, that a folded merge
+// puts on workgroup 0 of a grouped launch.
+#define BFP8_MERGE_COST_BLOCKS 16
 // Number of workgroups the persistent GEMV kernels keep resident.
 int bfp8_stream_grid();
 hipError_t bfp8_launch_gemv_batch(float* Y, const uint32_t* xsplit, const float* xscale,

@@ -640,15 +640,64 @@ int bfp8_dev_copy_probe(void* dst, const void* src, size_t bytes, void* stream) 
 // =========================== plans ================================================
 namespace {
 
+// One persistent grouped launch: its dealt tile table.
+struct Launch {
+    DevBuf tiles, wg_off;
+    int nwg = 0;
+};
+
 struct Plan {
     std::vector<bfp8_plan_item> items;
     std::vector<int> odd_items;    // items needing the odd-row kernel
     std::vector<int> float_items;  // K > 4096 items (float path, own launches)
-    DevBuf descs, tiles, qdescs, xq, xscale, xsplit, partials, wg_off;
-    int ntiles = 0, nq = 0, max_nb = 0, nwg = 0;
-    bool any_topk = false;
+    DevBuf descs, qdescs, xq, xscale, xsplit, partials;
+    Launch head, rest;             // lm_head tiles, then every other GEMV's
+    int nq = 0, max_nb = 0;
+    int topk_desc = -1;            // the lm_head item, if any
     std::vector<Bfp8GemvDesc> hdesc;
 };
+
+// Deals the tiles of `idx` (in that order) over at most bfp8_stream_grid()
+// workgroups, longest first onto the least-loaded workgroup (bytes), and
+// uploads the table.  `wg0_extra` blocks of load are pre-charged to
+// workgroup 0 (a folded merge).
+int deal_tiles(Launch& L, const std::vector<int>& idx, const bfp8_plan_item* items, int wg0_extra) {
+    std::vector<Bfp8TileRef> order;
+    for (int i : idx)
+        for (int t = 0; t < bfp8_ntiles(items[i].M); ++t) order.push_back(Bfp8TileRef{i, t});
+    if (order.empty()) return BFP8_OK;
+    const int nwg = std::min<int>((int)order.size(), bfp8_stream_grid());
+    std::vector<std::vector<Bfp8TileRef>> per(nwg);
+    using Load = std::pair<long long, int>;
+    std::priority_queue<Load, std::vector<Load>, std::greater<Load>> heap;
+    for (int w = 0; w < nwg; ++w) heap.push({w == 0 ? (long long)wg0_extra * 4160 : 0LL, w});
+    for (const Bfp8TileRef& tr : order) {
+        Load l = heap.top();
+        heap.pop();
+        per[l.second].push_back(tr);
+        l.first += (long long)bfp8_nblocks(items[tr.desc].K) * 4160;
+        heap.push(l);
+    }
+    std::vector<Bfp8TileRef> tiles;
+    std::vector<int> wg_off(1, 0);
+    for (const auto& v : per) {
+        tiles.insert(tiles.end(), v.begin(), v.end());
+        wg_off.push_back((int)tiles.size());
+    }
+    int rc;
+    if ((rc = L.tiles.reserve(tiles.size() * sizeof(Bfp8TileRef))) || (rc = L.wg_off.reserve(wg_off.size() * sizeof(int))))
+        return rc;
+    HIP_OK(hipMemcpy(L.tiles.p, tiles.data(), tiles.size() * sizeof(Bfp8TileRef), hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(L.wg_off.p, wg_off.data(), wg_off.size() * sizeof(int), hipMemcpyHostToDevice));
+    L.nwg = nwg;
+    return BFP8_OK;
+}
+
+void release_plan(Plan* p) {
+    p->descs.release(); p->qdescs.release(); p->xq.release(); p->xscale.release(); p->xsplit.release();
+    p->partials.release();
+    p->head.tiles.release(); p->head.wg_off.release(); p->rest.tiles.release(); p->rest.wg_off.release();
+}
 
 }  // namespace
 
@@ -723,7 +772,7 @@ void* bfp8_plan_create(const bfp8_plan_item* items, int n) {
             d.out_scores = it.out_scores;
             d.out_count = it.out_count;
             d.out_argmax = it.out_argmax;
-            p->any_topk = true;
+            p->topk_desc = (int)p->hdesc.size();
         }
         if ((it.M & 1) && it.topk <= 0) p->odd_items.push_back(i);
         p->hdesc.push_back(d);
@@ -731,58 +780,28 @@ void* bfp8_plan_create(const bfp8_plan_item* items, int n) {
         of += nb;
         oq += (size_t)nb * 64;
     }
-    // Tile order: the lm_head first (its final merge then overlaps the
-    // rest), then larger K before smaller K.  Tiles are dealt to the
-    // persistent kernel's workgroups longest-first onto the least-loaded
-    // workgroup (bytes), and each workgroup walks its tiles in dealing order.
-    std::vector<int> idx;
-    for (int i = 0; i < n; ++i)
-        if (items[i].K <= 4096) idx.push_back(i);
-    std::stable_sort(idx.begin(), idx.end(), [&](int a, int b) {
-        const bool ta = items[a].topk > 0, tb = items[b].topk > 0;
-        if (ta != tb) return ta;
-        return items[a].K > items[b].K;
-    });
-    std::vector<Bfp8TileRef> order;
-    for (int i : idx)
-        for (int t = 0; t < bfp8_ntiles(items[i].M); ++t) order.push_back(Bfp8TileRef{i, t});
-    const int nwg = std::min<int>((int)order.size(), bfp8_stream_grid());
-    std::vector<std::vector<Bfp8TileRef>> per(nwg);
-    {
-        using Load = std::pair<long long, int>;
-        std::priority_queue<Load, std::vector<Load>, std::greater<Load>> heap;
-        for (int w = 0; w < nwg; ++w) heap.push({0LL, w});
-        for (const Bfp8TileRef& tr : order) {
-            Load l = heap.top();
-            heap.pop();
-            per[l.second].push_back(tr);
-            l.first += (long long)bfp8_nblocks(items[tr.desc].K) * 4160;
-            heap.push(l);
-        }
+    // Two persistent launches: the lm_head's tiles, then every other GEMV's
+    // (larger K first).  Workgroup 0 of the second launch merges the lm_head's
+    // top-k partials before its own tiles (the launch boundary makes them
+    // visible); without other GEMVs the stand-alone merge kernel runs instead.
+    std::vector<int> head_idx, rest_idx;
+    for (int i = 0; i < n; ++i) {
+        if (items[i].K > 4096) continue;
+        (items[i].topk > 0 ? head_idx : rest_idx).push_back(i);
     }
-    std::vector<Bfp8TileRef> tiles;
-    std::vector<int> wg_off(1, 0);
-    for (const auto& v : per) {
-        tiles.insert(tiles.end(), v.begin(), v.end());
-        wg_off.push_back((int)tiles.size());
-    }
-    p->ntiles = (int)tiles.size();
-    p->nwg = nwg;
+    std::stable_sort(rest_idx.begin(), rest_idx.end(), [&](int a, int b) { return items[a].K > items[b].K; });
+    const bool fold = p->topk_desc >= 0 && !rest_idx.empty();
+    rc = rc ? rc : deal_tiles(p->head, head_idx, items, 0);
+    rc = rc ? rc : deal_tiles(p->rest, rest_idx, items, fold ? BFP8_MERGE_COST_BLOCKS : 0);
     p->nq = (int)hq.size();
     rc = rc ? rc : p->descs.reserve(p->hdesc.size() * sizeof(Bfp8GemvDesc));
-    rc = rc ? rc : p->tiles.reserve(tiles.size() * sizeof(Bfp8TileRef));
     rc = rc ? rc : p->qdescs.reserve(hq.size() * sizeof(Bfp8QuantDesc));
-    rc = rc ? rc : p->wg_off.reserve(wg_off.size() * sizeof(int));
     if (!rc && (hipMemcpy(p->descs.p, p->hdesc.data(), p->hdesc.size() * sizeof(Bfp8GemvDesc), hipMemcpyHostToDevice) != hipSuccess ||
-                (!tiles.empty() && hipMemcpy(p->tiles.p, tiles.data(), tiles.size() * sizeof(Bfp8TileRef), hipMemcpyHostToDevice) != hipSuccess) ||
-                (!hq.empty() && hipMemcpy(p->qdescs.p, hq.data(), hq.size() * sizeof(Bfp8QuantDesc), hipMemcpyHostToDevice) != hipSuccess) ||
-                hipMemcpy(p->wg_off.p, wg_off.data(), wg_off.size() * sizeof(int), hipMemcpyHostToDevice) != hipSuccess))
+                (!hq.empty() && hipMemcpy(p->qdescs.p, hq.data(), hq.size() * sizeof(Bfp8QuantDesc), hipMemcpyHostToDevice) != hipSuccess)))
         rc = BFP8_EHIP;
     if (rc) {
         set_error("bfp8_plan_create: allocation or upload failed (%d)", rc);
-        p->descs.release(); p->tiles.release(); p->qdescs.release(); p->xq.release();
-        p->xscale.release(); p->xsplit.release(); p->partials.release();
-        p->wg_off.release();
+        release_plan(p);
         delete p;
         return nullptr;
     }
@@ -800,10 +819,13 @@ int bfp8_plan_run_gemv(void* plan, void* stream) {
     Plan* p = static_cast<Plan*>(plan);
     if (!p) return BFP8_EINVAL;
     hipStream_t s = pick_stream(stream);
-    HIP_OK(bfp8_launch_gemv_grouped(p->descs.as<Bfp8GemvDesc>(), p->tiles.as<Bfp8TileRef>(),
-                                    p->wg_off.as<int>(), p->nwg, s));
-    for (const Bfp8GemvDesc& d : p->hdesc)
-        if (d.topk > 0) HIP_OK(bfp8_launch_topk_merge(d, s));
+    const Bfp8GemvDesc* descs = p->descs.as<Bfp8GemvDesc>();
+    HIP_OK(bfp8_launch_gemv_grouped(descs, p->head.tiles.as<Bfp8TileRef>(), p->head.wg_off.as<int>(), p->head.nwg,
+                                    -1, s));
+    const bool fold = p->topk_desc >= 0 && p->rest.nwg > 0;
+    HIP_OK(bfp8_launch_gemv_grouped(descs, p->rest.tiles.as<Bfp8TileRef>(), p->rest.wg_off.as<int>(), p->rest.nwg,
+                                    fold ? p->topk_desc : -1, s));
+    if (p->topk_desc >= 0 && !fold) HIP_OK(bfp8_launch_topk_merge(p->hdesc[p->topk_desc], s));
     for (int i : p->odd_items) {
         const Bfp8GemvDesc& d = p->hdesc[i];
         HIP_OK(bfp8_launch_tail_row(d.y, d.xsplit, d.xscale, d.mant, d.exps, d.M, d.K, s));
@@ -827,9 +849,7 @@ void bfp8_plan_destroy(void* plan) {
         std::lock_guard<std::mutex> lk(g.mu);
         if (g.ready) (void)hipDeviceSynchronize();
     }
-    p->descs.release(); p->tiles.release(); p->qdescs.release(); p->xq.release();
-    p->xscale.release(); p->xsplit.release(); p->partials.release();
-    p->wg_off.release();
+    release_plan(p);
     delete p;
 }
 

@@ -324,7 +324,9 @@ def lm_head_topk(mat: DeviceMatrix, xsplit, xscale, k: int):
 
 
 class SweepPlan:
-    """Grouped GEMV plan: one quantize launch + one grouped GEMV launch per run.
+    """Grouped GEMV plan: per run one quantize launch, then the persistent
+    streaming launches (the lm_head's tiles, then every other GEMV's, whose
+    workgroup 0 also merges the lm_head's top-k).
 
     items: sequence of dicts with keys x (device f32 [K]), mat (DeviceMatrix) and either
     y (device f32 [M]) or topk (int) for the fused lm_head (outputs allocated here).

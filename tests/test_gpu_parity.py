@@ -313,7 +313,7 @@ def test_lm_head_topk_fused(gpu, torch_mod, lm_head_case, k):
     say("lm_head fused top-k", k)
     dm = qk.DeviceMatrix.from_soa(mant, exps)
     _, xs, xsp = qk.quantize(torch.from_numpy(x).cuda())
-    for rep in range(3):  # the last-workgroup counter must reset between launches
+    for rep in range(3):  # repeated launches reuse the partials workspace
         ids, sc, cnt, am = qk.lm_head_topk(dm, xsp, xs, k)
         torch.cuda.synchronize()
         ids_ref, sc_ref = ol.topk(y_ref, k)
@@ -362,6 +362,41 @@ def test_lm_head_small_vocab_and_invalid_arguments(gpu, torch_mod):
     assert kk.lm_head_topk(x, mant, exps, 100, 128, 65)[0].size == 0
     assert kk.lm_head_topk(x, mant, exps, 100, 128, 0)[0].size == 0
     assert kk.lm_head_argmax(x, mant, exps, 99, 128) == -1
+
+
+@pytest.mark.parametrize("shape", ["alone", "with_small_gemv", "ragged_2049_tiles"])
+def test_plan_lm_head_merge_paths(gpu, torch_mod, shape):
+    """A plan's lm_head merge runs as the stand-alone merge kernel (lm_head
+    alone) or folded into workgroup 0 of the second launch (other GEMVs
+    present, here a 2-tile one); a 2049-tile ragged vocabulary takes several
+    passes over the list heads."""
+    qk, torch = gpu, torch_mod
+    V, H, k = {"alone": (16384, 1024, 64), "with_small_gemv": (65536, 1024, 40),
+               "ragged_2049_tiles": (131074, 1024, 40)}[shape]
+    say("plan lm_head", shape, V, H, k)
+    lm = qk.DeviceMatrix.synth(V, H, 777, 122, 128)
+    xl = qk.synth_normal(H, 778)
+    items = [{"mat": lm, "x": torch.from_numpy(xl).cuda(), "topk": k}]
+    small = None
+    if shape != "alone":
+        small = (128, 256, 779)
+        xs = qk.synth_normal(256, 780)
+        items.append({"mat": qk.DeviceMatrix.synth(128, 256, 779, 124, 130), "x": torch.from_numpy(xs).cuda(),
+                      "y": torch.empty(128, dtype=torch.float32, device="cuda")})
+    plan = qk.SweepPlan(items)
+    mant, exps = qk.synth_planes(V, H, 777, 122, 128)
+    y_ref, *_ = ol.gemv_neon(xl, mant, exps)
+    ids_ref, sc_ref = ol.topk(y_ref, k)
+    for rep in range(2):
+        plan.run()
+        torch.cuda.synchronize()
+        ids, sc, cnt = plan.topk_out
+        assert int(cnt[0].item()) == k and int(cnt[1].item()) == ol.argmax(y_ref), rep
+        assert np.array_equal(ids.cpu().numpy(), ids_ref) and same_f32(sc.cpu().numpy(), sc_ref), rep
+        if small:
+            sm, se = qk.synth_planes(128, 256, 779, 124, 130)
+            assert same_f32(items[1]["y"].cpu().numpy(), ol.gemv_neon(xs, sm, se)[0])
+    plan.close()
 
 
 # ---- batch and sweep ---------------------------------------------------------------------------------
