@@ -7,10 +7,15 @@ weight sweep at batch 1 -- per layer gate 3584x1024, up 3584x1024, down
 the 65536x1024 lm_head with fused greedy argmax + top-40.  Mantissas uniform
 in [-127, 127], exponents uniform in [124, 130] ([122, 128] for the lm_head),
 a fresh N(0,1) activation per GEMV (silu(a)*b with 1% +-20 outliers for the
-down projection).  One step = quantize every activation (one launch) + one
-grouped GEMV launch over all 121 GEMVs and the lm_head, weights resident in
-HBM.  Weight copies rotate (2 sweeps = 1.08 GB) so the 256 MB Infinity Cache
-cannot serve repeats.
+down projection).  One step = quantize every activation (one launch) + two
+persistent streaming launches (the lm_head's 1024 tiles, then the other 120
+GEMVs' tiles, whose workgroup 0 first merges the lm_head top-k), weights
+resident in HBM.  Weight copies rotate (2 sweeps = 1.08 GB) so the 256 MB
+Infinity Cache cannot serve repeats.
+
+roofline: the launch that moves the most bytes (the 120-GEMV launch for the
+sweep), timed alone with HIP events on its stream; its algorithmic bytes =
+weights + int16 activations (2 B/element) + f32 block scales + f32 outputs.
 
 value = algorithmic bytes per sweep (weights once + f32 x in + f32 y out; the
 fused lm_head writes no logits) / wall time per step, in GB/s.
@@ -78,12 +83,14 @@ def kernel_bytes(items):
     return sum(wbytes(M, K) + 2 * K + 4 * (K // 64) + (0 if tk else 4 * M) for _, M, K, _, _, tk in items)
 
 
-def read_traffic(workload):
-    """HBM bytes per dispatch from the committed rocprofv3 PMC summary, if any."""
-    p = ROOT / "profiles" / f"{workload}_gemv_pmc.md"
+def read_traffic(workload, kernel):
+    """HBM bytes per dispatch of `kernel` from the committed rocprofv3 PMC
+    summary of this workload, if any (a line `traffic_bytes_per_dispatch
+    <kernel>: <bytes>`)."""
+    p = ROOT / "profiles" / f"{workload}_pmc.md"
     if not p.exists():
         return None
-    m = re.search(r"traffic_bytes_per_dispatch:\s*([0-9.]+)", p.read_text())
+    m = re.search(r"traffic_bytes_per_dispatch " + re.escape(kernel) + r":\s*([0-9.]+)", p.read_text())
     return float(m.group(1)) if m else None
 
 
@@ -121,12 +128,13 @@ def cpu_baseline(items, seconds=10.0):
             fn(y.ctypes.data, x.ctypes.data, mant.ctypes.data, exps.ctypes.data, M, K)
         sweeps += 1
         el = time.perf_counter() - t0
-        if el >= seconds or sweeps >= 200:
+        if el >= seconds:
             break
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count()
     return {"value": round(nbytes * sweeps / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
-            "sample": f"{sweeps} x the same GEMV list on host planes ({nbytes / 1e6:.1f} MB per pass), "
-                      f"float path with OpenMP over rows, {el:.1f} s"}
+            "sample": f"{sweeps} passes over the same GEMV list ({len(items)} GEMVs, {nbytes / 1e6:.1f} MB per pass; "
+                      f"the lm_head as a plain GEMV, the reference having no fused BFP8 lm_head), host float path "
+                      f"with OpenMP over rows, {el:.1f} s"}
 
 
 def main():
@@ -193,31 +201,48 @@ def main():
     value = mbytes / (ms_per_step * 1e-3) / 1e9
     print(f"[bench] timed {args.steps} steps: {ms_per_step * 1e3:.1f} us/step", file=sys.stderr, flush=True)
 
-    # dominant kernel: the grouped GEMV launch alone, HIP events on its stream
+    # each GEMV launch alone, HIP events on the stream it is launched on:
+    # stage 0 streams the lm_head's tiles, stage 1 every other GEMV's (its
+    # workgroup 0 also merges the lm_head top-k; with no other GEMV, stage 1
+    # is the stand-alone merge kernel)
     stream = torch.cuda.current_stream()
-    evs = []
-    for i in range(args.steps):
+    head = [it for it in items if it[5]]
+    rest = [it for it in items if not it[5]]
+    stages = []
+    for stage, its in ((0, head), (1, rest)):
+        if stage == 0 and not head:
+            continue
+        # `steps` back-to-back launches of this stage between one event pair
+        # (rotating weight copies): per-launch time without the dispatch
+        # latency of an isolated launch, as the kernel trace measures it
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        for i in range(2):
+            plans[i % copies].launch(stage)
         a.record(stream)
-        plans[i % copies].run_gemv()
+        for i in range(args.steps):
+            plans[i % copies].launch(stage)
         b.record(stream)
-        evs.append((a, b))
-    torch.cuda.synchronize()
-    kus = [a.elapsed_time(b) * 1e3 for a, b in evs]
-    kernel_us = float(np.mean(kus))
-    kbytes = kernel_bytes(items)
-    achieved = kbytes / (kernel_us * 1e-6) / 1e9
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / args.steps
+        if stage == 0:
+            name = "bfp8_gemv_grouped_kernel"
+        elif not rest:
+            name = "bfp8_topk_merge_kernel"
+        else:
+            name = "bfp8_gemv_grouped_merge_kernel" if head else "bfp8_gemv_grouped_kernel"
+        stages.append({"stage": stage, "name": name, "avg_us": us, "bytes": kernel_bytes(its)})
+    dom = max(stages, key=lambda st: st["bytes"])
+    kernel_us = dom["avg_us"]
+    achieved = dom["bytes"] / (kernel_us * 1e-6) / 1e9
 
-    # quantize launch alone
-    qev = []
-    for i in range(min(args.steps, 20)):
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(stream)
+    # quantize launch alone (back-to-back, like the stages)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for i in range(args.steps):
         plans[i % copies].quantize()
-        b.record(stream)
-        qev.append((a, b))
+    b.record(stream)
     torch.cuda.synchronize()
-    quant_us = float(np.mean([a.elapsed_time(b) * 1e3 for a, b in qev]))
+    quant_us = a.elapsed_time(b) * 1e3 / args.steps
 
     # measured read-only ceiling over 1 GiB, and a copy of known size (the
     # PMC counter calibration kernel)
@@ -240,7 +265,7 @@ def main():
     torch.cuda.synchronize()
     del buf, cpy
 
-    traffic = read_traffic(args.workload)
+    traffic = read_traffic(args.workload, dom["name"])
     result = {
         "metric": "BFP8 GEMV achieved HBM GB/s (% of peak); us per 24-layer decode sweep",
         "value": round(value, 2),
@@ -259,8 +284,10 @@ def main():
                    "rotating_copies": copies, "parallelism": "single GPU"},
         "us_per_step": round(ms_per_step * 1e3, 2),
         "pct_of_peak": round(100 * value / PEAK_HBM_GBPS, 2),
-        "kernel": {"name": "bfp8_gemv_grouped_kernel", "avg_us": round(kernel_us, 2),
-                   "min_us": round(min(kus), 2), "quantize_avg_us": round(quant_us, 2)},
+        "kernel": {"name": dom["name"], "stage": dom["stage"], "avg_us": round(kernel_us, 2),
+                   "algorithmic_bytes": dom["bytes"]},
+        "launches_us": {f"stage{st['stage']}:{st['name']}": round(st["avg_us"], 2) for st in stages}
+                       | {"quantize": round(quant_us, 2)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": traffic},
         "hbm_read_ceiling_GBps": round(ceiling, 1),

@@ -147,10 +147,11 @@ int bfp8_dev_lm_head_topk(int* out_ids, float* out_scores, int* out_count, int* 
                           const uint8_t* exps_gpu, int vocab, int hidden, int k, void* stream);
 
 /* A sweep plan: many independent GEMVs (and at most one fused lm_head)
- * executed as one quantize launch plus one grouped GEMV launch.  Item i reads
- * x (device, K floats) and writes y (device, M floats), or, for the lm_head
- * item (topk > 0), the four top-k outputs.  Tiles of larger K are issued
- * first; the lm_head's tiles lead so that its final merge overlaps the rest. */
+ * executed as one quantize launch plus two persistent streaming launches:
+ * the lm_head's tiles, then every other GEMV's (larger K first), whose
+ * workgroup 0 first merges the lm_head's per-tile top-k partials.  Item i
+ * reads x (device, K floats) and writes y (device, M floats), or, for the
+ * lm_head item (topk > 0), the four top-k outputs. */
 typedef struct bfp8_plan_item {
     const float* x;
     float* y;
@@ -167,9 +168,14 @@ typedef struct bfp8_plan_item {
 
 void* bfp8_plan_create(const bfp8_plan_item* items, int n);
 int bfp8_plan_run(void* plan, void* stream);
-/* Only the grouped GEMV launch (activations already quantized by a previous
+/* Only the GEMV launches (activations already quantized by a previous
  * bfp8_plan_run or bfp8_plan_quantize). */
 int bfp8_plan_run_gemv(void* plan, void* stream);
+/* One stage of bfp8_plan_run_gemv, for timing each launch on its own:
+ * 0 = the lm_head's tiles, 1 = the other GEMVs' tiles with the top-k merge
+ * (or the stand-alone merge kernel when the plan has no other GEMV),
+ * 2 = odd-row tails and K > 4096 items.  Stages must run in this order. */
+int bfp8_plan_launch(void* plan, int stage, void* stream);
 int bfp8_plan_quantize(void* plan, void* stream);
 void bfp8_plan_destroy(void* plan);
 

@@ -510,13 +510,22 @@ __global__ __launch_bounds__(256) void bfp8_gemv_kernel(Bfp8GemvDesc d) {
 }
 
 // Grouped GEMV, persistent: workgroup w walks tiles[wg_off[w] .. wg_off[w+1]).
-// With merge_desc >= 0, workgroup 0 first merges that descriptor's top-k
-// partials, written by an earlier launch on the stream.
 extern "C" __global__ __launch_bounds__(256) void bfp8_gemv_grouped_kernel(
+    const Bfp8GemvDesc* __restrict__ descs, const Bfp8TileRef* __restrict__ tiles,
+    const int* __restrict__ wg_off) {
+    __shared__ StreamLds L;
+    const int beg = wg_off[blockIdx.x];
+    TableTiles src{descs, tiles, beg, wg_off[blockIdx.x + 1] - beg};
+    stream_tiles<false>(src, L);
+}
+
+// The same, with workgroup 0 first merging descs[merge_desc]'s top-k
+// partials, written by an earlier launch on the stream.
+extern "C" __global__ __launch_bounds__(256) void bfp8_gemv_grouped_merge_kernel(
     const Bfp8GemvDesc* __restrict__ descs, const Bfp8TileRef* __restrict__ tiles,
     const int* __restrict__ wg_off, int merge_desc) {
     __shared__ StreamLds L;
-    if (merge_desc >= 0 && blockIdx.x == 0) topk_merge_folded(topk_args(descs[merge_desc]), L.merge);
+    if (blockIdx.x == 0) topk_merge_folded(topk_args(descs[merge_desc]), L.merge);
     const int beg = wg_off[blockIdx.x];
     TableTiles src{descs, tiles, beg, wg_off[blockIdx.x + 1] - beg};
     stream_tiles<false>(src, L);
@@ -622,8 +631,9 @@ static int resident_grid(const void* kernel) {
 }
 
 int bfp8_stream_grid() {
-    static const int grid = resident_grid(reinterpret_cast<const void*>(bfp8_gemv_grouped_kernel));
-    return grid;
+    static const int a = resident_grid(reinterpret_cast<const void*>(bfp8_gemv_grouped_kernel));
+    static const int b = resident_grid(reinterpret_cast<const void*>(bfp8_gemv_grouped_merge_kernel));
+    return a < b ? a : b;
 }
 
 hipError_t bfp8_launch_gemv(const Bfp8GemvDesc& d, hipStream_t s) {
@@ -650,8 +660,12 @@ hipError_t bfp8_launch_topk_merge(const Bfp8GemvDesc& d, hipStream_t s) {
 hipError_t bfp8_launch_gemv_grouped(const Bfp8GemvDesc* descs_dev, const Bfp8TileRef* tiles_dev,
                                     const int* wg_off_dev, int nwg, int merge_desc, hipStream_t s) {
     if (nwg <= 0) return hipSuccess;
-    hipLaunchKernelGGL(bfp8_gemv_grouped_kernel, dim3(nwg), dim3(256), 0, s, descs_dev, tiles_dev,
-                       wg_off_dev, merge_desc);
+    if (merge_desc >= 0)
+        hipLaunchKernelGGL(bfp8_gemv_grouped_merge_kernel, dim3(nwg), dim3(256), 0, s, descs_dev, tiles_dev,
+                           wg_off_dev, merge_desc);
+    else
+        hipLaunchKernelGGL(bfp8_gemv_grouped_kernel, dim3(nwg), dim3(256), 0, s, descs_dev, tiles_dev,
+                           wg_off_dev);
     return hipGetLastError();
 }
 

@@ -815,26 +815,36 @@ int bfp8_plan_quantize(void* plan, void* stream) {
     return BFP8_OK;
 }
 
-int bfp8_plan_run_gemv(void* plan, void* stream) {
+int bfp8_plan_launch(void* plan, int stage, void* stream) {
     Plan* p = static_cast<Plan*>(plan);
-    if (!p) return BFP8_EINVAL;
+    if (!p || stage < 0 || stage > 2) return BFP8_EINVAL;
     hipStream_t s = pick_stream(stream);
     const Bfp8GemvDesc* descs = p->descs.as<Bfp8GemvDesc>();
-    HIP_OK(bfp8_launch_gemv_grouped(descs, p->head.tiles.as<Bfp8TileRef>(), p->head.wg_off.as<int>(), p->head.nwg,
-                                    -1, s));
     const bool fold = p->topk_desc >= 0 && p->rest.nwg > 0;
-    HIP_OK(bfp8_launch_gemv_grouped(descs, p->rest.tiles.as<Bfp8TileRef>(), p->rest.wg_off.as<int>(), p->rest.nwg,
-                                    fold ? p->topk_desc : -1, s));
-    if (p->topk_desc >= 0 && !fold) HIP_OK(bfp8_launch_topk_merge(p->hdesc[p->topk_desc], s));
-    for (int i : p->odd_items) {
-        const Bfp8GemvDesc& d = p->hdesc[i];
-        HIP_OK(bfp8_launch_tail_row(d.y, d.xsplit, d.xscale, d.mant, d.exps, d.M, d.K, s));
-    }
-    for (int i : p->float_items) {
-        const bfp8_plan_item& it = p->items[i];
-        HIP_OK(bfp8_launch_gemv_float(it.y, it.x, (const uint8_t*)it.mant_gpu, it.exps_gpu, it.M, it.K, s));
+    if (stage == 0) {
+        HIP_OK(bfp8_launch_gemv_grouped(descs, p->head.tiles.as<Bfp8TileRef>(), p->head.wg_off.as<int>(),
+                                        p->head.nwg, -1, s));
+    } else if (stage == 1) {
+        HIP_OK(bfp8_launch_gemv_grouped(descs, p->rest.tiles.as<Bfp8TileRef>(), p->rest.wg_off.as<int>(),
+                                        p->rest.nwg, fold ? p->topk_desc : -1, s));
+        if (p->topk_desc >= 0 && !fold) HIP_OK(bfp8_launch_topk_merge(p->hdesc[p->topk_desc], s));
+    } else {
+        for (int i : p->odd_items) {
+            const Bfp8GemvDesc& d = p->hdesc[i];
+            HIP_OK(bfp8_launch_tail_row(d.y, d.xsplit, d.xscale, d.mant, d.exps, d.M, d.K, s));
+        }
+        for (int i : p->float_items) {
+            const bfp8_plan_item& it = p->items[i];
+            HIP_OK(bfp8_launch_gemv_float(it.y, it.x, (const uint8_t*)it.mant_gpu, it.exps_gpu, it.M, it.K, s));
+        }
     }
     return BFP8_OK;
+}
+
+int bfp8_plan_run_gemv(void* plan, void* stream) {
+    int rc = BFP8_OK;
+    for (int stage = 0; stage < 3 && !rc; ++stage) rc = bfp8_plan_launch(plan, stage, stream);
+    return rc;
 }
 
 int bfp8_plan_run(void* plan, void* stream) {

@@ -97,6 +97,8 @@ def bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     for name in ("bfp8_plan_run", "bfp8_plan_run_gemv", "bfp8_plan_quantize"):
         getattr(lib, name).argtypes = [vp, vp]
         getattr(lib, name).restype = i
+    lib.bfp8_plan_launch.argtypes = [vp, i, vp]
+    lib.bfp8_plan_launch.restype = i
     lib.bfp8_plan_destroy.argtypes = [vp]
     lib.bfp8_plan_destroy.restype = None
     lib.bfp8_synth_planes_host.argtypes = [vp, vp, i, i, c_uint64, i, i]
@@ -365,6 +367,10 @@ class SweepPlan:
 
     def run_gemv(self):
         check(load().bfp8_plan_run_gemv(self.handle, _stream()), "plan_run_gemv")
+
+    def launch(self, stage):
+        """One GEMV stage: 0 lm_head tiles, 1 other tiles + merge, 2 tails."""
+        check(load().bfp8_plan_launch(self.handle, stage, _stream()), "plan_launch")
 
     def close(self):
         if self.handle:
