@@ -210,7 +210,8 @@ def main():
     rest = [it for it in items if not it[5]]
     stages = []
     for stage, its in ((0, head), (1, rest)):
-        if stage == 0 and not head:
+        name = plans[0].kernel_name(stage)
+        if not name:
             continue
         # `steps` back-to-back launches of this stage between one event pair
         # (rotating weight copies): per-launch time without the dispatch
@@ -224,13 +225,8 @@ def main():
         b.record(stream)
         torch.cuda.synchronize()
         us = a.elapsed_time(b) * 1e3 / args.steps
-        if stage == 0:
-            name = "bfp8_gemv_grouped_kernel"
-        elif not rest:
-            name = "bfp8_topk_merge_kernel"
-        else:
-            name = "bfp8_gemv_grouped_merge_kernel" if head else "bfp8_gemv_grouped_kernel"
-        stages.append({"stage": stage, "name": name, "avg_us": us, "bytes": kernel_bytes(its)})
+        stages.append({"stage": stage, "name": name, "avg_us": us,
+                       "bytes": kernel_bytes(its) if name != "bfp8_topk_merge_kernel" else 0})
     dom = max(stages, key=lambda st: st["bytes"])
     kernel_us = dom["avg_us"]
     achieved = dom["bytes"] / (kernel_us * 1e-6) / 1e9

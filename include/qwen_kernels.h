@@ -147,11 +147,12 @@ int bfp8_dev_lm_head_topk(int* out_ids, float* out_scores, int* out_count, int* 
                           const uint8_t* exps_gpu, int vocab, int hidden, int k, void* stream);
 
 /* A sweep plan: many independent GEMVs (and at most one fused lm_head)
- * executed as one quantize launch plus two persistent streaming launches:
- * the lm_head's tiles, then every other GEMV's (larger K first), whose
- * workgroup 0 first merges the lm_head's per-tile top-k partials.  Item i
- * reads x (device, K floats) and writes y (device, M floats), or, for the
- * lm_head item (topk > 0), the four top-k outputs. */
+ * executed as one quantize launch plus two streaming launches: the lm_head's
+ * tiles, then every other GEMV's (larger K first), whose workgroup 0 first
+ * merges the lm_head's per-tile top-k partials.  A plan without an lm_head
+ * and with few row tiles runs its GEMVs one tile per 16-wavefront workgroup.
+ * Item i reads x (device, K floats) and writes y (device, M floats), or, for
+ * the lm_head item (topk > 0), the four top-k outputs. */
 typedef struct bfp8_plan_item {
     const float* x;
     float* y;
@@ -176,6 +177,8 @@ int bfp8_plan_run_gemv(void* plan, void* stream);
  * (or the stand-alone merge kernel when the plan has no other GEMV),
  * 2 = odd-row tails and K > 4096 items.  Stages must run in this order. */
 int bfp8_plan_launch(void* plan, int stage, void* stream);
+/* Name of the (main) kernel a stage launches, "" if the stage is empty. */
+const char* bfp8_plan_kernel_name(void* plan, int stage);
 int bfp8_plan_quantize(void* plan, void* stream);
 void bfp8_plan_destroy(void* plan);
 

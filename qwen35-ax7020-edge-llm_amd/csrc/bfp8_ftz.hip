@@ -498,6 +498,96 @@ __device__ __forceinline__ void stream_tiles(const Src& src, StreamLds& L) {
     }
 }
 
+// ---- one tile per workgroup, K split across wavefronts (small M) ------------------
+// A lone GEMV of a few thousand rows has too few 64-row tiles to keep the chip
+// busy with one 4-wavefront workgroup per tile.  Here 16 wavefronts own a
+// tile: wavefront (q, s) computes residue q of the 64 rows over block slice s
+// and issues all of that slice's loads before any arithmetic, so the whole
+// tile is in flight at once.  The per-block term t2 = (float(S) * 2^(e-134))
+// * xscale is formed independently per block (the same two roundings as the
+// streaming kernel); the reference's order is kept by adding the terms per
+// (row, q) in block order: slice 0 adds its own as it forms them, slices 1..3
+// leave theirs in LDS.
+constexpr int kWideWaves = 16;
+constexpr int kWideSlices = kWideWaves / 4;
+constexpr int kWideMaxPer = 16;  // blocks per slice (K <= 4096)
+
+__host__ __device__ __forceinline__ int wide_per(int nb) { return (nb + kWideSlices - 1) / kWideSlices; }
+
+template <bool kLanes>
+__device__ __forceinline__ void wide_tile(const Bfp8GemvDesc& d, int t, float* terms, float (*red)[64]) {
+    const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int r = threadIdx.x & 63;
+    const int q = w & 3, sl = w >> 2;
+    const int nb = d.K >> 6, nb4 = (nb + 3) >> 2;
+    const int per = wide_per(nb);
+    const int b0 = sl * per;
+    const int cnt = max(0, min(per, nb - b0));
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(d.mant + (size_t)t * nb * 4096u, (uint32_t)nb * 4096u);
+    const __amdgpu_buffer_rsrc_t ers = make_rsrc(d.exps + (size_t)t * nb4 * 256u, (uint32_t)nb4 * 256u);
+    const int voff = q * 1024 + r * 16;
+    u32x4 wv[kWideMaxPer];
+    uint32_t ev[kWideMaxPer];
+#pragma unroll
+    for (int u = 0; u < kWideMaxPer; ++u) {
+        if (u < cnt) {
+            const int b = b0 + u;
+            wv[u] = load_w(wrs, voff, b * 4096);
+            ev[u] = load_e(ers, r * 4, (b >> 2) * 256);
+        }
+    }
+    // The slice's split activation and scales, fetched with the weights by
+    // vector loads (a cold scalar cache would serialise one round trip per
+    // block): lane l holds word (l & 7) of block b0 + (l >> 3) (+ 8 in xb) and
+    // the scale of block b0 + l; v_readlane broadcasts them as SGPR operands.
+    const int xj = r >> 3, xw = r & 7;
+    const uint32_t xa = xj < cnt ? d.xsplit[((b0 + xj) * 4 + q) * 8 + xw] : 0u;
+    const uint32_t xb = xj + 8 < cnt ? d.xsplit[((b0 + xj + 8) * 4 + q) * 8 + xw] : 0u;
+    const float xsv = r < cnt ? d.xscale[b0 + r] : 0.0f;
+    const int row = t * BFP8_TILE_ROWS + r;
+    int32_t* lanes_row = (kLanes && d.lanes && row < d.M) ? d.lanes + (size_t)row * nb * 4 : nullptr;
+    float fs = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kWideMaxPer; ++u) {
+        if (u < cnt) {
+            const int b = b0 + u;
+            const uint32_t src = u < 8 ? xa : xb;
+            uint32_t x[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) x[k] = __builtin_amdgcn_readlane(src, (u & 7) * 8 + k);
+            const u32x4 w = wv[u];
+            int S = __builtin_amdgcn_sdot4((int)w.x, (int)x[0], 0, false);
+            S = __builtin_amdgcn_sdot4((int)w.y, (int)x[1], S, false);
+            S = __builtin_amdgcn_sdot4((int)w.z, (int)x[2], S, false);
+            S = __builtin_amdgcn_sdot4((int)w.w, (int)x[3], S, false);
+            S = (int)((uint32_t)S << 8);
+            S = __builtin_amdgcn_sdot4((int)w.x, (int)x[4], S, false);
+            S = __builtin_amdgcn_sdot4((int)w.y, (int)x[5], S, false);
+            S = __builtin_amdgcn_sdot4((int)w.z, (int)x[6], S, false);
+            S = __builtin_amdgcn_sdot4((int)w.w, (int)x[7], S, false);
+            if (kLanes && lanes_row) lanes_row[b * 4 + q] = S;
+            const uint32_t e = (ev[u] >> (8 * (b & 3))) & 0xffu;
+            const float t1 = (float)S * exp_scale_ftz(e);
+            const float t2 = t1 * __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(uint32_t, xsv), u));
+            if (sl == 0)
+                fs = fs + t2;
+            else
+                terms[((b - per) * 4 + q) * 64 + r] = t2;
+        }
+    }
+    __syncthreads();
+    if (sl == 0) {
+        for (int b = per; b < nb; ++b) fs = fs + terms[((b - per) * 4 + q) * 64 + r];
+        red[q][r] = fs;
+    }
+    __syncthreads();
+    if (w == 0) {
+        // vadd_f32(low, high) then vpadd_f32: y = (fs0 + fs2) + (fs1 + fs3)
+        const float y = (red[0][r] + red[2][r]) + (red[1][r] + red[3][r]);
+        if (d.y && row < d.pair_rows) d.y[row] = y;
+    }
+}
+
 }  // namespace
 
 // Single GEMV, persistent: workgroup w takes tiles w, w + gridDim, ...
@@ -529,6 +619,24 @@ extern "C" __global__ __launch_bounds__(256) void bfp8_gemv_grouped_merge_kernel
     const int beg = wg_off[blockIdx.x];
     TableTiles src{descs, tiles, beg, wg_off[blockIdx.x + 1] - beg};
     stream_tiles<false>(src, L);
+}
+
+// Small-M GEMV: one tile per workgroup of 16 wavefronts (dynamic LDS: the
+// terms of blocks wide_per(nb) .. nb-1).
+template <bool kLanes>
+__global__ __launch_bounds__(kWideWaves * 64) void bfp8_gemv_wide_kernel(Bfp8GemvDesc d) {
+    extern __shared__ float wide_terms[];
+    __shared__ float red[4][64];
+    wide_tile<kLanes>(d, blockIdx.x, wide_terms, red);
+}
+
+// The same over a tile table spanning several GEMVs (small plans).
+extern "C" __global__ __launch_bounds__(kWideWaves * 64) void bfp8_gemv_wide_grouped_kernel(
+    const Bfp8GemvDesc* __restrict__ descs, const Bfp8TileRef* __restrict__ tiles) {
+    extern __shared__ float wide_terms[];
+    __shared__ float red[4][64];
+    const Bfp8TileRef tr = tiles[blockIdx.x];
+    wide_tile<false>(descs[tr.desc], tr.tile, wide_terms, red);
 }
 
 // Stand-alone final top-k merge (one workgroup of 16 wavefronts).
@@ -636,9 +744,22 @@ int bfp8_stream_grid() {
     return a < b ? a : b;
 }
 
+static size_t wide_lds_bytes(int max_nb) {
+    const int rest = max_nb - wide_per(max_nb);
+    return (size_t)(rest > 0 ? rest : 1) * 4 * 64 * sizeof(float);
+}
+
 hipError_t bfp8_launch_gemv(const Bfp8GemvDesc& d, hipStream_t s) {
     const int nt = bfp8_ntiles(d.M);
     if (nt == 0) return hipSuccess;
+    if (d.topk <= 0 && nt <= BFP8_WIDE_MAX_TILES) {
+        const size_t lds = wide_lds_bytes(d.K >> 6);
+        if (d.lanes)
+            hipLaunchKernelGGL(bfp8_gemv_wide_kernel<true>, dim3(nt), dim3(kWideWaves * 64), lds, s, d);
+        else
+            hipLaunchKernelGGL(bfp8_gemv_wide_kernel<false>, dim3(nt), dim3(kWideWaves * 64), lds, s, d);
+        return hipGetLastError();
+    }
     static const int g_plain = resident_grid(reinterpret_cast<const void*>(bfp8_gemv_kernel<false>));
     static const int g_lanes = resident_grid(reinterpret_cast<const void*>(bfp8_gemv_kernel<true>));
     const int cap = d.lanes ? g_lanes : g_plain;
@@ -666,6 +787,14 @@ hipError_t bfp8_launch_gemv_grouped(const Bfp8GemvDesc* descs_dev, const Bfp8Til
     else
         hipLaunchKernelGGL(bfp8_gemv_grouped_kernel, dim3(nwg), dim3(256), 0, s, descs_dev, tiles_dev,
                            wg_off_dev);
+    return hipGetLastError();
+}
+
+hipError_t bfp8_launch_gemv_wide_grouped(const Bfp8GemvDesc* descs_dev, const Bfp8TileRef* tiles_dev, int ntiles,
+                                         int max_nb, hipStream_t s) {
+    if (ntiles <= 0) return hipSuccess;
+    hipLaunchKernelGGL(bfp8_gemv_wide_grouped_kernel, dim3(ntiles), dim3(kWideWaves * 64), wide_lds_bytes(max_nb), s,
+                       descs_dev, tiles_dev);
     return hipGetLastError();
 }
 

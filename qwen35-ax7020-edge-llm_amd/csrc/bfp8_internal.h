@@ -53,10 +53,21 @@ struct Bfp8TileRef {
 #define BFP8_TOPK_MAX 64
 #define BFP8_TOPK_MAX_TILES 4096
 #define BFP8_STREAM_WG_PER_CU 4
+// Row tiles up to which a GEMV (or a plan's GEMVs) runs one tile per
+// 16-wavefront workgroup instead of the persistent streaming kernel.
+#ifndef BFP8_WIDE_MAX_TILES
+#define BFP8_WIDE_MAX_TILES 384
+#endif
 
 // ---- bfp8_ftz.hip --------------------------------------------------------
-// Single GEMV (for topk > 0 followed by the stand-alone merge kernel).
+// Single GEMV: up to BFP8_WIDE_MAX_TILES row tiles one tile per 16-wavefront
+// workgroup, else the persistent streaming kernel (for topk > 0 always, then
+// followed by the stand-alone merge kernel).
 hipError_t bfp8_launch_gemv(const Bfp8GemvDesc& d, hipStream_t s);
+// One tile per 16-wavefront workgroup over a tile table (small plans);
+// max_nb = the largest K/64 among the table's GEMVs.
+hipError_t bfp8_launch_gemv_wide_grouped(const Bfp8GemvDesc* descs_dev, const Bfp8TileRef* tiles_dev, int ntiles,
+                                         int max_nb, hipStream_t s);
 // Stand-alone final top-k merge of partials an earlier launch wrote.
 hipError_t bfp8_launch_topk_merge(const Bfp8GemvDesc& d, hipStream_t s);
 // Persistent grouped launch: workgroup w walks tiles_dev[wg_off_dev[w] ..

@@ -640,10 +640,13 @@ int bfp8_dev_copy_probe(void* dst, const void* src, size_t bytes, void* stream) 
 // =========================== plans ================================================
 namespace {
 
-// One persistent grouped launch: its dealt tile table.
+// One grouped launch: its tile table, either dealt over a persistent grid
+// (wg_off per workgroup) or one tile per 16-wavefront workgroup (wide).
 struct Launch {
     DevBuf tiles, wg_off;
     int nwg = 0;
+    bool wide = false;
+    int ntiles = 0, max_nb = 0;
 };
 
 struct Plan {
@@ -661,11 +664,21 @@ struct Plan {
 // workgroups, longest first onto the least-loaded workgroup (bytes), and
 // uploads the table.  `wg0_extra` blocks of load are pre-charged to
 // workgroup 0 (a folded merge).
-int deal_tiles(Launch& L, const std::vector<int>& idx, const bfp8_plan_item* items, int wg0_extra) {
+int deal_tiles(Launch& L, const std::vector<int>& idx, const bfp8_plan_item* items, int wg0_extra, bool allow_wide) {
     std::vector<Bfp8TileRef> order;
-    for (int i : idx)
+    for (int i : idx) {
         for (int t = 0; t < bfp8_ntiles(items[i].M); ++t) order.push_back(Bfp8TileRef{i, t});
+        L.max_nb = std::max(L.max_nb, bfp8_nblocks(items[i].K));
+    }
     if (order.empty()) return BFP8_OK;
+    L.ntiles = (int)order.size();
+    if (allow_wide && L.ntiles <= BFP8_WIDE_MAX_TILES) {
+        L.wide = true;
+        int rc;
+        if ((rc = L.tiles.reserve(order.size() * sizeof(Bfp8TileRef)))) return rc;
+        HIP_OK(hipMemcpy(L.tiles.p, order.data(), order.size() * sizeof(Bfp8TileRef), hipMemcpyHostToDevice));
+        return BFP8_OK;
+    }
     const int nwg = std::min<int>((int)order.size(), bfp8_stream_grid());
     std::vector<std::vector<Bfp8TileRef>> per(nwg);
     using Load = std::pair<long long, int>;
@@ -791,8 +804,8 @@ void* bfp8_plan_create(const bfp8_plan_item* items, int n) {
     }
     std::stable_sort(rest_idx.begin(), rest_idx.end(), [&](int a, int b) { return items[a].K > items[b].K; });
     const bool fold = p->topk_desc >= 0 && !rest_idx.empty();
-    rc = rc ? rc : deal_tiles(p->head, head_idx, items, 0);
-    rc = rc ? rc : deal_tiles(p->rest, rest_idx, items, fold ? BFP8_MERGE_COST_BLOCKS : 0);
+    rc = rc ? rc : deal_tiles(p->head, head_idx, items, 0, false);
+    rc = rc ? rc : deal_tiles(p->rest, rest_idx, items, fold ? BFP8_MERGE_COST_BLOCKS : 0, !fold);
     p->nq = (int)hq.size();
     rc = rc ? rc : p->descs.reserve(p->hdesc.size() * sizeof(Bfp8GemvDesc));
     rc = rc ? rc : p->qdescs.reserve(hq.size() * sizeof(Bfp8QuantDesc));
@@ -825,8 +838,12 @@ int bfp8_plan_launch(void* plan, int stage, void* stream) {
         HIP_OK(bfp8_launch_gemv_grouped(descs, p->head.tiles.as<Bfp8TileRef>(), p->head.wg_off.as<int>(),
                                         p->head.nwg, -1, s));
     } else if (stage == 1) {
-        HIP_OK(bfp8_launch_gemv_grouped(descs, p->rest.tiles.as<Bfp8TileRef>(), p->rest.wg_off.as<int>(),
-                                        p->rest.nwg, fold ? p->topk_desc : -1, s));
+        if (p->rest.wide)
+            HIP_OK(bfp8_launch_gemv_wide_grouped(descs, p->rest.tiles.as<Bfp8TileRef>(), p->rest.ntiles,
+                                                 p->rest.max_nb, s));
+        else
+            HIP_OK(bfp8_launch_gemv_grouped(descs, p->rest.tiles.as<Bfp8TileRef>(), p->rest.wg_off.as<int>(),
+                                            p->rest.nwg, fold ? p->topk_desc : -1, s));
         if (p->topk_desc >= 0 && !fold) HIP_OK(bfp8_launch_topk_merge(p->hdesc[p->topk_desc], s));
     } else {
         for (int i : p->odd_items) {
@@ -839,6 +856,24 @@ int bfp8_plan_launch(void* plan, int stage, void* stream) {
         }
     }
     return BFP8_OK;
+}
+
+const char* bfp8_plan_kernel_name(void* plan, int stage) {
+    const Plan* p = static_cast<const Plan*>(plan);
+    if (!p) return "";
+    const bool fold = p->topk_desc >= 0 && p->rest.nwg > 0;
+    if (stage == 0) return p->head.nwg > 0 ? "bfp8_gemv_grouped_kernel" : "";
+    if (stage == 1) {
+        if (p->rest.wide) return "bfp8_gemv_wide_grouped_kernel";
+        if (fold) return "bfp8_gemv_grouped_merge_kernel";
+        if (p->rest.nwg > 0) return "bfp8_gemv_grouped_kernel";
+        return p->topk_desc >= 0 ? "bfp8_topk_merge_kernel" : "";
+    }
+    if (stage == 2) {
+        if (!p->odd_items.empty()) return "bfp8_tail_row_kernel";
+        return p->float_items.empty() ? "" : "bfp8_gemv_float_kernel";
+    }
+    return "";
 }
 
 int bfp8_plan_run_gemv(void* plan, void* stream) {

@@ -99,6 +99,8 @@ def bind(lib: ctypes.CDLL) -> ctypes.CDLL:
         getattr(lib, name).restype = i
     lib.bfp8_plan_launch.argtypes = [vp, i, vp]
     lib.bfp8_plan_launch.restype = i
+    lib.bfp8_plan_kernel_name.argtypes = [vp, i]
+    lib.bfp8_plan_kernel_name.restype = ctypes.c_char_p
     lib.bfp8_plan_destroy.argtypes = [vp]
     lib.bfp8_plan_destroy.restype = None
     lib.bfp8_synth_planes_host.argtypes = [vp, vp, i, i, c_uint64, i, i]
@@ -367,6 +369,10 @@ class SweepPlan:
 
     def run_gemv(self):
         check(load().bfp8_plan_run_gemv(self.handle, _stream()), "plan_run_gemv")
+
+    def kernel_name(self, stage):
+        """Name of the kernel a stage launches ("" if the stage is empty)."""
+        return load().bfp8_plan_kernel_name(self.handle, stage).decode()
 
     def launch(self, stage):
         """One GEMV stage: 0 lm_head tiles, 1 other tiles + merge, 2 tails."""

@@ -171,6 +171,8 @@ def test_known_answer_279616_on_gpu(gpu, torch_mod):
     (1024, 3584, 124, 130, 2),   # down projection
     (6144, 1024, 124, 130, 3),   # in-projection stand-in
     (1024, 2048, 124, 130, 4),   # out-projection stand-in
+    (40000, 1024, 122, 128, 5),  # 625 row tiles: the persistent streaming kernel
+    (2048, 4096, 124, 130, 6),   # K = 4096: the widest block slice (16 blocks)
 ])
 def test_gemv_configured_shapes(gpu, torch_mod, M, K, elo, ehi, seed):
     qk, torch = gpu, torch_mod
@@ -362,6 +364,33 @@ def test_lm_head_small_vocab_and_invalid_arguments(gpu, torch_mod):
     assert kk.lm_head_topk(x, mant, exps, 100, 128, 65)[0].size == 0
     assert kk.lm_head_topk(x, mant, exps, 100, 128, 0)[0].size == 0
     assert kk.lm_head_argmax(x, mant, exps, 99, 128) == -1
+
+
+def test_small_plan_one_tile_per_workgroup(gpu, torch_mod):
+    """A plan without an lm_head and with few row tiles runs its GEMVs one tile
+    per 16-wavefront workgroup; an odd-M item adds the tail-row kernel and a
+    K > 4096 item the float path."""
+    qk, torch = gpu, torch_mod
+    shapes = [(3584, 1024), (1024, 3584), (1023, 2048), (130, 64), (2048, 4096), (64, 4160)]
+    items, refs = [], []
+    for j, (M, K) in enumerate(shapes):
+        dm = qk.DeviceMatrix.synth(M, K, 4242 + j, 124, 130)
+        x = qk.synth_swiglu(K, 4300 + j) if K == 3584 else qk.synth_normal(K, 4300 + j)
+        items.append({"mat": dm, "x": torch.from_numpy(x).cuda(), "y": torch.empty(M, dtype=torch.float32, device="cuda")})
+        refs.append((M, K, 4242 + j, x))
+    plan = qk.SweepPlan(items)
+    assert plan.kernel_name(1) == "bfp8_gemv_wide_grouped_kernel"
+    say("small plan")
+    for rep in range(2):
+        for it in items:
+            it["y"].fill_(np.nan)
+        plan.run()
+        torch.cuda.synchronize()
+        for it, (M, K, seed, x) in zip(items, refs):
+            mant, exps = qk.synth_planes(M, K, seed, 124, 130)
+            y_ref = ol.gemv_neon(x, mant, exps)[0] if K <= 4096 else ol.gemv_float(x, mant, exps)
+            assert same_f32(it["y"].cpu().numpy(), y_ref), (rep, M, K, mismatch(it["y"].cpu().numpy(), y_ref))
+    plan.close()
 
 
 @pytest.mark.parametrize("shape", ["alone", "with_small_gemv", "ragged_2049_tiles"])
