@@ -60,6 +60,15 @@ void init_kernels(void);
  * writable weight buffers are re-uploaded on every call. */
 void bfp8_gemv(float* y, const float* x, const int8_t* mantissas, const uint8_t* exps, int M, int K);
 
+/* Replaces lm_head_argmax(), 04/qwen_kernels_opt.c:401-506: the bf16 tied-
+ * embedding lm_head (embed_table uint16 [vocab][hidden], the high halves of
+ * floats) dotted with h[hidden] in the board build's order (two float32x4
+ * accumulators over 8-element chunks, flush-to-zero; hidden % 8 trailing
+ * elements dropped), then the lowest id among the maximal scores above -1e30,
+ * else 0.  Host pointers; a read-only table is kept on the device after the
+ * first call. */
+int lm_head_argmax(const float* h, const uint16_t* embed_table, int vocab_size, int hidden_dim);
+
 /* Replace the stage profiler, 04/qwen_kernels_opt.c:87-91 (same 15 slots and
  * names).  Slot 0 (bfp8_gemv) accumulates wall milliseconds of bfp8_gemv and
  * bfp8_gemv_batch; slot 1 (lm_head_argmax) of the fused lm_head calls. */
@@ -90,6 +99,15 @@ int bfp8_lm_head_argmax(const float* h, const int8_t* mantissas, const uint8_t* 
  * entry, 01/FINAL_REPORT.md:361); results are bit-identical to those. */
 void bfp8_gemv_batch(float* Y, const float* X, const int8_t* mantissas, const uint8_t* exps, int M,
                      int K, int B);
+
+/* The implementations behind libqwen_sampling.so (include/qwen_sampling.h):
+ * lm_head_topk over the bf16 table (04/qwen_sampling.c:283-353; k <= 64,
+ * else 0 with bfp8_last_error set) and sample_from_topk
+ * (04/qwen_sampling.c:384-529; n <= 4096 candidates, else -1). */
+int qwen_lm_head_topk_bf16(const float* h, const uint16_t* embed_table, int vocab_size, int hidden_dim, int k,
+                           int* out_ids, float* out_scores);
+int qwen_sample_from_topk(const int* ids, const float* scores, int n, float temperature, int top_k, float top_p,
+                          unsigned int* rng_state);
 
 /* Message of the most recent failure of this library ("" if none). */
 const char* bfp8_last_error(void);
@@ -145,6 +163,24 @@ int bfp8_dev_gemv_batch(float* Y, const uint32_t* xsplit, const float* xscale,
 int bfp8_dev_lm_head_topk(int* out_ids, float* out_scores, int* out_count, int* out_argmax,
                           const uint32_t* xsplit, const float* xscale, const int8_t* mant_gpu,
                           const uint8_t* exps_gpu, int vocab, int hidden, int k, void* stream);
+
+/* bf16 tied-embedding lm_head on device buffers: scores of every row in the
+ * board build's order (tail = 0: hidden % 8 trailing elements dropped, as
+ * lm_head_argmax; tail = 1: added, as lm_head_topk), written to logits[vocab]
+ * when logits is not NULL; with k in 1..64 also the fused top-k (ids[k],
+ * scores[k], count, argmax by the lm_head_argmax rule).  k = 0 needs logits. */
+int bf16_dev_lm_head(int* out_ids, float* out_scores, int* out_count, int* out_argmax, float* logits,
+                     const float* h, const uint16_t* embed_table, int vocab, int hidden, int k, int tail,
+                     void* stream);
+
+/* sample_from_topk (04/qwen_sampling.c:384-529) on the device: candidates
+ * ids[]/scores[] (count from *count when count is not NULL, else n; n is the
+ * capacity, at most 4096), xorshift32 state *rng_state updated in place
+ * (NULL: greedy ids[0]), chosen id to *out_id.  work: 8*n bytes of device
+ * scratch. */
+int bfp8_dev_sample_from_topk(int* out_id, const int* ids, const float* scores, const int* count, int n,
+                              float temperature, int top_k, float top_p, uint32_t* rng_state, void* work,
+                              void* stream);
 
 /* A sweep plan: many independent GEMVs (and at most one fused lm_head)
  * executed as one quantize launch plus two streaming launches: the lm_head's

@@ -22,6 +22,7 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 OUT = PKG / "libqwen_kernels.so"
+OUT_SAMPLING = PKG / "libqwen_sampling.so"
 BUILD = PKG / "_build"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -34,6 +35,7 @@ COMMON = [
 ]
 UNITS = {
     "bfp8_ftz.hip": ["-fgpu-flush-denormals-to-zero"],
+    "bf16_head.hip": ["-fgpu-flush-denormals-to-zero"],
     "bfp8_ieee.hip": [],
     "qwen_kernels_api.cpp": [],
 }
@@ -60,8 +62,18 @@ def build(verbose: bool = False) -> Path:
         sys.stderr.write(res.stdout + res.stderr)
         raise RuntimeError("hipcc link failed")
     os.replace(tmp, OUT)
+    # libqwen_sampling.so: host-only forwarding library, resolved next to
+    # libqwen_kernels.so through its run path
+    tmp = OUT_SAMPLING.with_suffix(".so.tmp")
+    cmd = [HIPCC, "-O2", "-fPIC", "-shared", "-std=c++17", "-fvisibility=hidden", f"-I{ROOT / 'include'}",
+           str(CSRC / "qwen_sampling.cpp"), "-o", str(tmp), f"-L{PKG}", "-lqwen_kernels", "-Wl,-rpath,$ORIGIN"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise RuntimeError("libqwen_sampling.so link failed")
+    os.replace(tmp, OUT_SAMPLING)
     if verbose:
-        print(f"built {OUT}")
+        print(f"built {OUT} and {OUT_SAMPLING}")
     return OUT
 
 

@@ -257,6 +257,94 @@ extern "C" __global__ __launch_bounds__(256) void bfp8_copy_probe_kernel(
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) dst[i] = src[i];
 }
 
+// ---- sampler (04/qwen_sampling.c:358-529) --------------------------------------------
+// One thread over the candidate list: xorshift32 draw, softmax weights summed
+// in double, top-k / top-p cut, as the reference.  expf is formed as the
+// float rounding of the double exponential (correctly rounded but for
+// results within about 2^-29 ulp of a rounding boundary).
+__device__ __forceinline__ float sample_expf(float x) { return (float)exp((double)x); }
+
+extern "C" __global__ __launch_bounds__(64) void bfp8_sample_kernel(Bfp8SampleArgs a) {
+    if (threadIdx.x != 0) return;
+    const int n = a.count ? *a.count : a.n;
+    if (n <= 0) {
+        *a.out = -1;
+        return;
+    }
+    int* id = a.work_ids;
+    float* sc = a.work_scores;
+    bool sorted = true;
+    for (int i = 0; i < n; ++i) {
+        id[i] = a.ids[i];
+        sc[i] = a.scores[i];
+        if (i > 0 && sc[i] > sc[i - 1]) sorted = false;
+    }
+    if (!a.rng) {
+        *a.out = id[0];
+        return;
+    }
+    if (!sorted) {  // (score desc, id asc)
+        for (int i = 1; i < n; ++i) {
+            const int ci = id[i];
+            const float cs = sc[i];
+            int j = i - 1;
+            while (j >= 0 && (sc[j] < cs || (!(sc[j] > cs) && id[j] > ci))) {
+                id[j + 1] = id[j];
+                sc[j + 1] = sc[j];
+                --j;
+            }
+            id[j + 1] = ci;
+            sc[j + 1] = cs;
+        }
+    }
+    int out = id[0];
+    if (a.temperature >= 1e-6f) {
+        const int m = (a.top_k > 0 && a.top_k < n) ? a.top_k : n;
+        float mx = sc[0];
+        for (int i = 1; i < m; ++i)
+            if (sc[i] > mx) mx = sc[i];
+        const float inv_t = 1.0f / a.temperature;
+        double all = 0.0;
+        for (int i = 0; i < m; ++i) all += (double)sample_expf((sc[i] - mx) * inv_t);
+        if (all > 0.0) {
+            float p = a.top_p;
+            if (!(p > 0.0f)) p = 0.0f;
+            if (p > 1.0f) p = 1.0f;
+            int keep = m;
+            double cum = 0.0;
+            for (int i = 0; i < m; ++i) {
+                cum += (double)sample_expf((sc[i] - mx) * inv_t) / all;
+                if (cum > (double)p) {
+                    keep = i + 1;
+                    break;
+                }
+            }
+            double kept = 0.0;
+            for (int i = 0; i < keep; ++i) kept += (double)sample_expf((sc[i] - mx) * inv_t);
+            if (kept > 0.0) {
+                uint32_t x = *a.rng;
+                if (x == 0u) x = 0x9E3779B9u;
+                x ^= x << 13;
+                x ^= x >> 17;
+                x ^= x << 5;
+                *a.rng = x;
+                const double r = (double)((float)(x >> 8) * (1.0f / 16777216.0f)) * kept;
+                int pick = keep - 1;
+                cum = 0.0;
+                for (int i = 0; i < keep; ++i) {
+                    cum += (double)sample_expf((sc[i] - mx) * inv_t);
+                    if (r < cum) {
+                        pick = i;
+                        break;
+                    }
+                }
+                out = id[pick];
+            }
+        }
+    }
+    *a.out = out;
+}
+
 // ---- launchers ----------------------------------------------------------------------
 static int grid_for(size_t work, int per_block) {
     size_t g = (work + per_block - 1) / per_block;
@@ -325,6 +413,11 @@ hipError_t bfp8_launch_synth_planes(int8_t* mant_soa, uint8_t* exps_soa, int M, 
     const size_t nm = (size_t)M * K, ne = (size_t)M * bfp8_nblocks(K);
     hipLaunchKernelGGL(bfp8_synth_kernel, dim3(grid_for(nm, 256 * 16)), dim3(256), 0, s, mant_soa, exps_soa, nm,
                        ne, seed, e_lo, e_hi);
+    return hipGetLastError();
+}
+
+hipError_t bfp8_launch_sample(const Bfp8SampleArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL(bfp8_sample_kernel, dim3(1), dim3(64), 0, s, a);
     return hipGetLastError();
 }
 

@@ -44,6 +44,32 @@ struct Bfp8QuantDesc {
     int pad_;
 };
 
+// The bf16 tied-embedding lm_head (bf16_head.hip).
+struct Bf16HeadDesc {
+    const uint16_t* table;  // [vocab][hidden] bf16 (high halves of floats)
+    const float* h;         // [hidden]
+    float* logits;          // optional [vocab] scores, may be null
+    uint64_t* partials;     // [ntiles][topk] per-tile sorted keys (topk > 0)
+    int vocab, hidden;
+    int topk;               // 0: scores only
+    int tail;               // 1: add the hidden % 8 trailing elements (lm_head_topk)
+};
+
+// The sampler over a sorted candidate list (bfp8_ieee.hip).
+struct Bfp8SampleArgs {
+    const int* ids;
+    const float* scores;
+    const int* count;       // device candidate count, or null to use n
+    int n;
+    float temperature;
+    int top_k;
+    float top_p;
+    uint32_t* rng;          // xorshift32 state, updated in place (null: greedy)
+    int* out;               // chosen id
+    int* work_ids;          // n-entry scratch
+    float* work_scores;
+};
+
 // Grouped-launch work item: which descriptor and which row tile.
 struct Bfp8TileRef {
     int desc;
@@ -52,6 +78,7 @@ struct Bfp8TileRef {
 
 #define BFP8_TOPK_MAX 64
 #define BFP8_TOPK_MAX_TILES 4096
+#define BFP8_SAMPLE_MAX 4096  // candidates the sampler takes
 #define BFP8_STREAM_WG_PER_CU 4
 // Row tiles up to which a GEMV (or a plan's GEMVs) runs one tile per
 // 16-wavefront workgroup instead of the persistent streaming kernel.
@@ -85,7 +112,11 @@ hipError_t bfp8_launch_gemv_batch(float* Y, const uint32_t* xsplit, const float*
                                   const uint8_t* mant, const uint8_t* exps, int M, int K, int B,
                                   hipStream_t s);
 
+// ---- bf16_head.hip --------------------------------------------------------
+hipError_t bf16_launch_lm_head(const Bf16HeadDesc& d, hipStream_t s);
+
 // ---- bfp8_ieee.hip -------------------------------------------------------
+hipError_t bfp8_launch_sample(const Bfp8SampleArgs& a, hipStream_t s);
 hipError_t bfp8_launch_quantize(const Bfp8QuantDesc* descs_dev, int ndesc, int max_nb, hipStream_t s);
 hipError_t bfp8_launch_quantize1(const Bfp8QuantDesc& d, hipStream_t s);
 hipError_t bfp8_launch_tail_row(float* y, const uint32_t* xsplit, const float* xscale,

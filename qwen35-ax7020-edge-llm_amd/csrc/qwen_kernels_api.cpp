@@ -138,7 +138,11 @@ struct State {
     DevBuf x, xq, xscale, xsplit, y;            // activation / output workspace
     DevBuf soa_m, soa_e, gpu_m, gpu_e;          // per-call weight upload
     DevBuf tk_partials, tk_out;                 // fused lm_head workspace
+    DevBuf bf16_ws;                             // per-call bf16 table upload
+    DevBuf smp_in, smp_work, smp_out;           // sampler inputs / scratch / outputs
+    PinnedBuf smp_h;
     std::map<WeightKey, CachedWeights> cache;
+    std::map<WeightKey, DevBuf> bf16_cache;     // read-only bf16 embedding tables
     size_t cache_bytes = 0;
 };
 
@@ -227,6 +231,88 @@ int weights_for(const int8_t* mant, const uint8_t* exps, int M, int K, DevWeight
         g.cache.emplace(key, cw);
     }
     return BFP8_OK;
+}
+
+int upload_x(const float* x, size_t nfloat);
+
+// Device copy of a host bf16 table [vocab][hidden]: cached when it lives in
+// read-only memory (the engine's mmap), else uploaded per call.
+int bf16_table_for(const uint16_t* table, int vocab, int hidden, const uint16_t** out) {
+    const size_t bytes = (size_t)vocab * (size_t)hidden * 2;
+    const WeightKey key{table, nullptr, vocab, hidden};
+    auto it = g.bf16_cache.find(key);
+    if (it != g.bf16_cache.end()) {
+        *out = it->second.as<uint16_t>();
+        return BFP8_OK;
+    }
+    const bool cacheable = g.cache_bytes + bytes <= kCacheLimit && range_readonly(table, bytes);
+    DevBuf fresh;
+    DevBuf* d = cacheable ? &fresh : &g.bf16_ws;
+    int rc;
+    if ((rc = d->reserve(bytes))) return rc;
+    HIP_OK(hipMemcpyAsync(d->p, table, bytes, hipMemcpyHostToDevice, g.stream));
+    *out = d->as<uint16_t>();
+    if (cacheable) {
+        g.cache_bytes += fresh.n;
+        g.bf16_cache.emplace(key, fresh);
+    }
+    return BFP8_OK;
+}
+
+// bf16 lm_head scores (+ fused top-k) on device buffers.
+int bf16_lm_head_dev(int* ids, float* scores, int* count, int* argmax, float* logits, const float* h,
+                     const uint16_t* table, int vocab, int hidden, int k, int tail, hipStream_t s) {
+    const int kk = k > 0 ? std::min(k, vocab) : 0;
+    int rc;
+    if (kk > 0 && (rc = g.tk_partials.reserve((size_t)bfp8_ntiles(vocab) * kk * 8))) return rc;
+    Bf16HeadDesc d{};
+    d.table = table;
+    d.h = h;
+    d.logits = logits;
+    d.partials = kk > 0 ? g.tk_partials.as<uint64_t>() : nullptr;
+    d.vocab = vocab;
+    d.hidden = hidden;
+    d.topk = kk;
+    d.tail = tail;
+    HIP_OK(bf16_launch_lm_head(d, s));
+    if (kk > 0) {
+        Bfp8GemvDesc md{};
+        md.M = vocab;
+        md.topk = kk;
+        md.partials = d.partials;
+        md.out_ids = ids;
+        md.out_scores = scores;
+        md.out_count = count;
+        md.out_argmax = argmax;
+        HIP_OK(bfp8_launch_topk_merge(md, s));
+    }
+    return BFP8_OK;
+}
+
+// Host-pointer bf16 lm_head: returns the candidate count (fills ids/scores
+// when given) and the argmax through *am.
+int host_bf16_lm_head(const float* h, const uint16_t* table, int vocab, int hidden, int k, int tail,
+                      int* out_ids, float* out_scores, int* am) {
+    int rc;
+    const uint16_t* tdev;
+    if ((rc = bf16_table_for(table, vocab, hidden, &tdev)) || (rc = upload_x(h, (size_t)hidden))) return rc;
+    const int kk = std::min(k, vocab);
+    if ((rc = g.tk_out.reserve((size_t)(2 * BFP8_TOPK_MAX + 2) * 4)) || (rc = g.h_out.reserve((size_t)(2 * BFP8_TOPK_MAX + 2) * 4)))
+        return rc;
+    int* d_ids = g.tk_out.as<int>();
+    float* d_sc = reinterpret_cast<float*>(d_ids + BFP8_TOPK_MAX);
+    int* d_cnt = d_ids + 2 * BFP8_TOPK_MAX;
+    if ((rc = bf16_lm_head_dev(d_ids, d_sc, d_cnt, d_cnt + 1, nullptr, g.x.as<float>(), tdev, vocab, hidden, kk, tail,
+                               g.stream)))
+        return rc;
+    HIP_OK(hipMemcpyAsync(g.h_out.p, g.tk_out.p, (size_t)(2 * BFP8_TOPK_MAX + 2) * 4, hipMemcpyDeviceToHost, g.stream));
+    HIP_OK(hipStreamSynchronize(g.stream));
+    const int* hi = static_cast<const int*>(g.h_out.p);
+    const int n = hi[2 * BFP8_TOPK_MAX];
+    if (am) *am = hi[2 * BFP8_TOPK_MAX + 1];
+    if (out_ids && n > 0) memcpy(out_ids, hi, (size_t)n * 4);
+    if (out_scores && n > 0) memcpy(out_scores, hi + BFP8_TOPK_MAX, (size_t)n * 4);
+    return n;
 }
 
 int upload_x(const float* x, size_t nfloat) {
@@ -465,6 +551,72 @@ int bfp8_lm_head_argmax(const float* h, const int8_t* mantissas, const uint8_t* 
     return n < 0 ? -1 : am;
 }
 
+int lm_head_argmax(const float* h, const uint16_t* embed_table, int vocab_size, int hidden_dim) {
+    ProfScope ps(QP_LMHEAD);
+    if (!h || !embed_table || vocab_size <= 0 || hidden_dim <= 0) return 0;
+    std::lock_guard<std::mutex> lk(g.mu);
+    int am = 0;
+    if (ensure_init_locked() != BFP8_OK ||
+        host_bf16_lm_head(h, embed_table, vocab_size, hidden_dim, 1, 0, nullptr, nullptr, &am) < 0)
+        fatal("lm_head_argmax");
+    return am;
+}
+
+int qwen_lm_head_topk_bf16(const float* h, const uint16_t* embed_table, int vocab_size, int hidden_dim, int k,
+                           int* out_ids, float* out_scores) {
+    ProfScope ps(QP_LMHEAD);
+    if (!h || !embed_table || !out_ids || !out_scores || vocab_size <= 0 || hidden_dim <= 0 || k <= 0) return 0;
+    if (std::min(k, vocab_size) > BFP8_TOPK_MAX) {
+        set_error("lm_head_topk: k = %d above the fused limit %d", k, BFP8_TOPK_MAX);
+        return 0;
+    }
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (ensure_init_locked() != BFP8_OK) return 0;
+    const int n = host_bf16_lm_head(h, embed_table, vocab_size, hidden_dim, k, 1, out_ids, out_scores, nullptr);
+    return n < 0 ? 0 : n;
+}
+
+int qwen_sample_from_topk(const int* ids, const float* scores, int n, float temperature, int top_k, float top_p,
+                          unsigned int* rng_state) {
+    if (!ids || !scores || n <= 0) return -1;
+    if (!rng_state) return ids[0];
+    if (n > BFP8_SAMPLE_MAX) {
+        set_error("sample_from_topk: n = %d above %d candidates", n, BFP8_SAMPLE_MAX);
+        return -1;
+    }
+    std::lock_guard<std::mutex> lk(g.mu);
+    if (ensure_init_locked() != BFP8_OK) return -1;
+    int rc;
+    if ((rc = g.smp_in.reserve((size_t)n * 8 + 4)) || (rc = g.smp_work.reserve((size_t)n * 8)) ||
+        (rc = g.smp_out.reserve(8)) || (rc = g.smp_h.reserve((size_t)n * 8 + 8)))
+        fatal("sample_from_topk");
+    char* hb = static_cast<char*>(g.smp_h.p);
+    memcpy(hb, ids, (size_t)n * 4);
+    memcpy(hb + (size_t)n * 4, scores, (size_t)n * 4);
+    memcpy(hb + (size_t)n * 8, rng_state, 4);
+    Bfp8SampleArgs a{};
+    a.ids = g.smp_in.as<int>();
+    a.scores = reinterpret_cast<const float*>(g.smp_in.as<char>() + (size_t)n * 4);
+    a.rng = reinterpret_cast<uint32_t*>(g.smp_in.as<char>() + (size_t)n * 8);
+    a.n = n;
+    a.temperature = temperature;
+    a.top_k = top_k;
+    a.top_p = top_p;
+    a.out = g.smp_out.as<int>();
+    a.work_ids = g.smp_work.as<int>();
+    a.work_scores = reinterpret_cast<float*>(g.smp_work.as<char>() + (size_t)n * 4);
+    if (hipMemcpyAsync(g.smp_in.p, hb, (size_t)n * 8 + 4, hipMemcpyHostToDevice, g.stream) != hipSuccess ||
+        bfp8_launch_sample(a, g.stream) != hipSuccess ||
+        hipMemcpyAsync(hb, g.smp_out.p, 4, hipMemcpyDeviceToHost, g.stream) != hipSuccess ||
+        hipMemcpyAsync(hb + 4, a.rng, 4, hipMemcpyDeviceToHost, g.stream) != hipSuccess ||
+        hipStreamSynchronize(g.stream) != hipSuccess)
+        fatal("sample_from_topk");
+    int out;
+    memcpy(&out, hb, 4);
+    memcpy(rng_state, hb + 4, 4);
+    return out;
+}
+
 const char* bfp8_last_error(void) {
     static thread_local std::string copy;
     std::lock_guard<std::mutex> lk(g_err_mu);
@@ -475,6 +627,8 @@ const char* bfp8_last_error(void) {
 void bfp8_cache_clear(void) {
     std::lock_guard<std::mutex> lk(g.mu);
     if (g.ready) (void)hipStreamSynchronize(g.stream);
+    for (auto& kv : g.bf16_cache) kv.second.release();
+    g.bf16_cache.clear();
     for (auto& kv : g.cache) {
         kv.second.mant.release();
         kv.second.exps.release();
@@ -632,6 +786,42 @@ int bfp8_dev_read_probe(const void* buf, size_t bytes, uint32_t* out, void* stre
 int bfp8_dev_copy_probe(void* dst, const void* src, size_t bytes, void* stream) {
     DEV_PROLOGUE();
     HIP_OK(bfp8_launch_copy_probe(dst, src, bytes, pick_stream(stream)));
+    return BFP8_OK;
+}
+
+int bf16_dev_lm_head(int* out_ids, float* out_scores, int* out_count, int* out_argmax, float* logits,
+                     const float* h, const uint16_t* table, int vocab, int hidden, int k, int tail, void* stream) {
+    DEV_PROLOGUE();
+    if (!h || !table || vocab <= 0 || hidden <= 0 || k < 0 || std::min(k, vocab) > BFP8_TOPK_MAX ||
+        (k > 0 && (!out_ids || !out_scores || !out_count || !out_argmax)) || (k == 0 && !logits)) {
+        set_error("bf16_dev_lm_head: invalid arguments");
+        return BFP8_EINVAL;
+    }
+    return bf16_lm_head_dev(out_ids, out_scores, out_count, out_argmax, logits, h, table, vocab, hidden, k,
+                            tail ? 1 : 0, pick_stream(stream));
+}
+
+int bfp8_dev_sample_from_topk(int* out_id, const int* ids, const float* scores, const int* count, int n,
+                              float temperature, int top_k, float top_p, uint32_t* rng_state, void* work,
+                              void* stream) {
+    DEV_PROLOGUE();
+    if (!out_id || !ids || !scores || n <= 0 || n > BFP8_SAMPLE_MAX || !work) {
+        set_error("bfp8_dev_sample_from_topk: invalid arguments");
+        return BFP8_EINVAL;
+    }
+    Bfp8SampleArgs a{};
+    a.ids = ids;
+    a.scores = scores;
+    a.count = count;
+    a.n = n;
+    a.temperature = temperature;
+    a.top_k = top_k;
+    a.top_p = top_p;
+    a.rng = rng_state;
+    a.out = out_id;
+    a.work_ids = static_cast<int*>(work);
+    a.work_scores = reinterpret_cast<float*>(static_cast<char*>(work) + (size_t)n * 4);
+    HIP_OK(bfp8_launch_sample(a, pick_stream(stream)));
     return BFP8_OK;
 }
 

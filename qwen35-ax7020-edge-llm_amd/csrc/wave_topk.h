@@ -1,0 +1,103 @@
+// wave_topk.h -- wavefront-level top-k building blocks shared by the GEMV
+// and lm_head kernels: 64-bit (score, row) keys, xor-lane exchange, bitonic
+// sort and merge networks over one wave64.  Device code only; every function
+// is inline and works on integers, so it behaves the same in flush-to-zero and
+// IEEE translation units.
+#pragma once
+
+#include <float.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+// ---- top-k keys ------------------------------------------------------------
+// Order (score desc, id asc) as one unsigned 64-bit key, larger = better.
+// Candidates are the scores the reference would ever offer: > -FLT_MAX, not
+// NaN (04/qwen_sampling.c:243-248 with thr = -FLT_MAX).  -0 equals +0 there,
+// so it is keyed as +0.  0 is "no candidate".
+__device__ __forceinline__ uint64_t topk_key(float y, int row) {
+    if (!(y > -FLT_MAX)) return 0;
+    uint32_t b = __float_as_uint(y == 0.0f ? 0.0f : y);
+    uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((uint64_t)o << 32) | (uint32_t)~(uint32_t)row;
+}
+__device__ __forceinline__ float key_score(uint64_t k) {
+    uint32_t o = (uint32_t)(k >> 32);
+    return __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
+}
+__device__ __forceinline__ int key_id(uint64_t k) { return (int)~(uint32_t)k; }
+
+// ---- wavefront exchange ----------------------------------------------------
+// Lane i receives lane i^j.  j = 1, 2: DPP quad permutes; j = 4, 8, 16:
+// ds_swizzle bit-mask mode (and 0x1f, xor j, within 32 lanes); j = 32, 63:
+// ds_bpermute.  Always called with j a constant after unrolling.
+__device__ __forceinline__ uint32_t xor_lane32(uint32_t v, int j) {
+    switch (j) {
+        case 1: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);
+        case 2: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);
+        case 4: return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x1F | (4 << 10));
+        case 8: return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x1F | (8 << 10));
+        case 16: return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x1F | (16 << 10));
+        default: return (uint32_t)__shfl_xor((int)v, j, 64);
+    }
+}
+__device__ __forceinline__ uint64_t xor_lane(uint64_t v, int j) {
+    const uint32_t lo = xor_lane32((uint32_t)v, j);
+    const uint32_t hi = xor_lane32((uint32_t)(v >> 32), j);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// Bitonic sort of N independent columns (one key per lane each), column n
+// descending by lane when desc[n], else ascending; the N compare-exchange
+// chains interleave.  A compare-exchange keeps the partner's key when
+// (partner > own) equals "this lane keeps the larger" -- one 64-bit compare
+// and one select.
+template <int N>
+__device__ __forceinline__ void wave_sort(uint64_t (&key)[N], const bool (&desc)[N], int lane) {
+#pragma unroll
+    for (int k = 2; k <= 64; k <<= 1) {
+#pragma unroll
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            const bool up = ((lane & j) == 0) == ((lane & k) == 0);
+#pragma unroll
+            for (int n = 0; n < N; ++n) {
+                const uint64_t o = xor_lane(key[n], j);
+                key[n] = ((o > key[n]) == (up == desc[n])) ? o : key[n];
+            }
+        }
+    }
+}
+
+// a and b sorted in opposite directions -> the 64 largest keys of both,
+// sorted descending (kDesc) or ascending: max(a[i], b[i]) holds them as a
+// bitonic sequence, six half-cleaner stages sort it.
+template <bool kDesc>
+__device__ __forceinline__ uint64_t wave_merge(uint64_t a, uint64_t b, int lane) {
+    uint64_t c = a > b ? a : b;
+#pragma unroll
+    for (int j = 32; j > 0; j >>= 1) {
+        const uint64_t o = xor_lane(c, j);
+        c = ((o > c) == (((lane & j) == 0) == kDesc)) ? o : c;
+    }
+    return c;
+}
+
+// Pairwise tree merge of N (power of two) lists held as even = descending,
+// odd = ascending; the result is descending.
+template <int N>
+__device__ __forceinline__ uint64_t wave_merge_tree(uint64_t (&v)[N], int lane) {
+#pragma unroll
+    for (int s = 1; s < N; s <<= 1) {
+#pragma unroll
+        for (int i = 0; i < N; i += 2 * s) {
+            if ((i / (2 * s)) % 2 == 0)
+                v[i] = wave_merge<true>(v[i], v[i + s], lane);
+            else
+                v[i] = wave_merge<false>(v[i], v[i + s], lane);
+        }
+    }
+    return v[0];
+}
+
+}  // namespace

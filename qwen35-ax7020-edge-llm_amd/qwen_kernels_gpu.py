@@ -68,6 +68,13 @@ def bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.bfp8_lm_head_argmax.restype = i
     lib.bfp8_gemv_batch.argtypes = [vp, vp, vp, vp, i, i, i]
     lib.bfp8_gemv_batch.restype = None
+    # the bf16 tied-embedding lm_head (04/qwen_real_engine.py:691-696) and sampler
+    lib.lm_head_argmax.argtypes = [vp, vp, i, i]
+    lib.lm_head_argmax.restype = i
+    lib.qwen_lm_head_topk_bf16.argtypes = [vp, vp, i, i, i, vp, vp]
+    lib.qwen_lm_head_topk_bf16.restype = i
+    lib.qwen_sample_from_topk.argtypes = [vp, vp, i, c_float, i, c_float, vp]
+    lib.qwen_sample_from_topk.restype = i
     lib.bfp8_last_error.argtypes = []
     lib.bfp8_last_error.restype = ctypes.c_char_p
     lib.bfp8_cache_clear.argtypes = []
@@ -88,7 +95,9 @@ def bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.bfp8_dev_synth_planes.argtypes = [vp, vp, i, i, c_uint64, i, i, vp]
     lib.bfp8_dev_read_probe.argtypes = [vp, c_size_t, vp, vp]
     lib.bfp8_dev_copy_probe.argtypes = [vp, vp, c_size_t, vp]
-    for name in ("bfp8_dev_pack", "bfp8_dev_unpack", "bfp8_dev_quantize", "bfp8_dev_gemv",
+    lib.bf16_dev_lm_head.argtypes = [vp, vp, vp, vp, vp, vp, vp, i, i, i, i, vp]
+    lib.bfp8_dev_sample_from_topk.argtypes = [vp, vp, vp, vp, i, c_float, i, c_float, vp, vp, vp]
+    for name in ("bf16_dev_lm_head", "bfp8_dev_sample_from_topk", "bfp8_dev_pack", "bfp8_dev_unpack", "bfp8_dev_quantize", "bfp8_dev_gemv",
                  "bfp8_dev_gemv_float", "bfp8_dev_gemv_batch", "bfp8_dev_lm_head_topk",
                  "bfp8_dev_synth_planes", "bfp8_dev_read_probe", "bfp8_dev_copy_probe"):
         getattr(lib, name).restype = i
@@ -129,6 +138,28 @@ def load(path: Optional[str] = None) -> ctypes.CDLL:
     if path is None:
         _LIB = lib
     return lib
+
+
+SAMPLING_PATH = LIB_PATH.with_name("libqwen_sampling.so")
+_SAMPLING: Optional[ctypes.CDLL] = None
+
+
+def load_sampling() -> ctypes.CDLL:
+    """libqwen_sampling.so, bound as 04/chat_v3.py:150-159 binds the reference's."""
+    global _SAMPLING
+    if _SAMPLING is None:
+        if not SAMPLING_PATH.exists():
+            raise FileNotFoundError(f"{SAMPLING_PATH} not built: run qwen35-ax7020-edge-llm_amd/build_lib.py")
+        load()
+        lib = ctypes.CDLL(str(SAMPLING_PATH))
+        lib.lm_head_topk.restype = ctypes.c_int
+        lib.lm_head_topk.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                     ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_float)]
+        lib.sample_from_topk.restype = ctypes.c_int
+        lib.sample_from_topk.argtypes = [ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_float), ctypes.c_int,
+                                         ctypes.c_float, ctypes.c_int, ctypes.c_float, ctypes.POINTER(ctypes.c_uint)]
+        _SAMPLING = lib
+    return _SAMPLING
 
 
 def check(rc: int, what: str = "call") -> None:

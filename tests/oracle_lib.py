@@ -39,6 +39,11 @@ def oracle() -> ctypes.CDLL:
         lib.orc_topk.argtypes = [vp, i, i, vp, vp]
         lib.orc_topk.restype = i
         lib.orc_gemv_f64.argtypes = [vp, vp, vp, vp, vp, i, i]
+        lib.orc_bf16_dot.argtypes = [vp, vp, i, i]
+        lib.orc_bf16_dot.restype = c_float
+        lib.orc_bf16_logits.argtypes = [vp, vp, i, i, i, vp]
+        lib.orc_sample_from_topk.argtypes = [vp, vp, i, c_float, i, c_float, vp]
+        lib.orc_sample_from_topk.restype = i
         _orc = lib
     return _orc
 
@@ -149,6 +154,8 @@ def ref_sampling() -> ctypes.CDLL:
         lib = ctypes.CDLL(str(REF_SAMPLING))
         lib.lm_head_topk.argtypes = [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p, c_void_p]
         lib.lm_head_topk.restype = c_int
+        lib.sample_from_topk.argtypes = [c_void_p, c_void_p, c_int, c_float, c_int, c_float, c_void_p]
+        lib.sample_from_topk.restype = c_int
         _refs = lib
     return _refs
 
@@ -187,3 +194,45 @@ def ref_argmax(logits_bf16_bits):
 
 def bf16_to_f32(bits):
     return (np.asarray(bits, dtype=np.uint32) << 16).view(np.float32)
+
+
+# ---- bf16 tied-embedding lm_head and the sampler ------------------------------------
+def bf16_dot(h, row, tail):
+    h = np.ascontiguousarray(h, dtype=np.float32)
+    row = np.ascontiguousarray(row, dtype=np.uint16)
+    return oracle().orc_bf16_dot(_p(h), _p(row), row.size, int(tail))
+
+
+def bf16_logits(h, table, tail):
+    """Board-build scores of every row (tail: 0 = lm_head_argmax's rule,
+    1 = lm_head_topk's)."""
+    h = np.ascontiguousarray(h, dtype=np.float32)
+    table = np.ascontiguousarray(table, dtype=np.uint16)
+    V, H = table.shape
+    out = np.zeros(V, dtype=np.float32)
+    oracle().orc_bf16_logits(_p(h), _p(table), V, H, int(tail), _p(out))
+    return out
+
+
+def sample_from_topk(ids, scores, temperature, top_k, top_p, state):
+    """Returns (chosen id, new state)."""
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    scores = np.ascontiguousarray(scores, dtype=np.float32)
+    st = np.array([state], dtype=np.uint32)
+    r = oracle().orc_sample_from_topk(_p(ids), _p(scores), ids.size, temperature, top_k, top_p, _p(st))
+    return r, int(st[0])
+
+
+def ref_sample_from_topk(ids, scores, temperature, top_k, top_p, state):
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    scores = np.ascontiguousarray(scores, dtype=np.float32)
+    st = np.array([state], dtype=np.uint32)
+    r = ref_sampling().sample_from_topk(_p(ids), _p(scores), ids.size, temperature, top_k, top_p, _p(st))
+    return r, int(st[0])
+
+
+def f32_to_bf16_bits(x):
+    """Round-to-nearest-even bf16 bits of float32 values (test data only)."""
+    b = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    b = (b + 0x7FFF + ((b >> 16) & 1)) >> 16
+    return b.astype(np.uint16)

@@ -14,17 +14,19 @@ import pytest
 ROOT = Path(__file__).resolve().parent.parent
 HEADER = ROOT / "include" / "qwen_kernels.h"
 LIB = ROOT / "qwen35-ax7020-edge-llm_amd" / "libqwen_kernels.so"
+SAMPLING_HEADER = ROOT / "include" / "qwen_sampling.h"
+SAMPLING_LIB = ROOT / "qwen35-ax7020-edge-llm_amd" / "libqwen_sampling.so"
 
 
-def declared_functions():
-    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+def declared_functions(header=HEADER):
+    text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
     text = "\n".join(l for l in text.splitlines() if not l.lstrip().startswith("#"))
     names = re.findall(r"(?:^|;|\})\s*(?:const\s+)?[A-Za-z_][\w]*\s*\**\s*\b([a-z_][a-z0-9_]*)\s*\(", text, re.M)
     return sorted(set(names) - {"struct", "typedef"})
 
 
-def exported_symbols():
-    out = subprocess.run(["nm", "-D", "--defined-only", str(LIB)], capture_output=True, text=True, check=True)
+def exported_symbols(lib=LIB):
+    out = subprocess.run(["nm", "-D", "--defined-only", str(lib)], capture_output=True, text=True, check=True)
     return {l.split()[-1] for l in out.stdout.splitlines() if " T " in l}
 
 
@@ -35,7 +37,7 @@ def test_library_built_and_loads():
 
 def test_exports_every_declared_symbol():
     decl = declared_functions()
-    assert len(decl) >= 35 and "bfp8_gemv" in decl and "bfp8_plan_create" in decl
+    assert len(decl) >= 40 and "bfp8_gemv" in decl and "lm_head_argmax" in decl and "bfp8_plan_create" in decl
     missing = set(decl) - exported_symbols()
     assert not missing, missing
 
@@ -43,6 +45,15 @@ def test_exports_every_declared_symbol():
 def test_exports_nothing_undeclared():
     extra = exported_symbols() - set(declared_functions())
     assert not extra, extra
+
+
+def test_sampling_library_exports_exactly_the_reference_pair():
+    """libqwen_sampling.so stands in for the reference's sampling library
+    (04/chat_v3.py:145-159 binds lm_head_topk and sample_from_topk)."""
+    decl = set(declared_functions(SAMPLING_HEADER))
+    assert decl == {"lm_head_topk", "sample_from_topk"}
+    assert exported_symbols(SAMPLING_LIB) == decl
+    ctypes.CDLL(str(SAMPLING_LIB))  # finds libqwen_kernels.so next to it
 
 
 def test_reference_symbol_signatures_bind_like_the_engine():

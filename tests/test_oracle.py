@@ -268,3 +268,126 @@ def test_oracle_regression_vectors():
         assert np.array_equal(y.view(np.uint32), d[f"{case}_y"].view(np.uint32))
         assert np.array_equal(xq, d[f"{case}_xq"]) and np.array_equal(lanes, d[f"{case}_lanes"])
         assert np.array_equal(xs.view(np.uint32), d[f"{case}_xscale"].view(np.uint32))
+
+
+# ---- bf16 tied-embedding lm_head (board build) -------------------------------------------------
+F = np.float32
+
+
+def _bf(values):
+    return ol.f32_to_bf16_bits(np.asarray(values, dtype=F))
+
+
+def test_bf16_dot_exact_integer_rows_and_tail_rules():
+    """Small integers make every product and partial sum exact, so any order
+    gives the integer dot; the tail rule of each entry point is then the only
+    difference: lm_head_argmax drops the hidden % 8 last elements,
+    lm_head_topk adds them."""
+    rng = np.random.default_rng(11)
+    for hidden in (8, 64, 1000, 1003):
+        w = rng.integers(-8, 9, hidden)
+        h = rng.integers(-8, 9, hidden).astype(F)
+        full = int(np.dot(w, h.astype(np.int64)))
+        body = int(np.dot(w[: hidden - hidden % 8], h[: hidden - hidden % 8].astype(np.int64)))
+        assert ol.bf16_dot(h, _bf(w), tail=1) == full
+        assert ol.bf16_dot(h, _bf(w), tail=0) == body
+
+
+@pytest.mark.parametrize("elems,expected", [
+    # lane 0 gets 2^24 then +1 (rounds back to 2^24), lane 2 gets -2^24: the
+    # 8-lane order gives 0; a plain left-to-right sum gives 1
+    ({0: 2.0**24, 8: 1.0, 2: -(2.0**24)}, 0.0),
+    # a0[0] and a1[0] cancel first (acc = a0 + a1), lane 1 survives: 1;
+    # adding a0's lanes before a1's would give 0
+    ({0: 2.0**24, 4: -(2.0**24), 1: 1.0}, 1.0),
+    # (acc0 + acc2) + (acc1 + acc3): (2^24 + 1) + (1 + 1) = 2^24 + 2; a
+    # sequential sum gives 2^24
+    ({0: 2.0**24, 2: 1.0, 1: 1.0, 3: 1.0}, 2.0**24 + 2),
+    # one lane accumulates its chunks in order: (2^24 + 1) + 1 = 2^24; a
+    # pairwise per-lane order gives 2^24 + 2
+    ({0: 2.0**24, 8: 1.0, 16: 1.0}, 2.0**24),
+])
+def test_bf16_dot_lane_order(elems, expected):
+    w = np.zeros(24, dtype=F)
+    for i, v in elems.items():
+        w[i] = v
+    h = np.ones(24, dtype=F)
+    assert ol.bf16_dot(h, _bf(w), tail=0) == expected
+    assert ol.bf16_dot(h, _bf(w), tail=1) == expected
+
+
+def test_bf16_dot_flush_to_zero_in_the_vector_body_only():
+    """Advanced SIMD flushes a subnormal product (and a subnormal bf16
+    operand) to zero; the scalar VFP tail of lm_head_topk keeps them."""
+    h = np.zeros(9, dtype=F)
+    w = np.zeros(9, dtype=F)
+    h[0], w[0] = 1e-30, 1e-10            # product ~1e-40: subnormal
+    assert ol.bf16_dot(h, _bf(w), tail=1) == 0.0
+    bits = _bf(w)
+    bits[0] = 0x0001                      # subnormal bf16 operand
+    h[0] = 1e10
+    assert ol.bf16_dot(h, bits, tail=0) == 0.0
+    h2 = np.zeros(9, dtype=F)
+    h2[8] = 1e-30                         # the ninth element is the tail
+    w2 = np.zeros(9, dtype=F)
+    w2[8] = 1e-10
+    v = ol.bf16_dot(h2, _bf(w2), tail=1)
+    assert v != 0.0 and abs(v) < np.finfo(F).tiny
+    assert ol.bf16_dot(h2, _bf(w2), tail=0) == 0.0
+
+
+def test_bf16_logits_float64_bound():
+    rng = np.random.default_rng(12)
+    V, H = 256, 1024
+    table = _bf(rng.standard_normal((V, H)).astype(F) * 0.05)
+    h = rng.standard_normal(H).astype(F)
+    got = ol.bf16_logits(h, table, tail=1)
+    w = ol.bf16_to_f32(table).astype(np.float64)
+    exact = w @ h.astype(np.float64)
+    bound = (H / 8 + 3) * np.finfo(F).eps * (np.abs(w) @ np.abs(h.astype(np.float64)))
+    assert np.all(np.abs(got - exact) <= bound)
+
+
+@pytest.mark.skipif(not ol.ref_available(), reason="oracle/_ref needs the reference sources")
+def test_bf16_selection_ids_agree_with_reference_host_build():
+    """The reference's host build sums each row left to right (its scalar
+    path), so its scores differ from the board's in the last bits; with no
+    near-ties the selected ids are the same."""
+    rng = np.random.default_rng(13)
+    V, H = 4096, 256
+    table = _bf(rng.standard_normal((V, H)).astype(F) * 0.05)
+    h = rng.standard_normal(H).astype(F)
+    logits = ol.bf16_logits(h, table, tail=1)
+    ids, sc = ol.topk(logits, 40)
+    r_ids = np.zeros(40, dtype=np.int32)
+    r_sc = np.zeros(40, dtype=np.float32)
+    n = ol.ref_sampling().lm_head_topk(ol._p(h), ol._p(table), V, H, 40, ol._p(r_ids), ol._p(r_sc))
+    assert n == 40 and np.array_equal(ids, r_ids)
+    assert np.allclose(sc, r_sc, rtol=1e-5, atol=1e-6)
+    assert ol.ref_kernels().lm_head_argmax(ol._p(h), ol._p(table), V, H) == ol.argmax(ol.bf16_logits(h, table, 0))
+
+
+@pytest.mark.skipif(not ol.ref_available(), reason="oracle/_ref needs the reference sources")
+def test_sample_from_topk_matches_reference_build():
+    """The sampler has no vector code, so the reference's host build is its
+    board behaviour: ids and the updated xorshift32 state must be identical."""
+    rng = np.random.default_rng(14)
+    cases = 0
+    for trial in range(300):
+        n = int(rng.integers(1, 65))
+        sc = np.sort(rng.standard_normal(n).astype(F) * rng.choice([0.1, 1.0, 8.0]))[::-1].copy()
+        if trial % 5 == 0:
+            rng.shuffle(sc)
+        if trial % 7 == 0 and n > 3:
+            sc[1] = sc[2]                 # ties
+        ids = rng.permutation(100000)[:n].astype(np.int32)
+        temp = float(rng.choice([0.0, 1e-7, 0.3, 0.7, 1.0, 2.5]))
+        top_k = int(rng.choice([0, 1, 5, 40, 100]))
+        top_p = float(rng.choice([-1.0, 0.0, 0.5, 0.9, 1.0, 1.5]))
+        state = int(rng.choice([0, 1, 0x9E3779B9, int(rng.integers(0, 2**32))]))
+        assert ol.sample_from_topk(ids, sc, temp, top_k, top_p, state) == \
+            ol.ref_sample_from_topk(ids, sc, temp, top_k, top_p, state), trial
+        cases += 1
+    assert cases == 300
+    # invalid arguments and a missing state
+    assert ol.sample_from_topk(np.zeros(0, np.int32), np.zeros(0, F), 1.0, 0, 1.0, 1)[0] == -1
