@@ -142,7 +142,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="sweep", choices=["sweep", "layers", "lm_head", "lm_head_plain", "gemv", "down", "batch16"])
+    ap.add_argument("--workload", default="sweep",
+                    choices=["sweep", "layers", "lm_head", "lm_head_plain", "gemv", "down", "batch16", "lm_head_bf16"])
     ap.add_argument("--rotate-gb", type=float, default=1.0, help="rotating weight copies totalling >= this")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     args = ap.parse_args()
@@ -162,6 +163,8 @@ def main():
     lib.init_kernels()
     if args.workload == "batch16":
         return bench_batch16(args, qk, torch, np)
+    if args.workload == "lm_head_bf16":
+        return bench_lm_head_bf16(args, qk, torch, np)
 
     items = workload_items(args.workload)
     per_copy = sum(wbytes(M, K) for _, M, K, *_ in items)
@@ -327,6 +330,59 @@ def bench_batch16(args, qk, torch, np):
                       "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
                       "us_per_step": round(us, 3), "int_tops": round(intops, 3), "higher_is_better": True,
                       "config": {"workload": "batch16", "M": M, "K": K, "B": B}}))
+
+
+def bench_lm_head_bf16(args, qk, torch, np):
+    """The reference's own lm_head: bf16 tied embedding 65536 x 1024 (134 MB)
+    with the fused top-64 (the chat sampler's k), rotating table copies."""
+    V, H, K = 65536, 1024, 64
+    lib = qk.load()
+    per_copy = V * H * 2
+    copies = max(1, int(np.ceil(args.rotate_gb * 1e9 / per_copy)))
+    tables = []
+    for c in range(copies):
+        g = torch.Generator(device="cuda").manual_seed(100 + c)
+        t = (torch.randn((V, H), device="cuda", generator=g) * 0.05).to(torch.bfloat16)
+        tables.append(t.view(torch.int16))
+    h = torch.randn(H, device="cuda", dtype=torch.float32)
+    ids = torch.empty(K, dtype=torch.int32, device="cuda")
+    sc = torch.empty(K, dtype=torch.float32, device="cuda")
+    cnt = torch.empty(2, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream()
+    s = stream.cuda_stream
+
+    def run(i, k):
+        qk.check(lib.bf16_dev_lm_head(ids.data_ptr(), sc.data_ptr(), cnt.data_ptr(), cnt.data_ptr() + 4, None,
+                                      h.data_ptr(), tables[i % copies].data_ptr(), V, H, k, 1, s))
+
+    for i in range(args.warmup):
+        run(i, K)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        run(i, K)
+    torch.cuda.synchronize()
+    us = (time.perf_counter() - t0) * 1e6 / args.steps
+    # the dot-product kernel alone (scores to a logits buffer, no selection)
+    logits = torch.empty(V, dtype=torch.float32, device="cuda")
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for i in range(args.steps):
+        qk.check(lib.bf16_dev_lm_head(None, None, None, None, logits.data_ptr(), h.data_ptr(),
+                                      tables[i % copies].data_ptr(), V, H, 0, 1, s))
+    b.record(stream)
+    torch.cuda.synchronize()
+    kus = a.elapsed_time(b) * 1e3 / args.steps
+    kbytes = per_copy + H * 4 + V * 4
+    step_bytes = per_copy + H * 4
+    print(json.dumps({"metric": "bf16 lm_head achieved HBM GB/s", "value": round(step_bytes / us / 1e3, 2),
+                      "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+                      "us_per_step": round(us, 2), "higher_is_better": True,
+                      "config": {"workload": "lm_head_bf16", "vocab": V, "hidden": H, "topk": K,
+                                 "rotating_copies": copies},
+                      "kernel": {"name": "bf16_lm_head_kernel", "avg_us": round(kus, 2), "algorithmic_bytes": kbytes},
+                      "roofline": {"bound": "hbm", "achieved": round(kbytes / kus / 1e3, 1), "peak": PEAK_HBM_GBPS,
+                                   "unit": "GB/s", "frac": round(kbytes / kus / 1e3 / PEAK_HBM_GBPS, 4)}}), flush=True)
 
 
 if __name__ == "__main__":

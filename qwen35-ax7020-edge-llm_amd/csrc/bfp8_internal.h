@@ -79,6 +79,7 @@ struct Bfp8TileRef {
 #define BFP8_TOPK_MAX 64
 #define BFP8_TOPK_MAX_TILES 4096
 #define BFP8_SAMPLE_MAX 4096  // candidates the sampler takes
+#define BF16_HEAD_MAX_HIDDEN 4096  // hidden size of the bf16 lm_head (LDS copy of h)
 #define BFP8_STREAM_WG_PER_CU 4
 // Row tiles up to which a GEMV (or a plan's GEMVs) runs one tile per
 // 16-wavefront workgroup instead of the persistent streaming kernel.

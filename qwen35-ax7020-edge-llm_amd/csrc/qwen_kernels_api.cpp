@@ -554,6 +554,10 @@ int bfp8_lm_head_argmax(const float* h, const int8_t* mantissas, const uint8_t* 
 int lm_head_argmax(const float* h, const uint16_t* embed_table, int vocab_size, int hidden_dim) {
     ProfScope ps(QP_LMHEAD);
     if (!h || !embed_table || vocab_size <= 0 || hidden_dim <= 0) return 0;
+    if (hidden_dim > BF16_HEAD_MAX_HIDDEN) {
+        set_error("lm_head_argmax: hidden_dim %d above %d", hidden_dim, BF16_HEAD_MAX_HIDDEN);
+        fatal("lm_head_argmax");
+    }
     std::lock_guard<std::mutex> lk(g.mu);
     int am = 0;
     if (ensure_init_locked() != BFP8_OK ||
@@ -566,8 +570,9 @@ int qwen_lm_head_topk_bf16(const float* h, const uint16_t* embed_table, int voca
                            int* out_ids, float* out_scores) {
     ProfScope ps(QP_LMHEAD);
     if (!h || !embed_table || !out_ids || !out_scores || vocab_size <= 0 || hidden_dim <= 0 || k <= 0) return 0;
-    if (std::min(k, vocab_size) > BFP8_TOPK_MAX) {
-        set_error("lm_head_topk: k = %d above the fused limit %d", k, BFP8_TOPK_MAX);
+    if (std::min(k, vocab_size) > BFP8_TOPK_MAX || hidden_dim > BF16_HEAD_MAX_HIDDEN) {
+        set_error("lm_head_topk: k = %d or hidden_dim = %d above the limits %d, %d", k, hidden_dim, BFP8_TOPK_MAX,
+                  BF16_HEAD_MAX_HIDDEN);
         return 0;
     }
     std::lock_guard<std::mutex> lk(g.mu);
@@ -792,7 +797,8 @@ int bfp8_dev_copy_probe(void* dst, const void* src, size_t bytes, void* stream) 
 int bf16_dev_lm_head(int* out_ids, float* out_scores, int* out_count, int* out_argmax, float* logits,
                      const float* h, const uint16_t* table, int vocab, int hidden, int k, int tail, void* stream) {
     DEV_PROLOGUE();
-    if (!h || !table || vocab <= 0 || hidden <= 0 || k < 0 || std::min(k, vocab) > BFP8_TOPK_MAX ||
+    if (!h || !table || vocab <= 0 || hidden <= 0 || hidden > BF16_HEAD_MAX_HIDDEN || k < 0 ||
+        std::min(k, vocab) > BFP8_TOPK_MAX ||
         (k > 0 && (!out_ids || !out_scores || !out_count || !out_argmax)) || (k == 0 && !logits)) {
         set_error("bf16_dev_lm_head: invalid arguments");
         return BFP8_EINVAL;

@@ -82,10 +82,11 @@ def test_lm_head_argmax_and_topk_host_abi(gpu, head_case):
 def test_ties_ragged_vocab_and_tail_rules(gpu):
     """Duplicated rows (ties broken by the lower id), a vocabulary that is not
     a multiple of 64, and hidden % 8 != 0, where lm_head_argmax drops the
-    trailing elements and lm_head_topk adds them."""
+    trailing elements and lm_head_topk adds them; hidden sizes above one
+    512-byte row slice and up to the 4096 limit."""
     qk = gpu
     lib = qk.load()
-    for vocab, hidden in ((1000, 1000), (4099, 1003), (130, 5), (64, 8)):
+    for vocab, hidden in ((1000, 1000), (4099, 1003), (130, 5), (64, 8), (1500, 1100), (3000, 2048), (300, 4096)):
         table, h = table_and_h(vocab, hidden, vocab + hidden)
         if vocab > 40:
             l1 = ol.bf16_logits(h, table, tail=1)
