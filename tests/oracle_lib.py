@@ -236,3 +236,142 @@ def f32_to_bf16_bits(x):
     b = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
     b = (b + 0x7FFF + ((b >> 16) & 1)) >> 16
     return b.astype(np.uint16)
+
+
+# ---- decode runtime kernels ---------------------------------------------------------
+_RT_BOUND = False
+
+
+def _rt():
+    global _RT_BOUND
+    lib = oracle()
+    if not _RT_BOUND:
+        vp, i, f = c_void_p, c_int, c_float
+        lib.orc_exp_neon.argtypes = [f]
+        lib.orc_exp_neon.restype = f
+        lib.orc_swiglu.argtypes = [vp, vp, vp, i]
+        lib.orc_add_residual.argtypes = [vp, vp, i]
+        lib.orc_rmsnorm.argtypes = [vp, vp, vp, i, f]
+        lib.orc_conv1d_silu.argtypes = [vp, vp, vp, vp, i]
+        lib.orc_qk_l2norm.argtypes = [vp, vp, i, i]
+        lib.orc_gdn_gates.argtypes = [vp, vp, vp, vp, vp, vp, vp, i, i]
+        lib.orc_gdn_step.argtypes = [vp, vp, vp, vp, vp, vp, vp, i, i]
+        lib.orc_rmsnorm_gated.argtypes = [vp, vp, vp, vp, i, i, f]
+        lib.orc_forward_linear_layer.argtypes = [vp, vp]
+        lib.orc_forward_mlp.argtypes = [vp, vp]
+        _RT_BOUND = True
+    return lib
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def exp_neon(x):
+    return _rt().orc_exp_neon(float(x))
+
+
+def swiglu(gate, up):
+    g, u = _f32(gate), _f32(up)
+    y = np.zeros_like(g)
+    _rt().orc_swiglu(_p(y), _p(g), _p(u), g.size)
+    return y
+
+
+def add_residual(x, res):
+    x, r = _f32(x).copy(), _f32(res)
+    _rt().orc_add_residual(_p(x), _p(r), x.size)
+    return x
+
+
+def rmsnorm(x, w, eps=1e-6):
+    x, w = _f32(x), _f32(w)
+    y = np.zeros_like(x)
+    _rt().orc_rmsnorm(_p(y), _p(x), _p(w), x.size, eps)
+    return y
+
+
+def conv1d_silu(x, state, weight):
+    """Returns (y, new state); state [3][C], weight [C][4]."""
+    x, st, w = _f32(x), _f32(state).copy(), _f32(weight)
+    y = np.zeros_like(x)
+    _rt().orc_conv1d_silu(_p(y), _p(x), _p(st), _p(w), x.size)
+    return y, st
+
+
+def qk_l2norm(q, k, H, D):
+    q, k = _f32(q).copy(), _f32(k).copy()
+    _rt().orc_qk_l2norm(_p(q), _p(k), H, D)
+    return q, k
+
+
+def gdn_gates(x, wa, wb, nea, dt):
+    H, K = wa.shape
+    a = np.zeros(H, dtype=np.float32)
+    b = np.zeros(H, dtype=np.float32)
+    _rt().orc_gdn_gates(_p(a), _p(b), _p(_f32(x)), _p(_f32(wa)), _p(_f32(wb)), _p(_f32(nea)), _p(_f32(dt)), H, K)
+    return a, b
+
+
+def gdn_step(S, q, k, v, alpha, beta, H, D):
+    """S: logical state [H][D][D] (row = input index i, column = output j).
+    Returns (out, new S)."""
+    S = _f32(S).copy()
+    out = np.zeros(H * D, dtype=np.float32)
+    _rt().orc_gdn_step(_p(out), _p(S), _p(_f32(q)), _p(_f32(k)), _p(_f32(v)), _p(_f32(alpha)), _p(_f32(beta)), H, D)
+    return out, S
+
+
+def rmsnorm_gated(x, z, w, H, D, eps=1e-6):
+    x, z, w = _f32(x), _f32(z), _f32(w)
+    y = np.zeros_like(x)
+    _rt().orc_rmsnorm_gated(_p(y), _p(x), _p(z), _p(w), H, D, eps)
+    return y
+
+
+def gdn_state_to_blocked(S, H, D):
+    """The reference's internal gdn state layout: block (jg, ig) of 16 floats,
+    state[h][((jg*ng + ig)*4 + l)*4 + t] = S[h][4ig+t][4jg+l]."""
+    S = np.asarray(S, dtype=np.float32).reshape(H, D // 4, 4, D // 4, 4)  # h, ig, t, jg, l
+    return np.ascontiguousarray(S.transpose(0, 3, 1, 4, 2)).reshape(-1)
+
+
+def gdn_state_from_blocked(B, H, D):
+    B = np.asarray(B, dtype=np.float32).reshape(H, D // 4, D // 4, 4, 4)  # h, jg, ig, l, t
+    return np.ascontiguousarray(B.transpose(0, 2, 4, 1, 3)).reshape(H, D, D)
+
+
+def ref_runtime():
+    """The reference host build's runtime kernels (scalar paths)."""
+    lib = ref_kernels()
+    vp, i, f = c_void_p, c_int, c_float
+    lib.rmsnorm.argtypes = [vp, vp, vp, i, f]
+    lib.swiglu.argtypes = [vp, vp, vp, i]
+    lib.add_residual.argtypes = [vp, vp, i]
+    lib.causal_conv1d_update_silu.argtypes = [vp, vp, vp, vp, i]
+    lib.qk_l2norm.argtypes = [vp, vp, i, i]
+    lib.gdn_gates.argtypes = [vp, vp, vp, vp, vp, vp, vp, i, i]
+    lib.gdn_recurrent_step.argtypes = [vp, vp, vp, vp, vp, vp, vp, i, i]
+    lib.rmsnorm_gated.argtypes = [vp, vp, vp, vp, i, i, f]
+    lib.forward_linear_layer.argtypes = [vp, vp]
+    lib.forward_mlp.argtypes = [vp, vp]
+    return lib
+
+
+class LinearPlan(ctypes.Structure):
+    """Field-for-field mirror of LinearLayerPlan (04/qwen_kernels_opt.c:866-901)."""
+    _fields_ = [(n, t) for n, t in [
+        ("in_ln_w", c_void_p), ("mant_qkv", c_void_p), ("exp_qkv", c_void_p), ("M_qkv", c_int), ("K_qkv", c_int),
+        ("conv_w", c_void_p), ("conv_s", c_void_p), ("wa", c_void_p), ("wb", c_void_p), ("nea", c_void_p),
+        ("dt", c_void_p), ("state", c_void_p), ("mant_z", c_void_p), ("exp_z", c_void_p), ("M_z", c_int),
+        ("K_z", c_int), ("norm_w", c_void_p), ("mant_o", c_void_p), ("exp_o", c_void_p), ("M_o", c_int),
+        ("K_o", c_int), ("post_ln_w", c_void_p), ("mant_gate", c_void_p), ("exp_gate", c_void_p),
+        ("M_gate", c_int), ("K_gate", c_int), ("mant_up", c_void_p), ("exp_up", c_void_p), ("M_up", c_int),
+        ("K_up", c_int), ("mant_down", c_void_p), ("exp_down", c_void_p), ("M_down", c_int), ("K_down", c_int)]]
+
+
+class MlpPlan(ctypes.Structure):
+    """Field-for-field mirror of MlpPlan (04/qwen_kernels_opt.c:903-917)."""
+    _fields_ = [("post_ln_w", c_void_p), ("mant_gate", c_void_p), ("exp_gate", c_void_p), ("M_gate", c_int),
+                ("K_gate", c_int), ("mant_up", c_void_p), ("exp_up", c_void_p), ("M_up", c_int), ("K_up", c_int),
+                ("mant_down", c_void_p), ("exp_down", c_void_p), ("M_down", c_int), ("K_down", c_int)]

@@ -391,3 +391,134 @@ def test_sample_from_topk_matches_reference_build():
     assert cases == 300
     # invalid arguments and a missing state
     assert ol.sample_from_topk(np.zeros(0, np.int32), np.zeros(0, F), 1.0, 0, 1.0, 1)[0] == -1
+
+
+# ---- decode runtime kernels (board build) ------------------------------------------------------
+def test_exp_neon_accuracy_and_special_points():
+    """The reference's polynomial exp: close to exp over the clamped range,
+    with the error its range reduction implies (fx = x*log2(e) is rounded
+    once, which moves the result by up to ln 2 * ulp(fx) relative, plus a few
+    ulps of polynomial and rounding); a wrong coefficient or Horner order is
+    off by orders of magnitude.  Exact at 0, clamped outside [-87, 88], NaN
+    propagates."""
+    xs = np.linspace(-87.0, 88.0, 200001, dtype=np.float32)[::7]
+    got = np.array([ol.exp_neon(x) for x in xs], dtype=np.float64)
+    ref = np.exp(xs.astype(np.float64))
+    fx = np.abs(xs.astype(np.float64)) * 1.4426950408889634
+    ulp_fx = np.spacing(fx.astype(np.float32)).astype(np.float64)
+    assert np.all(np.abs(got / ref - 1.0) <= 1e-6 + 0.7 * ulp_fx)
+    assert ol.exp_neon(0.0) == 1.0
+    assert ol.exp_neon(np.inf) == ol.exp_neon(88.0) and ol.exp_neon(-np.inf) == ol.exp_neon(-87.0)
+    assert ol.exp_neon(1000.0) == ol.exp_neon(88.0) and ol.exp_neon(-1000.0) == ol.exp_neon(-87.0)
+    assert math.isnan(ol.exp_neon(float("nan")))
+
+
+def test_swiglu_formula_and_scalar_tail():
+    rng = np.random.default_rng(21)
+    g = rng.standard_normal(1027).astype(F) * F(3)
+    u = rng.standard_normal(1027).astype(F)
+    y = ol.swiglu(g, u)
+    ref = g.astype(np.float64) / (1.0 + np.exp(-g.astype(np.float64))) * u
+    assert np.all(np.abs(y - ref) <= 4e-6 * np.abs(ref) + 1e-30)
+    if ol.ref_available():  # the last n % 4 elements are the reference's scalar code
+        yr = np.zeros_like(g)
+        ol.ref_runtime().swiglu(ol._p(yr), ol._p(g), ol._p(u), g.size)
+        assert np.array_equal(y[1024:].view(np.uint32), yr[1024:].view(np.uint32))
+
+
+def test_rmsnorm_lane_order_and_formulas():
+    n = 64
+    x = np.zeros(n, dtype=F)
+    x[0], x[1], x[2], x[3] = 4096.0, 1.0, 1.0, 1.0  # squares (2^24, 1, 1, 1) in lanes 0..3
+    y = ol.rmsnorm(x, np.zeros(n, dtype=F))
+    ss = F(2.0**24 + 2)                               # (2^24 + 1) + (1 + 1); left to right gives 2^24
+    r = F(1.0) / np.sqrt(F(ss / F(n)) + F(1e-6))
+    assert y[1] == F(F(1.0) * F(r * F(1.0)))
+    if ol.ref_available():
+        rng = np.random.default_rng(22)
+        xi = rng.integers(-30, 31, 1027).astype(F)  # exact sums of squares: every order agrees
+        w = np.zeros(1027, dtype=F)                  # x * (r * 1) == (x * r) * 1
+        yr = np.zeros_like(xi)
+        ol.ref_runtime().rmsnorm(ol._p(yr), ol._p(xi), ol._p(w), xi.size, F(1e-6))
+        assert np.array_equal(ol.rmsnorm(xi, w).view(np.uint32), yr.view(np.uint32))
+
+
+@pytest.mark.skipif(not ol.ref_available(), reason="oracle/_ref needs the reference sources")
+def test_qk_l2norm_gates_and_gated_norm_against_reference_build_on_exact_sums():
+    rng = np.random.default_rng(23)
+    H, D, K = 16, 128, 1024
+    rt = ol.ref_runtime()
+    q = rng.integers(-9, 10, H * D).astype(F)
+    k = rng.integers(-9, 10, H * D).astype(F)
+    q2, k2 = ol.qk_l2norm(q, k, H, D)
+    qr, kr = q.copy(), k.copy()
+    rt.qk_l2norm(ol._p(qr), ol._p(kr), H, D)
+    assert np.array_equal(q2.view(np.uint32), qr.view(np.uint32)) and np.array_equal(k2.view(np.uint32), kr.view(np.uint32))
+    x = rng.integers(-4, 5, K).astype(F)
+    wa = rng.integers(-4, 5, (H, K)).astype(F) * F(1.0 / 1024)
+    wb = rng.integers(-4, 5, (H, K)).astype(F) * F(1.0 / 1024)
+    nea = -np.exp(rng.standard_normal(H)).astype(F)
+    dt = rng.standard_normal(H).astype(F)
+    a, b = ol.gdn_gates(x, wa, wb, nea, dt)
+    ar, br = np.zeros(H, F), np.zeros(H, F)
+    rt.gdn_gates(ol._p(ar), ol._p(br), ol._p(x), ol._p(wa), ol._p(wb), ol._p(nea), ol._p(dt), H, K)
+    assert np.array_equal(a.view(np.uint32), ar.view(np.uint32)) and np.array_equal(b.view(np.uint32), br.view(np.uint32))
+    xg = rng.integers(-9, 10, H * D).astype(F)
+    z = rng.standard_normal(H * D).astype(F)
+    w = rng.standard_normal(D).astype(F)
+    yg = ol.rmsnorm_gated(xg, z, w, H, D)
+    yr = np.zeros_like(xg)
+    rt.rmsnorm_gated(ol._p(yr), ol._p(xg), ol._p(z), ol._p(w), H, D, F(1e-6))
+    assert np.array_equal(yg.view(np.uint32), yr.view(np.uint32))
+
+
+@pytest.mark.skipif(not ol.ref_available(), reason="oracle/_ref needs the reference sources")
+def test_gdn_step_matches_reference_build():
+    """Same operation order as the reference's blocked kernel (its scalar
+    host path), with q, k integer-valued so that q.k is exact in any order;
+    the state goes through the reference's internal layout."""
+    rng = np.random.default_rng(24)
+    H, D = 16, 128
+    S = rng.standard_normal((H, D, D)).astype(F) * F(0.1)
+    q = rng.integers(-3, 4, H * D).astype(F)
+    k = rng.integers(-3, 4, H * D).astype(F)
+    v = rng.standard_normal(H * D).astype(F)
+    a = rng.uniform(0.5, 1.0, H).astype(F)
+    b = rng.uniform(0.0, 1.0, H).astype(F)
+    out, S2 = ol.gdn_step(S, q, k, v, a, b, H, D)
+    blk = ol.gdn_state_to_blocked(S, H, D)
+    assert np.array_equal(ol.gdn_state_from_blocked(blk, H, D), S)
+    o_r = np.zeros(H * D, F)
+    ol.ref_runtime().gdn_recurrent_step(ol._p(o_r), ol._p(blk), ol._p(q), ol._p(k), ol._p(v), ol._p(a), ol._p(b), H, D)
+    assert np.array_equal(out.view(np.uint32), o_r.view(np.uint32))
+    assert np.array_equal(S2.view(np.uint32), ol.gdn_state_from_blocked(blk, H, D).view(np.uint32))
+
+
+def test_conv1d_silu_dot_order_state_shift_and_tail():
+    rng = np.random.default_rng(25)
+    C = 6147
+    x = rng.standard_normal(C).astype(F)
+    st = rng.standard_normal((3, C)).astype(F)
+    wt = rng.standard_normal((C, 4)).astype(F)
+    y, st2 = ol.conv1d_silu(x, st, wt)
+    assert np.array_equal(st2[0], st[1]) and np.array_equal(st2[1], st[2]) and np.array_equal(st2[2], x)
+    d = (((wt[:, 0] * st[0]).astype(F) + (wt[:, 1] * st[1]).astype(F)).astype(F) + (wt[:, 2] * st[2]).astype(F)).astype(F)
+    d = (d + (wt[:, 3] * x).astype(F)).astype(F)
+    ref = d.astype(np.float64) / (1.0 + np.exp(-d.astype(np.float64)))
+    assert np.all(np.abs(y[:6144] - ref[:6144]) <= 4e-6 * np.abs(ref[:6144]) + 1e-30)
+    if ol.ref_available():
+        # the host build compiles only the scalar tail loop (it starts at
+        # channels & ~3; the vector body is NEON-only), so only the tail
+        # channels are comparable
+        yr = np.zeros_like(x)
+        sr = st.copy()
+        ol.ref_runtime().causal_conv1d_update_silu(ol._p(yr), ol._p(x), ol._p(sr), ol._p(wt), C)
+        assert np.array_equal(yr[6144:].view(np.uint32), y[6144:].view(np.uint32))
+        assert np.array_equal(sr[:, 6144:], st2[:, 6144:])
+
+
+def test_add_residual_is_elementwise_sum():
+    rng = np.random.default_rng(26)
+    x = rng.standard_normal(1027).astype(F)
+    r = rng.standard_normal(1027).astype(F)
+    assert np.array_equal(ol.add_residual(x, r), (x + r).astype(F))
