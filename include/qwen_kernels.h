@@ -69,14 +69,82 @@ void bfp8_gemv(float* y, const float* x, const int8_t* mantissas, const uint8_t*
  * first call. */
 int lm_head_argmax(const float* h, const uint16_t* embed_table, int vocab_size, int hidden_dim);
 
-/* Replace the stage profiler, 04/qwen_kernels_opt.c:87-91 (same 15 slots and
- * names).  Slot 0 (bfp8_gemv) accumulates wall milliseconds of bfp8_gemv and
- * bfp8_gemv_batch; slot 1 (lm_head_argmax) of the fused lm_head calls. */
+/* Replace the stage profiler, 04/qwen_kernels_opt.c:63-101 (same 15 slots,
+ * names and order).  As in the reference, only forward_linear_layer,
+ * forward_mlp and forward_token_c accumulate into the slots: wall
+ * milliseconds per step, each step synchronised while profiling is on.  The
+ * forward's fused linear-attention kernel (conv1d, q/k norm, gates, recurrent
+ * step, gated norm) is booked to gdn_recurrent_step, residual adds fused into
+ * the next norm to rmsnorm. */
 void qwen_prof_enable(int on);
 void qwen_prof_reset(void);
 int qwen_prof_count(void);
 double qwen_prof_get(int i);
 const char* qwen_prof_name(int i);
+
+/* The decode runtime around the GEMV (04/qwen_kernels_opt.c), host pointers,
+ * synchronous, same arguments and results as the board build: Advanced SIMD
+ * steps in flush-to-zero float arithmetic in the reference's lane order,
+ * scalar steps in IEEE arithmetic; expf / log1pf are computed as exp / log1p
+ * in double rounded to float (the board's libm is within an ulp of that). */
+void rmsnorm(float* y, const float* x, const float* w, int n, float eps);             /* :140-175 */
+void swiglu(float* y, const float* gate, const float* up, int n);                      /* :365-384 */
+void add_residual(float* x, const float* res, int n);                                  /* :388-395 */
+void causal_conv1d_update_silu(float* y, const float* x, float* conv_state, const float* weight,
+                               int channels);                                          /* :511-542 */
+void qk_l2norm(float* q, float* k, int num_heads, int head_dim);                      /* :548-588 */
+void gdn_gates(float* alpha, float* beta, const float* x, const float* wa, const float* wb,
+               const float* neg_exp_alog, const float* dt, int H, int K);             /* :593-620 */
+/* state: the reference's blocked layout (:637-650), num_heads x head_dim^2
+ * floats; head_dim must be a multiple of 4 and at most 4096 (the board's
+ * vector path assumes the former). */
+void gdn_recurrent_step(float* attn_out, float* state, const float* q, const float* k, const float* v,
+                        const float* alpha, const float* beta, int num_heads, int head_dim);  /* :664-813 */
+void rmsnorm_gated(float* y, const float* x, const float* z, const float* norm_w, int num_heads,
+                   int head_dim, float eps);                                           /* :832-847 */
+
+/* The compiled forward loop, 04/qwen_kernels_opt.c:866-1049.  The plan
+ * structs have the reference's fields, order and layout (the engine's ctypes
+ * mirrors, 04/qwen_real_engine.py:20-74).  Shapes are the model's: hidden
+ * 1024, 16 linear-attention heads of 128, conv channels 6144, MLP 3584,
+ * vocabulary 65536; a plan with other GEMV shapes aborts.  Weights and
+ * parameters are converted to device copies on first use and treated as
+ * immutable afterwards (bfp8_cache_clear() drops them); the conv and
+ * recurrent states follow qwen_forward_state_resident(). */
+typedef struct LinearLayerPlan {
+    const float* in_ln_w;
+    const int8_t* mant_qkv; const uint8_t* exp_qkv; int M_qkv; int K_qkv;
+    const float* conv_w; float* conv_s;
+    const float* wa; const float* wb; const float* nea; const float* dt;
+    float* state;
+    const int8_t* mant_z; const uint8_t* exp_z; int M_z; int K_z;
+    const float* norm_w;
+    const int8_t* mant_o; const uint8_t* exp_o; int M_o; int K_o;
+    const float* post_ln_w;
+    const int8_t* mant_gate; const uint8_t* exp_gate; int M_gate; int K_gate;
+    const int8_t* mant_up; const uint8_t* exp_up; int M_up; int K_up;
+    const int8_t* mant_down; const uint8_t* exp_down; int M_down; int K_down;
+} LinearLayerPlan;
+
+typedef struct MlpPlan {
+    const float* post_ln_w;
+    const int8_t* mant_gate; const uint8_t* exp_gate; int M_gate; int K_gate;
+    const int8_t* mant_up; const uint8_t* exp_up; int M_up; int K_up;
+    const int8_t* mant_down; const uint8_t* exp_down; int M_down; int K_down;
+} MlpPlan;
+
+/* 04/qwen_kernels_opt.c:1006; called with the library unlocked, so it may
+ * call back into this library (the engine's attention runs bfp8_gemv). */
+typedef void (*FullAttnCallback)(int layer_idx, float* h, void* py_context);
+
+void forward_linear_layer(const LinearLayerPlan* p, float* h);                        /* :938-992 */
+void forward_mlp(const MlpPlan* p, float* h);                                         /* :994-1004 */
+/* :1008-1049: embedding row token_id % 65536 (a negative remainder wraps),
+ * 24 layers (full-attention layers: the callback on h, then the MLP), final
+ * rmsnorm, lm_head_argmax over 65536 x 1024; h ends as the last hidden state. */
+int forward_token_c(int token_id, float* h, const LinearLayerPlan* linear_plans, const MlpPlan* mlp_plans,
+                    const int* layer_is_full, const float* final_norm_w, const uint16_t* embed_table,
+                    FullAttnCallback full_attn_cb, void* py_context);
 
 /* ---- 2. new host-pointer symbols ------------------------------------------- */
 
@@ -109,10 +177,24 @@ int qwen_lm_head_topk_bf16(const float* h, const uint16_t* embed_table, int voca
 int qwen_sample_from_topk(const int* ids, const float* scores, int n, float temperature, int top_k, float top_p,
                           unsigned int* rng_state);
 
+/* Where the forward keeps the layers' conv and recurrent states.
+ * 0 (default): in the caller's buffers, as the reference does: every
+ * forward call copies them to the device and back.  1: on the device, after
+ * one copy from the caller's buffers when a layer is first seen; the caller's
+ * buffers are then neither read nor written, qwen_forward_reset_state()
+ * zeroes the device states (what the engine's reset_state does to its
+ * buffers, 04/qwen_real_engine.py:808-813) and qwen_forward_sync_state()
+ * copies them back.  Switching to 0 copies them back first.  Returns the
+ * previous mode. */
+int qwen_forward_state_resident(int on);
+void qwen_forward_reset_state(void);
+void qwen_forward_sync_state(void);
+
 /* Message of the most recent failure of this library ("" if none). */
 const char* bfp8_last_error(void);
 
-/* Drops every cached device copy of read-only weights. */
+/* Drops every cached device copy of weights and forward parameters (and
+ * the forward's device states, resident ones included). */
 void bfp8_cache_clear(void);
 
 /* ---- 3. device-level symbols ------------------------------------------------ */

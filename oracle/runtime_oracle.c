@@ -9,7 +9,8 @@
  * Vector arithmetic uses orc_neon_mul / orc_neon_add (flush-to-zero, one
  * rounding each); vmlaq_f32(a, b, c) is a + b*c with the product rounded
  * first.  Scalar code (VFP: IEEE subnormals) is plain C compiled with
- * -ffp-contract=off; expf, log1pf and sqrtf are the host C library's.
+ * -ffp-contract=off; sqrtf is the host C library's, expf / log1pf see
+ * o_expf below.
  *
  * Pinning (tests/test_oracle.py):
  *   orc_exp_neon        relative error bound against exp over [-87, 88],
@@ -23,6 +24,8 @@
  *                       state layout converted) on normal data
  *   orc_swiglu / orc_conv1d_silu  per-element formula with exp_neon, vs a
  *                       float64 bound; tails vs the reference host build
+ *   o_expf / o_log1pf   host libm by default; correctly rounded in
+ *                       orc_set_cr_libm(1) mode (checked against float64)
  */
 #include <float.h>
 #include <math.h>
@@ -38,6 +41,16 @@ float orc_bf16_dot(const float* h, const uint16_t* row, int hidden, int tail);
 int orc_argmax(const float* logits, int n);
 
 static float nsub(float a, float b) { return orc_neon_add(a, -b); }
+
+/* The reference's scalar code calls libm expf / log1pf.  By default the
+ * oracle uses the host C library's; orc_set_cr_libm(1) switches to exp /
+ * log1p in double rounded once to float (correctly rounded except within
+ * 2^-29 of a rounding boundary), the definition the GPU implements, so that
+ * whole-layer comparisons can be bit for bit. */
+static int g_cr_libm = 0;
+void orc_set_cr_libm(int on) { g_cr_libm = on; }
+static float o_expf(float x) { return g_cr_libm ? (float)exp((double)x) : expf(x); }
+static float o_log1pf(float x) { return g_cr_libm ? (float)log1p((double)x) : log1pf(x); }
 
 /* Advanced SIMD vmaxq/vminq: a NaN operand gives the default NaN. */
 static float nmax(float a, float b) { return (isnan(a) || isnan(b)) ? NAN : (a > b ? a : b); }
@@ -87,7 +100,7 @@ void orc_swiglu(float* y, const float* gate, const float* up, int n) {
     }
     for (; i < n; i++) {
         const float g = gate[i];
-        y[i] = (g / (1.0f + expf(-g))) * up[i];
+        y[i] = (g / (1.0f + o_expf(-g))) * up[i];
     }
 }
 
@@ -137,7 +150,7 @@ void orc_conv1d_silu(float* y, const float* x, float* st, const float* wt, int C
     for (; c < C; c++) {
         const float xc = x[c];
         const float dot = wt[c * 4] * s0[c] + wt[c * 4 + 1] * s1[c] + wt[c * 4 + 2] * s2[c] + wt[c * 4 + 3] * xc;
-        y[c] = dot / (1.0f + expf(-dot));
+        y[c] = dot / (1.0f + o_expf(-dot));
         s0[c] = s1[c];
         s1[c] = s2[c];
         s2[c] = xc;
@@ -193,9 +206,9 @@ void orc_gdn_gates(float* alpha, float* beta, const float* x, const float* wa, c
             av += ra[i] * x[i];
             bv += rb[i] * x[i];
         }
-        beta[h] = 1.0f / (1.0f + expf(-bv));
+        beta[h] = 1.0f / (1.0f + o_expf(-bv));
         const float z = av + dt[h];
-        alpha[h] = expf(nea[h] * log1pf(expf(z)));
+        alpha[h] = o_expf(nea[h] * o_log1pf(o_expf(z)));
     }
 }
 
@@ -249,7 +262,7 @@ void orc_rmsnorm_gated(float* y, const float* x, const float* z, const float* w,
         const float r = 1.0f / sqrtf((ss / (float)D) + eps);
         for (i = 0; i < D; i++) {
             const float zi = zh[i];
-            yh[i] = xh[i] * r * w[i] * (zi / (1.0f + expf(-zi)));
+            yh[i] = xh[i] * r * w[i] * (zi / (1.0f + o_expf(-zi)));
         }
     }
 }

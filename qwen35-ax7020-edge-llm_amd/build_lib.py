@@ -5,7 +5,10 @@
 Translation units:
   csrc/bfp8_ftz.hip          GEMV kernels, f32 flush-to-zero (Advanced SIMD semantics)
   csrc/bfp8_ieee.hip         quantizer / scalar-order kernels, IEEE subnormals
+  csrc/bf16_head.hip         bf16 tied-embedding lm_head, f32 flush-to-zero
+  csrc/runtime_ftz.hip       decode runtime kernels (norms, conv, GDN, swiglu), f32 flush-to-zero
   csrc/qwen_kernels_api.cpp  C ABI host code (include/qwen_kernels.h)
+  csrc/qwen_runtime_api.cpp  C ABI of the runtime kernels and the forward loop
 
 Every device TU is built with -ffp-contract=off (no fused multiply-add: the
 reference rounds every product and sum) and without packed FP32 ops.
@@ -36,8 +39,10 @@ COMMON = [
 UNITS = {
     "bfp8_ftz.hip": ["-fgpu-flush-denormals-to-zero"],
     "bf16_head.hip": ["-fgpu-flush-denormals-to-zero"],
+    "runtime_ftz.hip": ["-fgpu-flush-denormals-to-zero"],
     "bfp8_ieee.hip": [],
     "qwen_kernels_api.cpp": [],
+    "qwen_runtime_api.cpp": [],
 }
 
 

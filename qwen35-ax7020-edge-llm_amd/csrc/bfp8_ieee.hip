@@ -7,51 +7,21 @@
 #include <hip/hip_runtime.h>
 
 #include "bfp8_internal.h"
+#include "quant_block.h"
 
 namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // ---- activation quantizer, 04/qwen_kernels_opt.c:182-205 ------------------
-// One wavefront per 64-element block.
-//   amax = max |x| over the block (a NaN never wins `v > amax`)
-//   amax > 1e-20:  q = 16384/amax, xscale = amax/16384, xq = (int16)lrintf(x*q)
-//   otherwise:     xscale = 0, xq = 0
-// and the split xq = 256*xh + xl written in the residue-major record
-// (bfp8_layout.h) that the GEMV kernels read with scalar loads.
+// One wavefront per 64-element block (quant_block.h).
 __device__ __forceinline__ void quantize_block(const Bfp8QuantDesc& d, int b) {
     const int nb = d.K >> 6;
     if (b >= nb) return;
-    const int i = threadIdx.x;
-    const float xv = d.x[(size_t)b * 64 + i];
-    const float v = fabsf(xv);
-    float amax = (v > 0.0f) ? v : 0.0f;
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-        const float o = __shfl_xor(amax, m, 64);
-        amax = (o > amax) ? o : amax;
-    }
-    int xq = 0;
-    float xs = 0.0f;
-    if (amax > 1e-20f) {
-        const float q = __fdiv_rn(16384.0f, amax);
-        xs = __fdiv_rn(amax, 16384.0f);
-        const float p = __fmul_rn(xv, q);
-        // lrintf rounds half to even; a NaN product (x NaN, or inf*0) gives 0.
-        xq = (p == p) ? (int)__builtin_rintf(p) : 0;
-    }
-    if (d.xq) d.xq[(size_t)b * 64 + i] = (int16_t)xq;
-    if (i == 0) d.xscale[b] = xs;
-    const int xl = (int)(int8_t)(xq & 0xff);
-    const int xh = (xq - xl) >> 8;
-    const int res = i & 3, ii = i >> 2;
-    const int pos = res * 32 + (ii >> 2) * 4 + (ii & 3);
     __shared__ uint32_t rec[32];
-    uint8_t* rb = reinterpret_cast<uint8_t*>(rec);
-    rb[pos] = (uint8_t)xh;
-    rb[pos + 16] = (uint8_t)xl;
-    __syncthreads();
-    if (i < 32) d.xsplit[(size_t)b * 32 + i] = rec[i];
+    const int i = threadIdx.x;
+    bfp8_quant_block_wave(d.x[(size_t)b * 64 + i], i, d.xq ? d.xq + (size_t)b * 64 : nullptr, d.xscale + b,
+                          d.xsplit + (size_t)b * 32, rec);
 }
 
 // Residue sum from a 16-byte residue chunk and the split activation record.

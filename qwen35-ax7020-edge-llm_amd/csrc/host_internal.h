@@ -1,0 +1,159 @@
+// host_internal.h -- host-side state and helpers shared by the C-ABI
+// translation units (qwen_kernels_api.cpp, qwen_runtime_api.cpp).  Not part
+// of the public ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <map>
+#include <mutex>
+#include <string>
+#include <tuple>
+#include <vector>
+
+#include "bfp8_internal.h"
+#include "qwen_kernels.h"
+
+namespace qhost {
+
+// ---- errors -----------------------------------------------------------------------
+void set_error(const char* fmt, ...);
+// Prints the last error and aborts: void entry points have no error channel
+// and there is no CPU fallback.
+[[noreturn]] void fatal(const char* where);
+
+#define HIP_OK(expr)                                                                   \
+    do {                                                                               \
+        hipError_t e_ = (expr);                                                        \
+        if (e_ != hipSuccess) {                                                        \
+            set_error("%s: %s (%s:%d)", #expr, hipGetErrorString(e_), __FILE__, __LINE__); \
+            return BFP8_EHIP;                                                          \
+        }                                                                              \
+    } while (0)
+
+// ---- profiler slots: 04/qwen_kernels_opt.c:71-82 ------------------------------------
+enum {
+    QP_GEMV = 0, QP_LMHEAD, QP_GDN, QP_CONV, QP_SWIGLU, QP_RMSNORM,
+    QP_GATES, QP_QK, QP_GATED, QP_RESID, QP_EMBED, QP_PYCALLBACK,
+    QP_LINEAR, QP_MLP, QP_TOTAL, QP_N
+};
+extern const char* const kProfNames[QP_N];
+extern int g_prof_on;
+extern double g_prof_ms[QP_N];
+double now_ms();
+
+struct ProfScope {
+    int slot;
+    double t0;
+    explicit ProfScope(int s) : slot(s), t0(g_prof_on ? now_ms() : 0.0) {}
+    ~ProfScope() {
+        if (g_prof_on) g_prof_ms[slot] += now_ms() - t0;
+    }
+};
+
+// ---- device buffers -------------------------------------------------------------------
+struct DevBuf {
+    void* p = nullptr;
+    size_t n = 0;
+    int reserve(size_t bytes) {
+        if (bytes <= n) return BFP8_OK;
+        if (p) HIP_OK(hipFree(p));
+        p = nullptr;
+        n = 0;
+        size_t want = std::max<size_t>(bytes, 256);
+        HIP_OK(hipMalloc(&p, want));
+        n = want;
+        return BFP8_OK;
+    }
+    void release() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        n = 0;
+    }
+    template <class T>
+    T* as() const {
+        return static_cast<T*>(p);
+    }
+};
+
+struct PinnedBuf {
+    void* p = nullptr;
+    size_t n = 0;
+    int reserve(size_t bytes) {
+        if (bytes <= n) return BFP8_OK;
+        if (p) HIP_OK(hipHostFree(p));
+        p = nullptr;
+        n = 0;
+        size_t want = std::max<size_t>(bytes, 4096);
+        HIP_OK(hipHostMalloc(&p, want, hipHostMallocDefault));
+        n = want;
+        return BFP8_OK;
+    }
+};
+
+struct CachedWeights {
+    DevBuf mant, exps;
+};
+
+using WeightKey = std::tuple<const void*, const void*, int, int>;
+
+struct State {
+    std::mutex mu;
+    bool ready = false;
+    int device = 0;
+    hipStream_t stream = nullptr;
+    PinnedBuf h_in, h_out;
+    DevBuf x, xq, xscale, xsplit, y;            // activation / output workspace
+    DevBuf soa_m, soa_e, gpu_m, gpu_e;          // per-call weight upload
+    DevBuf tk_partials, tk_out;                 // fused lm_head workspace
+    DevBuf bf16_ws;                             // per-call bf16 table upload
+    DevBuf smp_in, smp_work, smp_out;           // sampler inputs / scratch / outputs
+    PinnedBuf smp_h;
+    DevBuf rt_dev;                              // runtime host-call arena (device)
+    PinnedBuf rt_pin;                           // runtime host-call arena (pinned)
+    std::map<WeightKey, CachedWeights> cache;
+    std::map<WeightKey, DevBuf> bf16_cache;     // read-only bf16 embedding tables
+    size_t cache_bytes = 0;
+};
+
+extern State g;
+
+int ensure_init_locked();
+// Device-level entry points run on the caller's stream; NULL is the HIP
+// default (null) stream, as everywhere in HIP.
+inline hipStream_t pick_stream(void* s) { return static_cast<hipStream_t>(s); }
+// Is every page of [p, p+n) mapped without write permission?
+bool range_readonly(const void* p, size_t n);
+
+struct DevWeights {
+    const uint8_t* mant;
+    const uint8_t* exps;
+};
+
+// Device GPU-layout planes for host reference planes: cached when the planes
+// are read-only (the engine's mmap), else converted into a per-call buffer.
+int weights_for(const int8_t* mant, const uint8_t* exps, int M, int K, DevWeights* out);
+// Device copy of a host bf16 table [vocab][hidden] (cached when read-only).
+int bf16_table_for(const uint16_t* table, int vocab, int hidden, const uint16_t** out);
+// bf16 lm_head scores (+ fused top-k) on device buffers.
+int bf16_lm_head_dev(int* ids, float* scores, int* count, int* argmax, float* logits, const float* h,
+                     const uint16_t* table, int vocab, int hidden, int k, int tail, hipStream_t s);
+Bfp8GemvDesc plain_desc(float* y, const uint32_t* xsplit, const float* xscale, const uint8_t* m,
+                        const uint8_t* e, int M, int K, int32_t* lanes);
+
+// One grouped launch: its tile table, either dealt over a persistent grid
+// (wg_off per workgroup) or one tile per 16-wavefront workgroup (wide).
+struct Launch {
+    DevBuf tiles, wg_off;
+    int nwg = 0;
+    bool wide = false;
+    int ntiles = 0, max_nb = 0;
+};
+
+// Drops the forward's device copies (qwen_runtime_api.cpp); g.mu held.
+void forward_cache_clear();
+
+// Deals the tiles of items[idx] over a launch (persistent or wide).
+int deal_tiles(Launch& L, const std::vector<int>& idx, const bfp8_plan_item* items, int wg0_extra, bool allow_wide);
+
+}  // namespace qhost

@@ -19,10 +19,9 @@
 #include <tuple>
 #include <vector>
 
-#include "bfp8_internal.h"
-#include "qwen_kernels.h"
+#include "host_internal.h"
 
-namespace {
+namespace qhost {
 
 // ---- errors ---------------------------------------------------------------------
 std::mutex g_err_mu;
@@ -50,17 +49,7 @@ void set_error(const char* fmt, ...) {
     abort();
 }
 
-#define HIP_OK(expr)                                                                   \
-    do {                                                                               \
-        hipError_t e_ = (expr);                                                        \
-        if (e_ != hipSuccess) {                                                        \
-            set_error("%s: %s (%s:%d)", #expr, hipGetErrorString(e_), __FILE__, __LINE__); \
-            return BFP8_EHIP;                                                          \
-        }                                                                              \
-    } while (0)
-
-// ---- profiler slots: names and order of 04/qwen_kernels_opt.c:66-78 ----------------
-enum { QP_GEMV = 0, QP_LMHEAD = 1, QP_N = 15 };
+// ---- profiler slots (names in the reference's order) -----------------------------
 const char* const kProfNames[QP_N] = {
     "bfp8_gemv", "lm_head_argmax", "gdn_recurrent_step", "conv1d_silu", "swiglu", "rmsnorm",
     "gdn_gates", "qk_l2norm", "rmsnorm_gated", "add_residual", "embed_lookup", "py_full_attn",
@@ -74,77 +63,6 @@ double now_ms() {
     return (double)ts.tv_sec * 1e3 + (double)ts.tv_nsec / 1e6;
 }
 
-struct ProfScope {
-    int slot;
-    double t0;
-    explicit ProfScope(int s) : slot(s), t0(g_prof_on ? now_ms() : 0.0) {}
-    ~ProfScope() {
-        if (g_prof_on) g_prof_ms[slot] += now_ms() - t0;
-    }
-};
-
-// ---- device buffers -------------------------------------------------------------------
-struct DevBuf {
-    void* p = nullptr;
-    size_t n = 0;
-    int reserve(size_t bytes) {
-        if (bytes <= n) return BFP8_OK;
-        if (p) HIP_OK(hipFree(p));
-        p = nullptr;
-        n = 0;
-        size_t want = std::max<size_t>(bytes, 256);
-        HIP_OK(hipMalloc(&p, want));
-        n = want;
-        return BFP8_OK;
-    }
-    void release() {
-        if (p) (void)hipFree(p);
-        p = nullptr;
-        n = 0;
-    }
-    template <class T>
-    T* as() const {
-        return static_cast<T*>(p);
-    }
-};
-
-struct PinnedBuf {
-    void* p = nullptr;
-    size_t n = 0;
-    int reserve(size_t bytes) {
-        if (bytes <= n) return BFP8_OK;
-        if (p) HIP_OK(hipHostFree(p));
-        p = nullptr;
-        n = 0;
-        size_t want = std::max<size_t>(bytes, 4096);
-        HIP_OK(hipHostMalloc(&p, want, hipHostMallocDefault));
-        n = want;
-        return BFP8_OK;
-    }
-};
-
-struct CachedWeights {
-    DevBuf mant, exps;
-};
-
-using WeightKey = std::tuple<const void*, const void*, int, int>;
-
-struct State {
-    std::mutex mu;
-    bool ready = false;
-    int device = 0;
-    hipStream_t stream = nullptr;
-    PinnedBuf h_in, h_out;
-    DevBuf x, xq, xscale, xsplit, y;            // activation / output workspace
-    DevBuf soa_m, soa_e, gpu_m, gpu_e;          // per-call weight upload
-    DevBuf tk_partials, tk_out;                 // fused lm_head workspace
-    DevBuf bf16_ws;                             // per-call bf16 table upload
-    DevBuf smp_in, smp_work, smp_out;           // sampler inputs / scratch / outputs
-    PinnedBuf smp_h;
-    std::map<WeightKey, CachedWeights> cache;
-    std::map<WeightKey, DevBuf> bf16_cache;     // read-only bf16 embedding tables
-    size_t cache_bytes = 0;
-};
 
 State g;
 constexpr size_t kCacheLimit = (size_t)200 << 30;
@@ -163,11 +81,6 @@ int ensure_init_locked() {
     return BFP8_OK;
 }
 
-// Device-level entry points run on the caller's stream; NULL is the HIP
-// default (null) stream, as everywhere in HIP.
-hipStream_t pick_stream(void* s) { return static_cast<hipStream_t>(s); }
-
-// Is every page of [p, p+n) mapped without write permission?
 bool range_readonly(const void* p, size_t n) {
     if (!p || n == 0) return false;
     FILE* f = fopen("/proc/self/maps", "r");
@@ -190,11 +103,6 @@ bool range_readonly(const void* p, size_t n) {
     fclose(f);
     return ok;
 }
-
-struct DevWeights {
-    const uint8_t* mant;
-    const uint8_t* exps;
-};
 
 // Device GPU-layout planes for host reference planes.
 int weights_for(const int8_t* mant, const uint8_t* exps, int M, int K, DevWeights* out) {
@@ -446,7 +354,9 @@ double normal_at(uint64_t seed, uint64_t i) {
     return std::sqrt(-2.0 * std::log(u1)) * std::cos(6.283185307179586 * u2);
 }
 
-}  // namespace
+}  // namespace qhost
+
+using namespace qhost;
 
 // =========================== C ABI ================================================
 extern "C" {
@@ -457,7 +367,6 @@ void init_kernels(void) {
 }
 
 void bfp8_gemv(float* y, const float* x, const int8_t* mantissas, const uint8_t* exps, int M, int K) {
-    ProfScope ps(QP_GEMV);
     if (M <= 0) return;
     std::lock_guard<std::mutex> lk(g.mu);
     if (ensure_init_locked() != BFP8_OK || host_gemv(y, x, mantissas, exps, M, K) != BFP8_OK)
@@ -466,7 +375,6 @@ void bfp8_gemv(float* y, const float* x, const int8_t* mantissas, const uint8_t*
 
 void bfp8_gemv_batch(float* Y, const float* X, const int8_t* mantissas, const uint8_t* exps, int M, int K,
                      int B) {
-    ProfScope ps(QP_GEMV);
     if (M <= 0 || B <= 0) return;
     std::lock_guard<std::mutex> lk(g.mu);
     if (ensure_init_locked() != BFP8_OK) fatal("bfp8_gemv_batch");
@@ -533,7 +441,6 @@ void bfp8_gemv_batch(float* Y, const float* X, const int8_t* mantissas, const ui
 
 int bfp8_lm_head_topk(const float* h, const int8_t* mantissas, const uint8_t* exps, int vocab, int hidden,
                       int k, int* out_ids, float* out_scores) {
-    ProfScope ps(QP_LMHEAD);
     if (!h || !mantissas || !exps || !out_ids || !out_scores || !lm_head_args_ok(vocab, hidden, k)) return 0;
     std::lock_guard<std::mutex> lk(g.mu);
     if (ensure_init_locked() != BFP8_OK) return 0;
@@ -542,7 +449,6 @@ int bfp8_lm_head_topk(const float* h, const int8_t* mantissas, const uint8_t* ex
 }
 
 int bfp8_lm_head_argmax(const float* h, const int8_t* mantissas, const uint8_t* exps, int vocab, int hidden) {
-    ProfScope ps(QP_LMHEAD);
     if (!h || !mantissas || !exps || !lm_head_args_ok(vocab, hidden, 1)) return -1;
     std::lock_guard<std::mutex> lk(g.mu);
     if (ensure_init_locked() != BFP8_OK) return -1;
@@ -552,7 +458,6 @@ int bfp8_lm_head_argmax(const float* h, const int8_t* mantissas, const uint8_t* 
 }
 
 int lm_head_argmax(const float* h, const uint16_t* embed_table, int vocab_size, int hidden_dim) {
-    ProfScope ps(QP_LMHEAD);
     if (!h || !embed_table || vocab_size <= 0 || hidden_dim <= 0) return 0;
     if (hidden_dim > BF16_HEAD_MAX_HIDDEN) {
         set_error("lm_head_argmax: hidden_dim %d above %d", hidden_dim, BF16_HEAD_MAX_HIDDEN);
@@ -568,7 +473,6 @@ int lm_head_argmax(const float* h, const uint16_t* embed_table, int vocab_size, 
 
 int qwen_lm_head_topk_bf16(const float* h, const uint16_t* embed_table, int vocab_size, int hidden_dim, int k,
                            int* out_ids, float* out_scores) {
-    ProfScope ps(QP_LMHEAD);
     if (!h || !embed_table || !out_ids || !out_scores || vocab_size <= 0 || hidden_dim <= 0 || k <= 0) return 0;
     if (std::min(k, vocab_size) > BFP8_TOPK_MAX || hidden_dim > BF16_HEAD_MAX_HIDDEN) {
         set_error("lm_head_topk: k = %d or hidden_dim = %d above the limits %d, %d", k, hidden_dim, BFP8_TOPK_MAX,
@@ -632,6 +536,7 @@ const char* bfp8_last_error(void) {
 void bfp8_cache_clear(void) {
     std::lock_guard<std::mutex> lk(g.mu);
     if (g.ready) (void)hipStreamSynchronize(g.stream);
+    forward_cache_clear();
     for (auto& kv : g.bf16_cache) kv.second.release();
     g.bf16_cache.clear();
     for (auto& kv : g.cache) {
@@ -834,16 +739,7 @@ int bfp8_dev_sample_from_topk(int* out_id, const int* ids, const float* scores, 
 }  // extern "C"
 
 // =========================== plans ================================================
-namespace {
-
-// One grouped launch: its tile table, either dealt over a persistent grid
-// (wg_off per workgroup) or one tile per 16-wavefront workgroup (wide).
-struct Launch {
-    DevBuf tiles, wg_off;
-    int nwg = 0;
-    bool wide = false;
-    int ntiles = 0, max_nb = 0;
-};
+namespace qhost {
 
 struct Plan {
     std::vector<bfp8_plan_item> items;
@@ -908,7 +804,7 @@ void release_plan(Plan* p) {
     p->head.tiles.release(); p->head.wg_off.release(); p->rest.tiles.release(); p->rest.wg_off.release();
 }
 
-}  // namespace
+}  // namespace qhost
 
 extern "C" {
 

@@ -1,0 +1,121 @@
+// runtime_internal.h -- descriptors and launchers of the decode-runtime
+// kernels (runtime_ftz.hip) shared with the C-ABI host code.  Not part of the
+// public ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+// rmsnorm (04/qwen_kernels_opt.c:140-175), optionally preceded by
+// add_residual into h (:386-393) and followed by the activation quantizer of
+// the next GEMV (:182-205).
+struct RtNormArgs {
+    float* h;             // x; with res, h = h + res is written back first
+    const float* res;     // residual, or null
+    const float* w;       // norm weight (applied as 1 + w)
+    float* y;             // normalised output, or null
+    float* xscale;        // non-null: quantize y (n / 64 blocks) ...
+    uint32_t* xsplit;     // ... into these GEMV activation records
+    int n;
+    float eps;
+};
+
+// swiglu (:363-384), optionally followed by the quantizer (n % 64 == 0).
+struct RtSwigluArgs {
+    float* y;
+    const float* gate;
+    const float* up;
+    float* xscale;
+    uint32_t* xsplit;
+    int n;
+};
+
+// causal_conv1d_update_silu (:511-542).
+struct RtConvArgs {
+    float* y;
+    const float* x;
+    float* state;  // [3][channels], oldest tap first
+    const float* w;  // [channels][4]
+    int channels;
+};
+
+// gdn_gates (:593-620).
+struct RtGatesArgs {
+    float* alpha;
+    float* beta;
+    const float* x;
+    const float* wa;
+    const float* wb;
+    const float* nea;
+    const float* dt;
+    int H, K;
+};
+
+// gdn_recurrent_step (:659-813); the state uses the reference's blocked
+// layout state[h][((jg*ng + ig)*4 + l)*4 + t] = S[h][4ig+t][4jg+l].
+struct RtGdnArgs {
+    float* out;
+    float* state;
+    const float* q;
+    const float* k;
+    const float* v;
+    const float* alpha;
+    const float* beta;
+    int H, D;
+};
+
+// rmsnorm_gated (:818-847), optionally followed by the quantizer of its
+// output (D % 64 == 0).
+struct RtGatedArgs {
+    float* y;
+    const float* x;
+    const float* z;
+    const float* w;
+    float* xscale;
+    uint32_t* xsplit;
+    int H, D;
+    float eps;
+};
+
+// The model's linear-attention block between the qkv/z GEMVs and the o GEMV
+// (04/qwen_kernels_opt.c:943-987, steps 3-8) for 16 heads of 128: conv1d +
+// SiLU over the head's q/k/v channels, q/k L2 norm, gates, recurrent step,
+// gated RMSNorm and the quantizer of the o GEMV's input; one workgroup per
+// head.
+#define RT_HEADS 16
+#define RT_HEAD_DIM 128
+#define RT_CONV_CH 6144
+#define RT_HIDDEN 1024
+struct RtLinearAttnArgs {
+    const float* qkv;     // [6144] qkv GEMV output
+    const float* zbuf;    // [2048] z GEMV output
+    const float* normed;  // [1024] input-norm output (gate input)
+    float* conv_s;        // [3][6144]
+    const float* conv_w;  // [6144][4]
+    const float* wa;      // [16][1024]
+    const float* wb;      // [16][1024]
+    const float* nea;     // [16]
+    const float* dt;      // [16]
+    float* state;         // [16][128*128], blocked
+    const float* norm_w;  // [128]
+    float* xscale;        // [32] o-GEMV activation scales
+    uint32_t* xsplit;     // [32][32] o-GEMV activation records
+    float* mixed;         // optional [6144]: q, k after L2 norm, v
+    float* attn;          // optional [2048]: recurrent-step output
+    float* gated;         // optional [2048]: gated RMSNorm output
+    float* alpha_beta;    // optional [32]: alpha[16], beta[16]
+};
+
+hipError_t rt_launch_rmsnorm(const RtNormArgs& a, hipStream_t s);
+hipError_t rt_launch_swiglu(const RtSwigluArgs& a, hipStream_t s);
+hipError_t rt_launch_conv1d(const RtConvArgs& a, hipStream_t s);
+hipError_t rt_launch_qk_l2norm(float* q, float* k, int H, int D, hipStream_t s);
+hipError_t rt_launch_gates(const RtGatesArgs& a, hipStream_t s);
+hipError_t rt_launch_gdn_step(const RtGdnArgs& a, hipStream_t s);
+hipError_t rt_launch_gated(const RtGatedArgs& a, hipStream_t s);
+hipError_t rt_launch_add_residual(float* x, const float* res, int n, hipStream_t s);
+hipError_t rt_launch_linear_attn(const RtLinearAttnArgs& a, hipStream_t s);
+// h[i] = the float whose high half is table[row*hidden + i]
+hipError_t rt_launch_embed(float* h, const uint16_t* table, int row, int hidden, hipStream_t s);
+
+// Largest head_dim / gate input the per-head kernels stage in LDS.
+#define RT_MAX_HEAD_DIM 4096

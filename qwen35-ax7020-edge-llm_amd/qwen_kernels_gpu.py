@@ -28,8 +28,10 @@ LIB_PATH = Path(__file__).resolve().parent / "libqwen_kernels.so"
 BFP8_OK, BFP8_EINVAL, BFP8_EHIP, BFP8_ENOMEM = 0, -1, -2, -3
 
 # Reference symbols whose signatures the engine binds (04/qwen_real_engine.py).
-REFERENCE_SYMBOLS = ("init_kernels", "bfp8_gemv", "qwen_prof_enable", "qwen_prof_reset",
-                     "qwen_prof_count", "qwen_prof_get", "qwen_prof_name")
+REFERENCE_SYMBOLS = ("add_residual", "bfp8_gemv", "causal_conv1d_update_silu", "forward_linear_layer",
+                     "forward_mlp", "forward_token_c", "gdn_gates", "gdn_recurrent_step", "init_kernels",
+                     "lm_head_argmax", "qk_l2norm", "qwen_prof_count", "qwen_prof_enable", "qwen_prof_get",
+                     "qwen_prof_name", "qwen_prof_reset", "rmsnorm", "rmsnorm_gated", "swiglu")
 
 
 class bfp8_plan_item(ctypes.Structure):
@@ -40,6 +42,35 @@ class bfp8_plan_item(ctypes.Structure):
         ("M", c_int), ("K", c_int), ("topk", c_int),
         ("out_ids", c_void_p), ("out_scores", c_void_p), ("out_count", c_void_p),
         ("out_argmax", c_void_p),
+    ]
+
+
+# void (*)(int layer, float* h, void* ctx), 04/qwen_real_engine.py:979
+FULL_ATTN_CALLBACK = ctypes.CFUNCTYPE(None, c_int, c_void_p, c_void_p)
+
+
+class LinearLayerPlan(ctypes.Structure):
+    """Mirror of ``LinearLayerPlan`` (include/qwen_kernels.h), field for field
+    the engine's ``LinearLayerPlanC`` (04/qwen_real_engine.py:20-56)."""
+
+    _fields_ = [
+        ("in_ln_w", c_void_p), ("mant_qkv", c_void_p), ("exp_qkv", c_void_p), ("M_qkv", c_int), ("K_qkv", c_int),
+        ("conv_w", c_void_p), ("conv_s", c_void_p), ("wa", c_void_p), ("wb", c_void_p), ("nea", c_void_p),
+        ("dt", c_void_p), ("state", c_void_p), ("mant_z", c_void_p), ("exp_z", c_void_p), ("M_z", c_int),
+        ("K_z", c_int), ("norm_w", c_void_p), ("mant_o", c_void_p), ("exp_o", c_void_p), ("M_o", c_int),
+        ("K_o", c_int), ("post_ln_w", c_void_p), ("mant_gate", c_void_p), ("exp_gate", c_void_p),
+        ("M_gate", c_int), ("K_gate", c_int), ("mant_up", c_void_p), ("exp_up", c_void_p), ("M_up", c_int),
+        ("K_up", c_int), ("mant_down", c_void_p), ("exp_down", c_void_p), ("M_down", c_int), ("K_down", c_int),
+    ]
+
+
+class MlpPlan(ctypes.Structure):
+    """Mirror of ``MlpPlan`` (include/qwen_kernels.h; the engine's ``MlpPlanC``)."""
+
+    _fields_ = [
+        ("post_ln_w", c_void_p), ("mant_gate", c_void_p), ("exp_gate", c_void_p), ("M_gate", c_int),
+        ("K_gate", c_int), ("mant_up", c_void_p), ("exp_up", c_void_p), ("M_up", c_int), ("K_up", c_int),
+        ("mant_down", c_void_p), ("exp_down", c_void_p), ("M_down", c_int), ("K_down", c_int),
     ]
 
 
@@ -75,6 +106,30 @@ def bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.qwen_lm_head_topk_bf16.restype = i
     lib.qwen_sample_from_topk.argtypes = [vp, vp, i, c_float, i, c_float, vp]
     lib.qwen_sample_from_topk.restype = i
+    # the decode runtime and forward loop, as the engine binds them
+    # (04/qwen_real_engine.py:676-725, :852-880, :978-985)
+    f = c_float
+    lib.rmsnorm.argtypes = [vp, vp, vp, i, f]
+    lib.swiglu.argtypes = [vp, vp, vp, i]
+    lib.add_residual.argtypes = [vp, vp, i]
+    lib.causal_conv1d_update_silu.argtypes = [vp, vp, vp, vp, i]
+    lib.qk_l2norm.argtypes = [vp, vp, i, i]
+    lib.gdn_gates.argtypes = [vp, vp, vp, vp, vp, vp, vp, i, i]
+    lib.gdn_recurrent_step.argtypes = [vp, vp, vp, vp, vp, vp, vp, i, i]
+    lib.rmsnorm_gated.argtypes = [vp, vp, vp, vp, i, i, f]
+    lib.forward_linear_layer.argtypes = [vp, vp]
+    lib.forward_mlp.argtypes = [vp, vp]
+    for name in ("rmsnorm", "swiglu", "add_residual", "causal_conv1d_update_silu", "qk_l2norm", "gdn_gates",
+                 "gdn_recurrent_step", "rmsnorm_gated", "forward_linear_layer", "forward_mlp"):
+        getattr(lib, name).restype = None
+    lib.forward_token_c.argtypes = [i, vp, vp, vp, vp, vp, vp, FULL_ATTN_CALLBACK, vp]
+    lib.forward_token_c.restype = i
+    lib.qwen_forward_state_resident.argtypes = [i]
+    lib.qwen_forward_state_resident.restype = i
+    lib.qwen_forward_reset_state.argtypes = []
+    lib.qwen_forward_reset_state.restype = None
+    lib.qwen_forward_sync_state.argtypes = []
+    lib.qwen_forward_sync_state.restype = None
     lib.bfp8_last_error.argtypes = []
     lib.bfp8_last_error.restype = ctypes.c_char_p
     lib.bfp8_cache_clear.argtypes = []

@@ -259,6 +259,9 @@ def _rt():
         lib.orc_rmsnorm_gated.argtypes = [vp, vp, vp, vp, i, i, f]
         lib.orc_forward_linear_layer.argtypes = [vp, vp]
         lib.orc_forward_mlp.argtypes = [vp, vp]
+        lib.orc_forward_token.argtypes = [i, vp, vp, vp, vp, vp, vp, vp, vp, i]
+        lib.orc_forward_token.restype = i
+        lib.orc_set_cr_libm.argtypes = [i]
         _RT_BOUND = True
     return lib
 
@@ -375,3 +378,39 @@ class MlpPlan(ctypes.Structure):
     _fields_ = [("post_ln_w", c_void_p), ("mant_gate", c_void_p), ("exp_gate", c_void_p), ("M_gate", c_int),
                 ("K_gate", c_int), ("mant_up", c_void_p), ("exp_up", c_void_p), ("M_up", c_int), ("K_up", c_int),
                 ("mant_down", c_void_p), ("exp_down", c_void_p), ("M_down", c_int), ("K_down", c_int)]
+
+
+class cr_libm:
+    """Context: the oracle's expf / log1pf become exp / log1p in double rounded
+    once to float (the definition the GPU implements)."""
+
+    def __enter__(self):
+        _rt().orc_set_cr_libm(1)
+        return self
+
+    def __exit__(self, *exc):
+        _rt().orc_set_cr_libm(0)
+
+
+def forward_mlp(plan, h):
+    """orc_forward_mlp on a copy of h; plan is a ctypes MlpPlan (states are
+    the host buffers the plan points at)."""
+    h = _f32(h).copy()
+    _rt().orc_forward_mlp(ctypes.addressof(plan), _p(h))
+    return h
+
+
+def forward_linear_layer(plan, h):
+    """orc_forward_linear_layer on a copy of h; updates the plan's conv and
+    recurrent state buffers in place (blocked state layout converted)."""
+    h = _f32(h).copy()
+    _rt().orc_forward_linear_layer(ctypes.addressof(plan), _p(h))
+    return h
+
+
+def forward_token(token_id, lin_plans, mlp_plans, is_full, final_norm_w, embed, vocab=65536):
+    h = np.zeros(1024, dtype=np.float32)
+    isf = np.ascontiguousarray(is_full, dtype=np.int32)
+    best = _rt().orc_forward_token(int(token_id), _p(h), ctypes.addressof(lin_plans), ctypes.addressof(mlp_plans),
+                                   _p(isf), _p(_f32(final_norm_w)), _p(embed), None, None, vocab)
+    return best, h

@@ -22,7 +22,7 @@ def declared_functions(header=HEADER):
     text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
     text = "\n".join(l for l in text.splitlines() if not l.lstrip().startswith("#"))
     names = re.findall(r"(?:^|;|\})\s*(?:const\s+)?[A-Za-z_][\w]*\s*\**\s*\b([a-z_][a-z0-9_]*)\s*\(", text, re.M)
-    return sorted(set(names) - {"struct", "typedef"})
+    return sorted(set(names) - {"struct", "typedef", "void"})  # "typedef void (*cb)(...)"
 
 
 def exported_symbols(lib=LIB):

@@ -285,7 +285,10 @@ def test_read_only_mapped_weights_are_cached(gpu, torch_mod):
     kk.lib.bfp8_cache_clear()
 
 
-def test_profiler_slot_accumulates(gpu, torch_mod):
+def test_profiler_slots_untouched_by_direct_calls(gpu, torch_mod):
+    """As in the reference (QP_TIME appears only inside the forward loop,
+    04/qwen_kernels_opt.c:943-1047), a bfp8_gemv called from the host books
+    nothing; the forward's slots are checked in test_gpu_runtime."""
     qk = gpu
     kk = qk.Bfp8Kernels()
     lib = kk.lib
@@ -294,7 +297,7 @@ def test_profiler_slot_accumulates(gpu, torch_mod):
     mant, exps = qk.synth_planes(128, 1024, 47, 124, 130)
     kk.gemv_bfp8(qk.synth_normal(1024, 48), mant, exps, 128, 1024)
     lib.qwen_prof_enable(0)
-    assert lib.qwen_prof_get(0) > 0.0 and lib.qwen_prof_get(2) == 0.0
+    assert all(lib.qwen_prof_get(i) == 0.0 for i in range(lib.qwen_prof_count()))
 
 
 # ---- fused lm_head -------------------------------------------------------------------------------

@@ -5,6 +5,7 @@ host build and its RTL testbench stimulus (tests/golden), closed forms whose
 answer follows from the arithmetic, ARM ARM flush-to-zero rules, and brute
 force on small inputs.
 """
+import ctypes
 import math
 from pathlib import Path
 
@@ -522,3 +523,32 @@ def test_add_residual_is_elementwise_sum():
     x = rng.standard_normal(1027).astype(F)
     r = rng.standard_normal(1027).astype(F)
     assert np.array_equal(ol.add_residual(x, r), (x + r).astype(F))
+
+
+def test_libm_modes_of_the_oracle():
+    """Host-libm mode (the reference's expf) and the correctly-rounded mode
+    (exp in double, rounded once: what the GPU computes) differ by at most one
+    ulp; the correctly-rounded mode agrees with float64 exp rounded to float32
+    on every point (swiglu's scalar tail: n = 3 puts every element there)."""
+    rng = np.random.default_rng(27)
+    g = (rng.standard_normal(3000) * 12.0).astype(F)
+    u = np.ones(3000, dtype=F)
+    host = np.concatenate([ol.swiglu(g[i:i + 3], u[i:i + 3]) for i in range(0, 3000, 3)])
+    with ol.cr_libm():
+        cr = np.concatenate([ol.swiglu(g[i:i + 3], u[i:i + 3]) for i in range(0, 3000, 3)])
+    e = np.exp(-g.astype(np.float64)).astype(F)
+    want = (g / (F(1.0) + e)).astype(F) * u
+    assert np.array_equal(cr.view(np.uint32), want.view(np.uint32))
+    gap = np.abs(host.view(np.int32).astype(np.int64) - cr.view(np.int32).astype(np.int64))
+    assert gap.max() <= 1
+
+
+def test_forward_plans_have_the_reference_layout():
+    """LinearLayerPlan / MlpPlan are 224 / 80 bytes without padding (the
+    reference's field order, 04/qwen_kernels_opt.c:866-917); the library's
+    ctypes mirrors agree field by field with the oracle's."""
+    import qwen_kernels_gpu as qk
+    assert ctypes.sizeof(qk.LinearLayerPlan) == ctypes.sizeof(ol.LinearPlan) == 224
+    assert ctypes.sizeof(qk.MlpPlan) == ctypes.sizeof(ol.MlpPlan) == 80
+    for a, b in ((qk.LinearLayerPlan, ol.LinearPlan), (qk.MlpPlan, ol.MlpPlan)):
+        assert [(n, getattr(a, n).offset) for n, _ in a._fields_] == [(n, getattr(b, n).offset) for n, _ in b._fields_]
