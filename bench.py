@@ -21,7 +21,10 @@ value = algorithmic bytes per sweep (weights once + f32 x in + f32 y out; the
 fused lm_head writes no logits) / wall time per step, in GB/s.
 
 Extra workloads for the per-config numbers: --workload lm_head (65536x1024
-fused top-40), gemv (3584x1024), down (1024x3584), batch16 (B=16 x 3584x1024).
+fused top-40), gemv (3584x1024), down (1024x3584), batch16 (B=16 x 3584x1024),
+lm_head_bf16 (the reference's bf16 tied-embedding lm_head, top-64),
+forward_token (the reference's forward_token_c: 24 layers at the model's
+shapes with distinct synthetic weights + bf16 lm_head argmax, per token).
 
     python bench.py [--steps K] [--warmup W] [--workload sweep] [--no-cpu]
 """
@@ -143,7 +146,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="sweep",
-                    choices=["sweep", "layers", "lm_head", "lm_head_plain", "gemv", "down", "batch16", "lm_head_bf16"])
+                    choices=["sweep", "layers", "lm_head", "lm_head_plain", "gemv", "down", "batch16", "lm_head_bf16",
+                             "forward_token"])
     ap.add_argument("--rotate-gb", type=float, default=1.0, help="rotating weight copies totalling >= this")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     args = ap.parse_args()
@@ -165,6 +169,8 @@ def main():
         return bench_batch16(args, qk, torch, np)
     if args.workload == "lm_head_bf16":
         return bench_lm_head_bf16(args, qk, torch, np)
+    if args.workload == "forward_token":
+        return bench_forward_token(args, qk, torch, np)
 
     items = workload_items(args.workload)
     per_copy = sum(wbytes(M, K) for _, M, K, *_ in items)
@@ -383,6 +389,149 @@ def bench_lm_head_bf16(args, qk, torch, np):
                       "kernel": {"name": "bf16_lm_head_kernel", "avg_us": round(kus, 2), "algorithmic_bytes": kbytes},
                       "roofline": {"bound": "hbm", "achieved": round(kbytes / kus / 1e3, 1), "peak": PEAK_HBM_GBPS,
                                    "unit": "GB/s", "frac": round(kbytes / kus / 1e3 / PEAK_HBM_GBPS, 4)}}), flush=True)
+
+
+class _SynthModel:
+    """Model-shaped synthetic weights in host memory, the engine's layout:
+    BFP8 planes (mantissas [M][K], exponents [M][K/64]) distinct per layer,
+    float parameters, states, a bf16 embedding table, and the plan arrays
+    forward_token_c takes."""
+
+    GEMVS = {"qkv": (6144, 1024), "z": (2048, 1024), "o": (1024, 2048), "gate": (3584, 1024),
+             "up": (3584, 1024), "down": (1024, 3584)}
+    FULL = (3, 7, 11, 15, 19, 23)
+
+    def __init__(self, qk, np, lin_type, mlp_type, seed=77):
+        lib = qk.load()
+        rng = np.random.default_rng(seed)
+        self.keep = []
+        self.is_full = np.array([1 if l in self.FULL else 0 for l in range(N_LAYERS)], dtype=np.int32)
+        self.lin = (lin_type * 18)()
+        self.mlp = (mlp_type * N_LAYERS)()
+        self.weight_bytes = 0
+        self.param_bytes = 0
+        self.state_bytes = 0
+        li, seed_i = 0, seed * 1000
+
+        def arr(a):
+            a = np.ascontiguousarray(a)
+            self.keep.append(a)
+            return a
+
+        def vec(n, scale):
+            self.param_bytes += 4 * n
+            return arr((rng.standard_normal(n) * scale).astype(np.float32))
+
+        def planes(plan, names):
+            nonlocal seed_i
+            for name in names:
+                M, K = self.GEMVS[name]
+                m = arr(np.empty(M * K, dtype=np.int8))
+                e = arr(np.empty(M * (K // 64), dtype=np.uint8))
+                lib.bfp8_synth_planes_host(m.ctypes.data, e.ctypes.data, M, K, seed_i, 122, 126)
+                seed_i += 1
+                self.weight_bytes += m.nbytes + e.nbytes
+                setattr(plan, "mant_" + name, m.ctypes.data)
+                setattr(plan, "exp_" + name, e.ctypes.data)
+                setattr(plan, "M_" + name, M)
+                setattr(plan, "K_" + name, K)
+
+        for l in range(N_LAYERS):
+            if self.is_full[l]:
+                p = self.mlp[l]
+                p.post_ln_w = vec(1024, 0.1).ctypes.data
+                planes(p, ("gate", "up", "down"))
+                continue
+            p = self.lin[li]
+            li += 1
+            p.in_ln_w, p.post_ln_w = vec(1024, 0.1).ctypes.data, vec(1024, 0.1).ctypes.data
+            p.conv_w = vec(6144 * 4, 0.5).ctypes.data
+            p.wa, p.wb = vec(16 * 1024, 0.03).ctypes.data, vec(16 * 1024, 0.03).ctypes.data
+            p.nea = arr((-rng.uniform(0.2, 3.0, 16)).astype(np.float32)).ctypes.data
+            p.dt = arr(rng.uniform(-2, 2, 16).astype(np.float32)).ctypes.data
+            p.norm_w = vec(128, 0.5).ctypes.data
+            p.conv_s = arr(np.zeros(3 * 6144, dtype=np.float32)).ctypes.data
+            p.state = arr(np.zeros(16 * 128 * 128, dtype=np.float32)).ctypes.data
+            self.state_bytes += 4 * (3 * 6144 + 16 * 128 * 128)
+            planes(p, ("qkv", "z", "o", "gate", "up", "down"))
+        self.final_w = vec(1024, 0.1)
+        # bf16 table: random sign, exponent 119..123, random 7-bit mantissa
+        u = rng.integers(0, 2 ** 16, size=65536 * 1024, dtype=np.uint16)
+        self.embed = arr((u & 0x807F) | ((119 + (u >> 7) % 5).astype(np.uint16) << 7))
+        self.h = arr(np.zeros(1024, dtype=np.float32))
+
+    def token_bytes(self):
+        """Algorithmic HBM bytes of one token: every BFP8 plane, the bf16
+        table (the lm_head reads all of it), the float parameters, and the
+        conv + recurrent states read and written once."""
+        return self.weight_bytes + self.embed.nbytes + self.param_bytes + 2 * self.state_bytes
+
+    def run(self, fn, token, cb=None):
+        return fn(token, self.h.ctypes.data, ctypes.addressof(self.lin), ctypes.addressof(self.mlp),
+                  self.is_full.ctypes.data, self.final_w.ctypes.data, self.embed.ctypes.data, cb, None)
+
+
+def bench_forward_token(args, qk, torch, np):
+    """forward_token_c (04/qwen_kernels_opt.c:1008-1049) called exactly as the
+    engine calls it (host pointers, synchronous): 18 linear-attention layers +
+    6 MLP-only layers (the full-attention layers' attention is the engine's
+    host callback and is not part of the library: none here), final rmsnorm,
+    bf16 lm_head argmax over 65536 x 1024.  Timed with the conv / recurrent
+    states resident on the device (qwen_forward_state_resident(1)) and, as a
+    second figure, with the reference's copy-in / copy-out of the states on
+    every call."""
+    lib = qk.load()
+    m = _SynthModel(qk, np, qk.LinearLayerPlan, qk.MlpPlan)
+    print(f"[bench] forward_token: {m.weight_bytes / 1e6:.1f} MB BFP8 + {m.embed.nbytes / 1e6:.1f} MB bf16 table "
+          f"+ {m.param_bytes / 1e6:.1f} MB params, {m.state_bytes / 1e6:.1f} MB states", flush=True)
+
+    def timed(resident, steps, warmup):
+        lib.qwen_forward_state_resident(resident)
+        no_cb = qk.FULL_ATTN_CALLBACK()  # NULL: no full-attention callback
+        for i in range(warmup):
+            m.run(lib.forward_token_c, 1000 + i, no_cb)
+        ts = []
+        for i in range(steps):
+            t0 = time.perf_counter()
+            m.run(lib.forward_token_c, 2000 + i, no_cb)
+            ts.append(time.perf_counter() - t0)
+        lib.qwen_forward_state_resident(0)
+        ts.sort()
+        return ts[len(ts) // 2] * 1e6, sum(ts) / len(ts) * 1e6
+
+    med_res, mean_res = timed(1, args.steps, args.warmup)
+    med_sync, mean_sync = timed(0, max(5, args.steps // 5), 2)
+    tb = m.token_bytes()
+    cpu = None
+    ref = ROOT / "oracle" / "_ref" / "libref_qwen_kernels.so"
+    if not args.no_cpu and ref.exists():
+        rl = ctypes.CDLL(str(ref))
+        rl.init_kernels()
+        fn = rl.forward_token_c
+        fn.argtypes = [ctypes.c_int] + [ctypes.c_void_p] * 8
+        fn.restype = ctypes.c_int
+        t0 = time.perf_counter()
+        n = 0
+        while time.perf_counter() - t0 < 10.0:
+            m.run(fn, 3000 + n)
+            n += 1
+        el = time.perf_counter() - t0
+        threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count()
+        cpu = {"value": round(n / el, 3), "unit": "tokens/s", "cores": threads, "kind": "reference",
+               "sample": f"{n} tokens of the reference's host-built forward_token_c (float-path GEMVs, scalar "
+                         f"runtime, OpenMP) on the same synthetic model, {el:.1f} s"}
+    print(json.dumps({
+        "metric": "decode tokens/s (forward_token_c: 24 layers + bf16 lm_head argmax)",
+        "value": round(1e6 / med_res, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "us_per_token": round(med_res, 1), "us_per_token_mean": round(mean_res, 1),
+        "us_per_token_state_copies": round(med_sync, 1), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32 (BFP8 int8 x int16 GEMV)", "data": "synthetic",
+        "config": {"workload": "forward_token", "layers": N_LAYERS, "linear_attention_layers": 18,
+                   "hidden": 1024, "vocab": 65536, "state": "device-resident"},
+        "roofline": {"bound": "hbm", "achieved": round(tb / med_res / 1e3, 1), "peak": PEAK_HBM_GBPS,
+                     "unit": "GB/s", "frac": round(tb / med_res / 1e3 / PEAK_HBM_GBPS, 4), "traffic": None,
+                     "scope": f"whole token: {tb / 1e6:.1f} MB algorithmic per token / wall time per token"},
+        "cpu_baseline": cpu}), flush=True)
 
 
 if __name__ == "__main__":
