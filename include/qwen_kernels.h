@@ -190,6 +190,30 @@ int qwen_forward_state_resident(int on);
 void qwen_forward_reset_state(void);
 void qwen_forward_sync_state(void);
 
+/* The weight image the exporter writes (05/export_qwen35_weights_bfp8_64k.py:
+ * 64-80, :159-174) and its JSON manifest (06/qwen35_weights_64k_manifest.json:
+ * per tensor type, shape, file_offset, byte_size, and for "block64_bfp8"
+ * mantissa_bytes / exponent_bytes).
+ *
+ * qwen_weights_scan parses and checks the manifest against an image of
+ * image_bytes: 64-byte aligned offsets inside the image, a BFP8 tensor [M, K]
+ * with K % 64 == 0 holding M*K mantissa bytes then ceil8(M*K/64) exponent
+ * bytes (05/bfp8_packer.py:53-86), raw tensors of 4 (fp32) or 2 (bf16) bytes
+ * per element.  Returns the number of tensors and fills the per-type counts
+ * and the BFP8 byte total; a negative BFP8_E* code on the first bad entry
+ * (bfp8_last_error names it).  No GPU is touched.
+ *
+ * qwen_weights_preload does the same checks on the mapped image (host
+ * memory), then converts every BFP8 tensor to the GPU layout once and keeps
+ * it under the host addresses the engine's slicing produces (mant = raw[:M*K],
+ * exps = raw[M*K:], 04/qwen_real_engine.py:834-846), so that bfp8_gemv and
+ * the forward find it resident; the bf16 table and the fp32 tensors are
+ * copied to the device too.  The image is treated as immutable until
+ * bfp8_cache_clear().  Returns the number of BFP8 tensors converted. */
+int qwen_weights_scan(const char* manifest_json, size_t image_bytes, int* n_bfp8, int* n_f32, int* n_bf16,
+                      uint64_t* bfp8_bytes);
+int qwen_weights_preload(const void* image, size_t image_bytes, const char* manifest_json);
+
 /* Message of the most recent failure of this library ("" if none). */
 const char* bfp8_last_error(void);
 
@@ -263,6 +287,14 @@ int bf16_dev_lm_head(int* out_ids, float* out_scores, int* out_count, int* out_a
 int bfp8_dev_sample_from_topk(int* out_id, const int* ids, const float* scores, const int* count, int n,
                               float temperature, int top_k, float top_p, uint32_t* rng_state, void* work,
                               void* stream);
+
+/* GPU planes of a tensor qwen_weights_preload converted, by manifest name. */
+int qwen_weights_find(const char* name, const int8_t** mant_gpu, const uint8_t** exps_gpu, int* M, int* K);
+
+/* GPU planes from the PL GEMV core's per-row stream (device memory): for each
+ * row, its K/64 exponent bytes, then its K mantissas (02/gemv_core.v:23-24,
+ * 02/tb_gemv_core.v:281-297).  K % 64 == 0. */
+int bfp8_dev_pack_rows(int8_t* mant_gpu, uint8_t* exps_gpu, const uint8_t* row_stream, int M, int K, void* stream);
 
 /* A sweep plan: many independent GEMVs (and at most one fused lm_head)
  * executed as one quantize launch plus two streaming launches: the lm_head's

@@ -9,6 +9,7 @@ Translation units:
   csrc/runtime_ftz.hip       decode runtime kernels (norms, conv, GDN, swiglu), f32 flush-to-zero
   csrc/qwen_kernels_api.cpp  C ABI host code (include/qwen_kernels.h)
   csrc/qwen_runtime_api.cpp  C ABI of the runtime kernels and the forward loop
+  csrc/qwen_weights.cpp      manifest-driven weight-image loader
 
 Every device TU is built with -ffp-contract=off (no fused multiply-add: the
 reference rounds every product and sum) and without packed FP32 ops.
@@ -43,6 +44,7 @@ UNITS = {
     "bfp8_ieee.hip": [],
     "qwen_kernels_api.cpp": [],
     "qwen_runtime_api.cpp": [],
+    "qwen_weights.cpp": [],
 }
 
 

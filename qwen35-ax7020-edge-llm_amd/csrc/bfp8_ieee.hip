@@ -125,8 +125,12 @@ extern "C" __global__ __launch_bounds__(64) void bfp8_gemv_float_kernel(
 // One thread per (row tile lane, block): reads the 64 mantissas of a block
 // (row stride K, as the engine slices them) and writes the four residue
 // chunks; rows past M are zero.
+// Reference planes -> GPU layout.  Row `row` of the mantissas starts at
+// ms + row * ms_stride and its exponents at es + row * es_stride: the packer's
+// SoA planes have strides K and K/64; the PL core's per-row stream (K/64
+// exponent bytes, then K mantissas per row) has K/64 + K for both.
 extern "C" __global__ __launch_bounds__(256) void bfp8_pack_mant_kernel(
-    uint8_t* __restrict__ mg, const int8_t* __restrict__ ms, int M, int K) {
+    uint8_t* __restrict__ mg, const int8_t* __restrict__ ms, int M, int K, size_t ms_stride) {
     const int nb = K >> 6;
     const size_t total = (size_t)bfp8_ntiles(M) * 64u * nb;
     for (size_t g = (size_t)blockIdx.x * blockDim.x + threadIdx.x; g < total;
@@ -138,7 +142,7 @@ extern "C" __global__ __launch_bounds__(256) void bfp8_pack_mant_kernel(
         const int row = t * 64 + r;
         u32x4 out[4] = {u32x4(0u), u32x4(0u), u32x4(0u), u32x4(0u)};
         if (row < M) {
-            const int8_t* src = ms + (size_t)row * K + (size_t)b * 64;
+            const int8_t* src = ms + (size_t)row * ms_stride + (size_t)b * 64;
             for (int k = 0; k < 64; ++k) {
                 const int q = k & 3, i = k >> 2;
                 out[q][i >> 2] |= ((uint32_t)(uint8_t)src[k]) << (8 * (i & 3));
@@ -150,7 +154,7 @@ extern "C" __global__ __launch_bounds__(256) void bfp8_pack_mant_kernel(
 }
 
 extern "C" __global__ __launch_bounds__(256) void bfp8_pack_exps_kernel(
-    uint8_t* __restrict__ eg, const uint8_t* __restrict__ es, int M, int K) {
+    uint8_t* __restrict__ eg, const uint8_t* __restrict__ es, int M, int K, size_t es_stride) {
     const int nb = K >> 6, nb4 = (nb + 3) >> 2;
     const size_t total = (size_t)bfp8_ntiles(M) * nb4 * 64u;
     for (size_t g = (size_t)blockIdx.x * blockDim.x + threadIdx.x; g < total;
@@ -163,7 +167,7 @@ extern "C" __global__ __launch_bounds__(256) void bfp8_pack_exps_kernel(
         uint32_t word = 0;
         for (int p = 0; p < 4; ++p) {
             const int b = grp * 4 + p;
-            if (row < M && b < nb) word |= (uint32_t)es[(size_t)row * nb + b] << (8 * p);
+            if (row < M && b < nb) word |= (uint32_t)es[(size_t)row * es_stride + b] << (8 * p);
         }
         reinterpret_cast<uint32_t*>(eg)[g] = word;
     }
@@ -354,17 +358,25 @@ hipError_t bfp8_launch_gemv_float(float* y, const float* x, const uint8_t* mant,
     return hipGetLastError();
 }
 
-hipError_t bfp8_launch_pack(uint8_t* mant_gpu, uint8_t* exps_gpu, const int8_t* mant_soa,
-                            const uint8_t* exps_soa, int M, int K, hipStream_t s) {
+hipError_t bfp8_launch_pack_strided(uint8_t* mant_gpu, uint8_t* exps_gpu, const int8_t* mant_src, size_t mant_stride,
+                                    const uint8_t* exps_src, size_t exps_stride, int M, int K, hipStream_t s) {
     const int nb = bfp8_nblocks(K);
     if (M <= 0 || nb <= 0) return hipSuccess;
     const size_t wm = (size_t)bfp8_ntiles(M) * 64u * nb;
-    hipLaunchKernelGGL(bfp8_pack_mant_kernel, dim3(grid_for(wm, 256)), dim3(256), 0, s, mant_gpu, mant_soa, M, K);
+    hipLaunchKernelGGL(bfp8_pack_mant_kernel, dim3(grid_for(wm, 256)), dim3(256), 0, s, mant_gpu, mant_src, M, K,
+                       mant_stride);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const size_t we = (size_t)bfp8_ntiles(M) * bfp8_nb4(nb) * 64u;
-    hipLaunchKernelGGL(bfp8_pack_exps_kernel, dim3(grid_for(we, 256)), dim3(256), 0, s, exps_gpu, exps_soa, M, K);
+    hipLaunchKernelGGL(bfp8_pack_exps_kernel, dim3(grid_for(we, 256)), dim3(256), 0, s, exps_gpu, exps_src, M, K,
+                       exps_stride);
     return hipGetLastError();
+}
+
+hipError_t bfp8_launch_pack(uint8_t* mant_gpu, uint8_t* exps_gpu, const int8_t* mant_soa,
+                            const uint8_t* exps_soa, int M, int K, hipStream_t s) {
+    return bfp8_launch_pack_strided(mant_gpu, exps_gpu, mant_soa, (size_t)K, exps_soa, (size_t)bfp8_nblocks(K), M,
+                                    K, s);
 }
 
 hipError_t bfp8_launch_unpack(int8_t* mant_soa, uint8_t* exps_soa, const uint8_t* mant_gpu,

@@ -126,6 +126,11 @@ hipError_t bfp8_launch_gemv_float(float* y, const float* x, const uint8_t* mant,
                                   int M, int K, hipStream_t s);
 hipError_t bfp8_launch_pack(uint8_t* mant_gpu, uint8_t* exps_gpu, const int8_t* mant_soa,
                             const uint8_t* exps_soa, int M, int K, hipStream_t s);
+// Row r's mantissas at mant_src + r*mant_stride, its exponents at
+// exps_src + r*exps_stride (SoA planes: K and K/64; the per-row stream of
+// exponents-then-mantissas: K/64 + K for both).
+hipError_t bfp8_launch_pack_strided(uint8_t* mant_gpu, uint8_t* exps_gpu, const int8_t* mant_src, size_t mant_stride,
+                                    const uint8_t* exps_src, size_t exps_stride, int M, int K, hipStream_t s);
 hipError_t bfp8_launch_unpack(int8_t* mant_soa, uint8_t* exps_soa, const uint8_t* mant_gpu,
                               const uint8_t* exps_gpu, int M, int K, hipStream_t s);
 hipError_t bfp8_launch_synth_planes(int8_t* mant_soa, uint8_t* exps_soa, int M, int K, uint64_t seed,

@@ -133,8 +133,14 @@ struct DevWeights {
 // Device GPU-layout planes for host reference planes: cached when the planes
 // are read-only (the engine's mmap), else converted into a per-call buffer.
 int weights_for(const int8_t* mant, const uint8_t* exps, int M, int K, DevWeights* out);
-// Device copy of a host bf16 table [vocab][hidden] (cached when read-only).
+// The same, cached whatever the memory's protection (force: the caller
+// declares the planes immutable until bfp8_cache_clear()).
+int weights_cached(const int8_t* mant, const uint8_t* exps, int M, int K, bool force, DevWeights* out);
+// Device copy of a host bf16 table [vocab][hidden] (cached when read-only or forced).
 int bf16_table_for(const uint16_t* table, int vocab, int hidden, const uint16_t** out);
+int bf16_table_cached(const uint16_t* table, int vocab, int hidden, bool force, const uint16_t** out);
+// Pre-loads a float parameter the forward reads (host address, bytes); g.mu held.
+int forward_preload_param(const void* p, size_t bytes);
 // bf16 lm_head scores (+ fused top-k) on device buffers.
 int bf16_lm_head_dev(int* ids, float* scores, int* count, int* argmax, float* logits, const float* h,
                      const uint16_t* table, int vocab, int hidden, int k, int tail, hipStream_t s);
@@ -152,6 +158,8 @@ struct Launch {
 
 // Drops the forward's device copies (qwen_runtime_api.cpp); g.mu held.
 void forward_cache_clear();
+// Forgets the preloaded tensors' names (qwen_weights.cpp); g.mu held.
+void weights_index_clear();
 
 // Deals the tiles of items[idx] over a launch (persistent or wide).
 int deal_tiles(Launch& L, const std::vector<int>& idx, const bfp8_plan_item* items, int wg0_extra, bool allow_wide);

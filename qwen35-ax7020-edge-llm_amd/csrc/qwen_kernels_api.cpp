@@ -105,7 +105,7 @@ bool range_readonly(const void* p, size_t n) {
 }
 
 // Device GPU-layout planes for host reference planes.
-int weights_for(const int8_t* mant, const uint8_t* exps, int M, int K, DevWeights* out) {
+int weights_cached(const int8_t* mant, const uint8_t* exps, int M, int K, bool force, DevWeights* out) {
     const int nb = bfp8_nblocks(K);
     const size_t mbytes = (size_t)M * (size_t)K, ebytes = (size_t)M * (size_t)nb;
     const WeightKey key{mant, exps, M, K};
@@ -121,7 +121,11 @@ int weights_for(const int8_t* mant, const uint8_t* exps, int M, int K, DevWeight
     HIP_OK(hipMemcpyAsync(g.soa_e.p, exps, ebytes, hipMemcpyHostToDevice, g.stream));
     const size_t gm = bfp8_gpu_mant_bytes(M, K), ge = bfp8_gpu_exps_bytes(M, K);
     const bool cacheable = g.cache_bytes + gm + ge <= kCacheLimit &&
-                           range_readonly(mant, mbytes) && range_readonly(exps, ebytes);
+                           (force || (range_readonly(mant, mbytes) && range_readonly(exps, ebytes)));
+    if (force && !cacheable) {
+        set_error("device weight cache full (%zu bytes)", g.cache_bytes);
+        return BFP8_EINVAL;
+    }
     DevBuf* dm = &g.gpu_m;
     DevBuf* de = &g.gpu_e;
     CachedWeights cw;
@@ -141,11 +145,15 @@ int weights_for(const int8_t* mant, const uint8_t* exps, int M, int K, DevWeight
     return BFP8_OK;
 }
 
+int weights_for(const int8_t* mant, const uint8_t* exps, int M, int K, DevWeights* out) {
+    return weights_cached(mant, exps, M, K, false, out);
+}
+
 int upload_x(const float* x, size_t nfloat);
 
 // Device copy of a host bf16 table [vocab][hidden]: cached when it lives in
-// read-only memory (the engine's mmap), else uploaded per call.
-int bf16_table_for(const uint16_t* table, int vocab, int hidden, const uint16_t** out) {
+// read-only memory (the engine's mmap) or when forced, else uploaded per call.
+int bf16_table_cached(const uint16_t* table, int vocab, int hidden, bool force, const uint16_t** out) {
     const size_t bytes = (size_t)vocab * (size_t)hidden * 2;
     const WeightKey key{table, nullptr, vocab, hidden};
     auto it = g.bf16_cache.find(key);
@@ -153,7 +161,7 @@ int bf16_table_for(const uint16_t* table, int vocab, int hidden, const uint16_t*
         *out = it->second.as<uint16_t>();
         return BFP8_OK;
     }
-    const bool cacheable = g.cache_bytes + bytes <= kCacheLimit && range_readonly(table, bytes);
+    const bool cacheable = g.cache_bytes + bytes <= kCacheLimit && (force || range_readonly(table, bytes));
     DevBuf fresh;
     DevBuf* d = cacheable ? &fresh : &g.bf16_ws;
     int rc;
@@ -165,6 +173,10 @@ int bf16_table_for(const uint16_t* table, int vocab, int hidden, const uint16_t*
         g.bf16_cache.emplace(key, fresh);
     }
     return BFP8_OK;
+}
+
+int bf16_table_for(const uint16_t* table, int vocab, int hidden, const uint16_t** out) {
+    return bf16_table_cached(table, vocab, hidden, false, out);
 }
 
 // bf16 lm_head scores (+ fused top-k) on device buffers.
@@ -537,6 +549,7 @@ void bfp8_cache_clear(void) {
     std::lock_guard<std::mutex> lk(g.mu);
     if (g.ready) (void)hipStreamSynchronize(g.stream);
     forward_cache_clear();
+    weights_index_clear();
     for (auto& kv : g.bf16_cache) kv.second.release();
     g.bf16_cache.clear();
     for (auto& kv : g.cache) {

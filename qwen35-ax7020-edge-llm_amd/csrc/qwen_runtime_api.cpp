@@ -561,6 +561,11 @@ void drop_forward() {
 // Called by bfp8_cache_clear (lock held).
 void forward_cache_clear() { drop_forward(); }
 
+int forward_preload_param(const void* p, size_t bytes) {
+    const void* d;
+    return fwd_param(p, bytes, &d);
+}
+
 }  // namespace qhost
 
 using namespace qhost;

@@ -130,6 +130,15 @@ def bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.qwen_forward_reset_state.restype = None
     lib.qwen_forward_sync_state.argtypes = []
     lib.qwen_forward_sync_state.restype = None
+    # the weight-image loader
+    lib.qwen_weights_scan.argtypes = [ctypes.c_char_p, c_size_t, vp, vp, vp, vp]
+    lib.qwen_weights_scan.restype = i
+    lib.qwen_weights_preload.argtypes = [vp, c_size_t, ctypes.c_char_p]
+    lib.qwen_weights_preload.restype = i
+    lib.qwen_weights_find.argtypes = [ctypes.c_char_p, vp, vp, vp, vp]
+    lib.qwen_weights_find.restype = i
+    lib.bfp8_dev_pack_rows.argtypes = [vp, vp, vp, i, i, vp]
+    lib.bfp8_dev_pack_rows.restype = i
     lib.bfp8_last_error.argtypes = []
     lib.bfp8_last_error.restype = ctypes.c_char_p
     lib.bfp8_cache_clear.argtypes = []
