@@ -74,8 +74,9 @@ int lm_head_argmax(const float* h, const uint16_t* embed_table, int vocab_size, 
  * forward_mlp and forward_token_c accumulate into the slots: wall
  * milliseconds per step, each step synchronised while profiling is on.  The
  * forward's fused linear-attention kernel (conv1d, q/k norm, gates, recurrent
- * step, gated norm) is booked to gdn_recurrent_step, residual adds fused into
- * the next norm to rmsnorm. */
+ * step, gated norm) is booked to gdn_recurrent_step; the norms, residual adds
+ * and swiglu computed inside the GEMV launches to bfp8_gemv; the final norm
+ * to rmsnorm. */
 void qwen_prof_enable(int on);
 void qwen_prof_reset(void);
 int qwen_prof_count(void);

@@ -7,6 +7,7 @@ Translation units:
   csrc/bfp8_ieee.hip         quantizer / scalar-order kernels, IEEE subnormals
   csrc/bf16_head.hip         bf16 tied-embedding lm_head, f32 flush-to-zero
   csrc/runtime_ftz.hip       decode runtime kernels (norms, conv, GDN, swiglu), f32 flush-to-zero
+  csrc/fused_gemv.hip        the forward's GEMVs with their activation prologue, f32 flush-to-zero
   csrc/qwen_kernels_api.cpp  C ABI host code (include/qwen_kernels.h)
   csrc/qwen_runtime_api.cpp  C ABI of the runtime kernels and the forward loop
   csrc/qwen_weights.cpp      manifest-driven weight-image loader
@@ -41,6 +42,7 @@ UNITS = {
     "bfp8_ftz.hip": ["-fgpu-flush-denormals-to-zero"],
     "bf16_head.hip": ["-fgpu-flush-denormals-to-zero"],
     "runtime_ftz.hip": ["-fgpu-flush-denormals-to-zero"],
+    "fused_gemv.hip": ["-fgpu-flush-denormals-to-zero"],
     "bfp8_ieee.hip": [],
     "qwen_kernels_api.cpp": [],
     "qwen_runtime_api.cpp": [],

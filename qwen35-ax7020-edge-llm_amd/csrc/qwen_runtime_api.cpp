@@ -97,11 +97,6 @@ struct DevState {
     bool dirty = false;          // device copy newer than the caller's buffers
 };
 
-struct FwdGemv {
-    DevWeights w;
-    int M, K;
-};
-
 // One layer (linear-attention layer or MLP of a full-attention layer).
 struct FwdLayer {
     bool linear;
@@ -111,18 +106,17 @@ struct FwdLayer {
     const float *in_ln_w = nullptr, *conv_w = nullptr, *wa = nullptr, *wb = nullptr, *nea = nullptr,
                 *dt = nullptr, *norm_w = nullptr, *post_ln_w = nullptr;
     DevState* st = nullptr;
-    // GEMV descriptors (device) and launches: linear = qkv, z, o, gate, up,
-    // down; MLP = gate, up, down
-    DevBuf descs;
-    Launch l_qkvz, l_o, l_gateup, l_down;
+    // GPU planes: linear = qkv, z, o, gate, up, down; MLP = gate, up, down
+    DevWeights w[6];
 };
 
 struct Workspace {
     DevBuf buf;
-    float *h, *normed, *qkv, *z, *o, *post, *gate, *up, *inter, *down;
-    float *xs_norm, *xs_gated, *xs_post, *xs_inter;  // activation scales
-    uint32_t *xr_norm, *xr_gated, *xr_post, *xr_inter;  // activation records
-    int* lm;  // [ids 1, scores 1, count, argmax]
+    float *h, *h2;  // the hidden state ping-pongs between these (see RtRowsArgs::h_out)
+    float *normed, *qkv, *z, *o, *gate, *up, *down;
+    float* xs_gated;     // the o GEMV's activation scales ...
+    uint32_t* xr_gated;  // ... and records (the other GEMVs quantize in their prologue)
+    int* lm;             // [ids 1, scores 1, count, argmax]
 };
 
 struct Forward {
@@ -186,12 +180,11 @@ int fwd_planes(const int8_t* mant, const uint8_t* exps, int M, int K, DevWeights
 int ensure_workspace() {
     if (F.ws_ready) return BFP8_OK;
     Workspace& w = F.ws;
-    const int nf[] = {kHidden, kHidden, kConv, kHD, kHidden, kHidden, kMlp, kMlp, kMlp, kHidden};
-    const int nbk[] = {kHidden / 64, kHD / 64, kHidden / 64, kMlp / 64};
+    const int nf[] = {kHidden, kHidden, kHidden, kConv, kHD, kHidden, kMlp, kMlp, kHidden};
+    const int nbk = kHD / 64;
     size_t total = 0;
     for (int n : nf) total += ((size_t)n * 4 + 255) & ~(size_t)255;
-    for (int b : nbk) total += (((size_t)b * 4 + 255) & ~(size_t)255) + (size_t)b * 128;
-    total += 256;
+    total += (((size_t)nbk * 4 + 255) & ~(size_t)255) + (size_t)nbk * 128 + 256;
     int rc;
     if ((rc = w.buf.reserve(total))) return rc;
     char* p = w.buf.as<char>();
@@ -200,14 +193,10 @@ int ensure_workspace() {
         p += (bytes + 255) & ~(size_t)255;
         return r;
     };
-    float** fl[] = {&w.h, &w.normed, &w.qkv, &w.z, &w.o, &w.post, &w.gate, &w.up, &w.inter, &w.down};
-    for (int i = 0; i < 10; ++i) *fl[i] = reinterpret_cast<float*>(take((size_t)nf[i] * 4));
-    float** xs[] = {&w.xs_norm, &w.xs_gated, &w.xs_post, &w.xs_inter};
-    uint32_t** xr[] = {&w.xr_norm, &w.xr_gated, &w.xr_post, &w.xr_inter};
-    for (int i = 0; i < 4; ++i) {
-        *xs[i] = reinterpret_cast<float*>(take((size_t)nbk[i] * 4));
-        *xr[i] = reinterpret_cast<uint32_t*>(take((size_t)nbk[i] * 128));
-    }
+    float** fl[] = {&w.h, &w.h2, &w.normed, &w.qkv, &w.z, &w.o, &w.gate, &w.up, &w.down};
+    for (int i = 0; i < 9; ++i) *fl[i] = reinterpret_cast<float*>(take((size_t)nf[i] * 4));
+    w.xs_gated = reinterpret_cast<float*>(take((size_t)nbk * 4));
+    w.xr_gated = reinterpret_cast<uint32_t*>(take((size_t)nbk * 128));
     w.lm = reinterpret_cast<int*>(take(16));
     F.ws_ready = true;
     return BFP8_OK;
@@ -261,37 +250,6 @@ int state_out(DevState* st) {
     return BFP8_OK;
 }
 
-// Builds the GEMV descriptors and launches of a layer.
-int build_gemvs(FwdLayer& L, const std::vector<FwdGemv>& gv) {
-    Workspace& w = F.ws;
-    std::vector<Bfp8GemvDesc> d;
-    std::vector<bfp8_plan_item> items(gv.size());
-    for (size_t i = 0; i < gv.size(); ++i) {
-        items[i].M = gv[i].M;
-        items[i].K = gv[i].K;
-    }
-    int rc;
-    if (L.linear) {
-        d.push_back(plain_desc(w.qkv, w.xr_norm, w.xs_norm, gv[0].w.mant, gv[0].w.exps, kConv, kHidden, nullptr));
-        d.push_back(plain_desc(w.z, w.xr_norm, w.xs_norm, gv[1].w.mant, gv[1].w.exps, kHD, kHidden, nullptr));
-        d.push_back(plain_desc(w.o, w.xr_gated, w.xs_gated, gv[2].w.mant, gv[2].w.exps, kHidden, kHD, nullptr));
-        if ((rc = deal_tiles(L.l_qkvz, {0, 1}, items.data(), 0, true)) ||
-            (rc = deal_tiles(L.l_o, {2}, items.data(), 0, true)))
-            return rc;
-    }
-    const int g0 = L.linear ? 3 : 0;
-    d.push_back(plain_desc(w.gate, w.xr_post, w.xs_post, gv[g0].w.mant, gv[g0].w.exps, kMlp, kHidden, nullptr));
-    d.push_back(plain_desc(w.up, w.xr_post, w.xs_post, gv[g0 + 1].w.mant, gv[g0 + 1].w.exps, kMlp, kHidden, nullptr));
-    d.push_back(plain_desc(w.down, w.xr_inter, w.xs_inter, gv[g0 + 2].w.mant, gv[g0 + 2].w.exps, kHidden, kMlp,
-                           nullptr));
-    if ((rc = deal_tiles(L.l_gateup, {g0, g0 + 1}, items.data(), 0, true)) ||
-        (rc = deal_tiles(L.l_down, {g0 + 2}, items.data(), 0, true)))
-        return rc;
-    if ((rc = L.descs.reserve(d.size() * sizeof(Bfp8GemvDesc)))) return rc;
-    HIP_OK(hipMemcpy(L.descs.p, d.data(), d.size() * sizeof(Bfp8GemvDesc), hipMemcpyHostToDevice));
-    return BFP8_OK;
-}
-
 std::vector<char> key_of(const void* p, size_t n, char tag) {
     std::vector<char> k(n + 1);
     k[0] = tag;
@@ -316,22 +274,17 @@ int fwd_linear_layer(const LinearLayerPlan* p, FwdLayer** out) {
     L->linear = true;
     L->lp = *p;
     int rc;
-    std::vector<FwdGemv> gv(6);
     const int8_t* m[6] = {p->mant_qkv, p->mant_z, p->mant_o, p->mant_gate, p->mant_up, p->mant_down};
     const uint8_t* e[6] = {p->exp_qkv, p->exp_z, p->exp_o, p->exp_gate, p->exp_up, p->exp_down};
     const int Ms[6] = {p->M_qkv, p->M_z, p->M_o, p->M_gate, p->M_up, p->M_down};
     const int Ks[6] = {p->K_qkv, p->K_z, p->K_o, p->K_gate, p->K_up, p->K_down};
-    for (int i = 0; i < 6; ++i) {
-        gv[i].M = Ms[i];
-        gv[i].K = Ks[i];
-        if ((rc = fwd_planes(m[i], e[i], Ms[i], Ks[i], &gv[i].w))) return rc;
-    }
+    for (int i = 0; i < 6; ++i)
+        if ((rc = fwd_planes(m[i], e[i], Ms[i], Ks[i], &L->w[i]))) return rc;
     if ((rc = fwd_vec(p->in_ln_w, kHidden, &L->in_ln_w)) || (rc = fwd_vec(p->conv_w, (size_t)kConv * 4, &L->conv_w)) ||
         (rc = fwd_vec(p->wa, (size_t)RT_HEADS * kHidden, &L->wa)) ||
         (rc = fwd_vec(p->wb, (size_t)RT_HEADS * kHidden, &L->wb)) || (rc = fwd_vec(p->nea, RT_HEADS, &L->nea)) ||
         (rc = fwd_vec(p->dt, RT_HEADS, &L->dt)) || (rc = fwd_vec(p->norm_w, RT_HEAD_DIM, &L->norm_w)) ||
-        (rc = fwd_vec(p->post_ln_w, kHidden, &L->post_ln_w)) || (rc = fwd_state(p->conv_s, p->state, &L->st)) ||
-        (rc = build_gemvs(*L, gv)))
+        (rc = fwd_vec(p->post_ln_w, kHidden, &L->post_ln_w)) || (rc = fwd_state(p->conv_s, p->state, &L->st)))
         return rc;
     *out = L.get();
     F.layers.emplace(key, std::move(L));
@@ -354,17 +307,13 @@ int fwd_mlp_layer(const MlpPlan* p, FwdLayer** out) {
     L->linear = false;
     L->mp = *p;
     int rc;
-    std::vector<FwdGemv> gv(3);
     const int8_t* m[3] = {p->mant_gate, p->mant_up, p->mant_down};
     const uint8_t* e[3] = {p->exp_gate, p->exp_up, p->exp_down};
     const int Ms[3] = {p->M_gate, p->M_up, p->M_down};
     const int Ks[3] = {p->K_gate, p->K_up, p->K_down};
-    for (int i = 0; i < 3; ++i) {
-        gv[i].M = Ms[i];
-        gv[i].K = Ks[i];
-        if ((rc = fwd_planes(m[i], e[i], Ms[i], Ks[i], &gv[i].w))) return rc;
-    }
-    if ((rc = fwd_vec(p->post_ln_w, kHidden, &L->post_ln_w)) || (rc = build_gemvs(*L, gv))) return rc;
+    for (int i = 0; i < 3; ++i)
+        if ((rc = fwd_planes(m[i], e[i], Ms[i], Ks[i], &L->w[i]))) return rc;
+    if ((rc = fwd_vec(p->post_ln_w, kHidden, &L->post_ln_w))) return rc;
     *out = L.get();
     F.layers.emplace(key, std::move(L));
     return BFP8_OK;
@@ -384,102 +333,141 @@ struct Step {
     }
 };
 
-int launch_gemvs(const FwdLayer& L, const Launch& l) {
-    const Bfp8GemvDesc* d = L.descs.as<Bfp8GemvDesc>();
-    if (l.wide)
-        RT_LAUNCH(bfp8_launch_gemv_wide_grouped(d, l.tiles.as<Bfp8TileRef>(), l.ntiles, l.max_nb, g.stream));
-    else
-        RT_LAUNCH(bfp8_launch_gemv_grouped(d, l.tiles.as<Bfp8TileRef>(), l.wg_off.as<int>(), l.nwg, -1, g.stream));
-    return BFP8_OK;
+RtRowsGemv rows_gemv(const DevWeights& w, float* y, int M) {
+    RtRowsGemv r{};
+    r.mant = w.mant;
+    r.exps = w.exps;
+    r.y = y;
+    r.M = M;
+    r.pair_rows = M & ~1;
+    return r;
 }
 
-int gemv_step(const FwdLayer& L, const Launch& l) {
+int rows_step(const RtRowsArgs& a) {
     Step s(QP_GEMV);
-    int rc = launch_gemvs(L, l);
-    return rc ? rc : s.done();
+    RT_LAUNCH(rt_launch_rows(a, g.stream));
+    return s.done();
 }
 
-// rmsnorm of ws.h (after adding res, if any) into y, quantized into (xs, xr).
-int norm_step(const float* res, const float* w, float* y, float* xs, uint32_t* xr) {
+// The other buffer of the hidden state's ping-pong.
+float* other_h(const float* h) { return h == F.ws.h ? F.ws.h2 : F.ws.h; }
+
+// rmsnorm of *h (after adding res, if any) into y, in place (the final norm).
+int norm_step(float* h, const float* res, const float* w, float* y) {
     Step s(QP_RMSNORM);
     RtNormArgs a{};
-    a.h = F.ws.h;
+    a.h = h;
     a.res = res;
     a.w = w;
     a.y = y;
-    a.xscale = xs;
-    a.xsplit = xr;
     a.n = kHidden;
     a.eps = 1e-6f;
     RT_LAUNCH(rt_launch_rmsnorm(a, g.stream));
     return s.done();
 }
 
-// The MLP half shared by both layer kinds: rmsnorm(h + res) -> gate, up ->
-// swiglu -> down.  Leaves the down projection in ws.down (not yet added).
-int mlp_steps(const FwdLayer& L, const float* res) {
+// The MLP half shared by both layer kinds (planes gud = gate, up, down):
+// rmsnorm(h + res) -> gate, up in one launch; swiglu -> down in another.
+// *h moves to the other buffer when a residual is added.  Leaves the down
+// projection in ws.down, not yet added.
+int mlp_steps(const FwdLayer& L, const DevWeights* gud, float** h, const float* res) {
     Workspace& w = F.ws;
+    RtRowsArgs a{};
+    a.g[0] = rows_gemv(gud[0], w.gate, kMlp);
+    a.g[1] = rows_gemv(gud[1], w.up, kMlp);
+    a.ngemv = 2;
+    a.split = kMlp / 16;
+    a.K = kHidden;
+    a.mode = RT_ROWS_NORM;
+    a.h = *h;
+    a.res = res;
+    a.w = L.post_ln_w;
+    a.eps = 1e-6f;
+    a.h_out = res ? other_h(*h) : nullptr;
     int rc;
-    if ((rc = norm_step(res, L.post_ln_w, w.post, w.xs_post, w.xr_post)) || (rc = gemv_step(L, L.l_gateup)))
-        return rc;
-    {
-        Step s(QP_SWIGLU);
-        RtSwigluArgs a{};
-        a.y = w.inter;
-        a.gate = w.gate;
-        a.up = w.up;
-        a.xscale = w.xs_inter;
-        a.xsplit = w.xr_inter;
-        a.n = kMlp;
-        RT_LAUNCH(rt_launch_swiglu(a, g.stream));
-        if ((rc = s.done())) return rc;
-    }
-    return gemv_step(L, L.l_down);
+    if ((rc = rows_step(a))) return rc;
+    if (res) *h = a.h_out;
+    RtRowsArgs d{};
+    d.g[0] = rows_gemv(gud[2], w.down, kHidden);
+    d.ngemv = 1;
+    d.split = kHidden / 16;
+    d.K = kMlp;
+    d.mode = RT_ROWS_SWIGLU;
+    d.gate = w.gate;
+    d.up = w.up;
+    return rows_step(d);
 }
 
-// forward_linear_layer on the device: h in ws.h, `res` a pending residual to
-// add first (null for none).  Leaves the MLP's down projection in ws.down.
-int linear_steps(const FwdLayer& L, const float* res) {
+// forward_linear_layer on the device: *h the hidden state, res a pending
+// residual to add first (null for none).  Leaves the MLP's down projection in
+// ws.down.
+int linear_steps(const FwdLayer& L, float** h, const float* res) {
     Workspace& w = F.ws;
+    RtRowsArgs a{};
+    a.g[0] = rows_gemv(L.w[0], w.qkv, kConv);
+    a.g[1] = rows_gemv(L.w[1], w.z, kHD);
+    a.ngemv = 2;
+    a.split = kConv / 16;
+    a.K = kHidden;
+    a.mode = RT_ROWS_NORM;
+    a.h = *h;
+    a.res = res;
+    a.w = L.in_ln_w;
+    a.eps = 1e-6f;
+    a.y_norm = w.normed;
+    a.h_out = res ? other_h(*h) : nullptr;
     int rc;
-    if ((rc = norm_step(res, L.in_ln_w, w.normed, w.xs_norm, w.xr_norm)) || (rc = gemv_step(L, L.l_qkvz))) return rc;
+    if ((rc = rows_step(a))) return rc;
+    if (res) *h = a.h_out;
     {
         Step s(QP_GDN);
-        RtLinearAttnArgs a{};
-        a.qkv = w.qkv;
-        a.zbuf = w.z;
-        a.normed = w.normed;
-        a.conv_s = L.st->conv.as<float>();
-        a.conv_w = L.conv_w;
-        a.wa = L.wa;
-        a.wb = L.wb;
-        a.nea = L.nea;
-        a.dt = L.dt;
-        a.state = L.st->rec.as<float>();
-        a.norm_w = L.norm_w;
-        a.xscale = w.xs_gated;
-        a.xsplit = w.xr_gated;
-        RT_LAUNCH(rt_launch_linear_attn(a, g.stream));
+        RtLinearAttnArgs la{};
+        la.qkv = w.qkv;
+        la.zbuf = w.z;
+        la.normed = w.normed;
+        la.conv_s = L.st->conv.as<float>();
+        la.conv_w = L.conv_w;
+        la.wa = L.wa;
+        la.wb = L.wb;
+        la.nea = L.nea;
+        la.dt = L.dt;
+        la.state = L.st->rec.as<float>();
+        la.norm_w = L.norm_w;
+        la.xscale = w.xs_gated;
+        la.xsplit = w.xr_gated;
+        RT_LAUNCH(rt_launch_linear_attn(la, g.stream));
         if ((rc = s.done())) return rc;
     }
-    if ((rc = gemv_step(L, L.l_o))) return rc;
-    return mlp_steps(L, w.o);
+    RtRowsArgs o{};
+    o.g[0] = rows_gemv(L.w[2], w.o, kHidden);
+    o.ngemv = 1;
+    o.split = kHidden / 16;
+    o.K = kHD;
+    o.mode = RT_ROWS_QUANTIZED;
+    o.xsplit = w.xr_gated;
+    o.xscale = w.xs_gated;
+    if ((rc = rows_step(o))) return rc;
+    return mlp_steps(L, &L.w[3], h, w.o);
 }
 
-int add_pending(const float* res) {
+int layer_steps(const FwdLayer& L, float** h, const float* res) {
+    return L.linear ? linear_steps(L, h, res) : mlp_steps(L, &L.w[0], h, res);
+}
+
+int add_pending(float* h, const float* res) {
     if (!res) return BFP8_OK;
     Step s(QP_RESID);
-    RT_LAUNCH(rt_launch_add_residual(F.ws.h, res, kHidden, g.stream));
+    RT_LAUNCH(rt_launch_add_residual(h, res, kHidden, g.stream));
     return s.done();
 }
 
-int h_in(const float* h) {
-    HIP_OK(hipMemcpyAsync(F.ws.h, h, (size_t)kHidden * 4, hipMemcpyHostToDevice, g.stream));
+int h_in(float* dev, const float* h) {
+    HIP_OK(hipMemcpyAsync(dev, h, (size_t)kHidden * 4, hipMemcpyHostToDevice, g.stream));
     return BFP8_OK;
 }
 
-int h_out(float* h) {
-    HIP_OK(hipMemcpyAsync(h, F.ws.h, (size_t)kHidden * 4, hipMemcpyDeviceToHost, g.stream));
+int h_out(float* h, const float* dev) {
+    HIP_OK(hipMemcpyAsync(h, dev, (size_t)kHidden * 4, hipMemcpyDeviceToHost, g.stream));
     HIP_OK(hipStreamSynchronize(g.stream));
     return BFP8_OK;
 }
@@ -524,23 +512,16 @@ int layer_call(const FwdLayer& L, float* h, int slot) {
     const double t0 = g_prof_on ? now_ms() : 0.0;
     int rc;
     const std::vector<FwdLayer*> one{const_cast<FwdLayer*>(&L)};
-    if ((rc = h_in(h)) || (rc = states_in(one))) return rc;
-    if ((rc = L.linear ? linear_steps(L, nullptr) : mlp_steps(L, nullptr)) || (rc = add_pending(F.ws.down))) return rc;
+    float* hd = F.ws.h;
+    if ((rc = h_in(hd, h)) || (rc = states_in(one))) return rc;
+    if ((rc = layer_steps(L, &hd, nullptr)) || (rc = add_pending(hd, F.ws.down))) return rc;
     if ((rc = states_out(one))) return rc;
-    if ((rc = h_out(h))) return rc;
+    if ((rc = h_out(h, hd))) return rc;
     if (g_prof_on) g_prof_ms[slot] += now_ms() - t0;
     return BFP8_OK;
 }
 
 void drop_forward() {
-    for (auto& kv : F.layers) {
-        FwdLayer& L = *kv.second;
-        L.descs.release();
-        for (Launch* l : {&L.l_qkvz, &L.l_o, &L.l_gateup, &L.l_down}) {
-            l->tiles.release();
-            l->wg_off.release();
-        }
-    }
     F.layers.clear();
     for (auto& kv : F.params) kv.second.release();
     F.params.clear();
@@ -802,12 +783,13 @@ int forward_token_c(int token_id, float* h, const LinearLayerPlan* linear_plans,
         RT_CHECK("forward_token_c", fwd_vec(embed_table, (size_t)kVocab * kHidden, &table));
     }
     Workspace& w = F.ws;
+    float* hd = w.h;  // the hidden state on the device
     RT_CHECK("forward_token_c", states_in(layers));
     {
         Step s(QP_EMBED);
         int row = token_id % kVocab;
         if (row < 0) row += kVocab;
-        if (rt_launch_embed(w.h, table, row, kHidden, g.stream) != hipSuccess) {
+        if (rt_launch_embed(hd, table, row, kHidden, g.stream) != hipSuccess) {
             set_error("embedding launch failed");
             fatal("forward_token_c");
         }
@@ -819,25 +801,25 @@ int forward_token_c(int token_id, float* h, const LinearLayerPlan* linear_plans,
         const double t_layer = g_prof_on ? now_ms() : 0.0;
         if (layer_is_full[l]) {
             if (full_attn_cb) {
-                RT_CHECK("forward_token_c", add_pending(pending));
+                RT_CHECK("forward_token_c", add_pending(hd, pending));
                 pending = nullptr;
-                RT_CHECK("forward_token_c", h_out(h));
+                RT_CHECK("forward_token_c", h_out(h, hd));
                 const double t_cb = g_prof_on ? now_ms() : 0.0;
                 lk.unlock();
                 full_attn_cb(l, h, py_context);
                 lk.lock();
                 if (g_prof_on) g_prof_ms[QP_PYCALLBACK] += now_ms() - t_cb;
-                RT_CHECK("forward_token_c", h_in(h));
+                RT_CHECK("forward_token_c", h_in(hd, h));
             }
-            RT_CHECK("forward_token_c", mlp_steps(L, pending));
+            RT_CHECK("forward_token_c", layer_steps(L, &hd, pending));
             if (g_prof_on) g_prof_ms[QP_MLP] += now_ms() - t_layer;
         } else {
-            RT_CHECK("forward_token_c", linear_steps(L, pending));
+            RT_CHECK("forward_token_c", layer_steps(L, &hd, pending));
             if (g_prof_on) g_prof_ms[QP_LINEAR] += now_ms() - t_layer;
         }
         pending = w.down;
     }
-    RT_CHECK("forward_token_c", norm_step(pending, fnorm, w.normed, nullptr, nullptr));
+    RT_CHECK("forward_token_c", norm_step(hd, pending, fnorm, w.normed));
     {
         Step s(QP_LMHEAD);
         RT_CHECK("forward_token_c", bf16_lm_head_dev(w.lm, reinterpret_cast<float*>(w.lm + 1), w.lm + 2, w.lm + 3,
@@ -850,7 +832,7 @@ int forward_token_c(int token_id, float* h, const LinearLayerPlan* linear_plans,
         fatal("forward_token_c");
     }
     RT_CHECK("forward_token_c", states_out(layers));
-    RT_CHECK("forward_token_c", h_out(h));
+    RT_CHECK("forward_token_c", h_out(h, hd));
     if (g_prof_on) g_prof_ms[QP_TOTAL] += now_ms() - t_total;
     return out[3];
 }

@@ -7,9 +7,9 @@
 // Compiled with f32 flush-to-zero and -ffp-contract=off: a plain float
 // operation here is one Advanced SIMD operation of the reference (vmulq,
 // vaddq, vsubq; vmlaq = product rounded, then sum rounded).  The reference's
-// scalar VFP steps keep IEEE subnormals; they go through ieee_*() below,
-// which compute in double and round once to float by hand, so they do not
-// depend on the f32 denormal mode.  expf / log1pf of the reference's libm are
+// scalar VFP steps keep IEEE subnormals; they go through ieee_*() of
+// runtime_dev.h, which compute in double and round once to float by hand, so
+// they do not depend on the f32 denormal mode.  expf / log1pf of the reference's libm are
 // taken as exp / log1p in double rounded to float.
 //
 // Reductions follow the reference's 4-lane accumulators: lane j adds the
@@ -18,243 +18,8 @@
 #include <hip/hip_runtime.h>
 
 #include "quant_block.h"
+#include "runtime_dev.h"
 #include "runtime_internal.h"
-
-namespace {
-
-// ---- exact scalar IEEE steps inside a flush-to-zero unit ----------------------------
-// float -> double, subnormals included (bit-built, so no conversion flushes them)
-__device__ __forceinline__ double widen(float x) {
-    const uint32_t u = __float_as_uint(x);
-    if ((u & 0x7f800000u) == 0u) {
-        const double m = (double)(u & 0x007fffffu) * 0x1p-149;
-        return (u >> 31) ? -m : m;
-    }
-    return (double)x;
-}
-
-// double -> float, round to nearest even, subnormal results built by hand.
-// The operations below round twice (to double, then to float); with 53 >=
-// 2*24 + 2 bits that never changes a product, sum, quotient or square root of
-// floats.
-__device__ __forceinline__ float narrow(double r) {
-    const double a = __builtin_fabs(r);
-    if (!(a < 0x1p-126)) return (float)r;  // normal, inf, NaN
-    const uint32_t m = (uint32_t)__builtin_rint(a * 0x1p149);  // <= 2^23 (2^23 = FLT_MIN)
-    return __uint_as_float(m | (__builtin_signbit(r) ? 0x80000000u : 0u));
-}
-
-__device__ __forceinline__ float ieee_mul(float a, float b) { return narrow(widen(a) * widen(b)); }
-__device__ __forceinline__ float ieee_add(float a, float b) { return narrow(widen(a) + widen(b)); }
-__device__ __forceinline__ float ieee_div(float a, float b) { return narrow(widen(a) / widen(b)); }
-__device__ __forceinline__ float ieee_sqrt(float a) { return narrow(__builtin_sqrt(widen(a))); }
-__device__ __forceinline__ float libm_expf(float x) { return narrow(exp(widen(x))); }
-__device__ __forceinline__ float libm_log1pf(float x) { return narrow(log1p(widen(x))); }
-
-// ---- exp_neon, 04/qwen_kernels_opt.c:332-352 --------------------------------------
-// Clamp to [-87, 88] (a NaN stays NaN), n = round(x*log2 e) by adding and
-// subtracting 1.5*2^23, f = x*log2 e - n, degree-6 Horner polynomial in f,
-// times 2^n built from the exponent bits (vcvtq_s32_f32 of NaN is 0).  The
-// constants are the reference's: the polynomial is part of the result.
-__device__ __forceinline__ float exp_neon(float x) {
-    x = (x < -87.0f) ? -87.0f : x;
-    x = (x > 88.0f) ? 88.0f : x;
-    const float fx = x * 1.44269504088896341f;
-    const float t = fx + 12582912.0f;
-    const float n = t - 12582912.0f;
-    const float f = fx - n;
-    float p = 1.5403530393381608e-4f;
-    p = 1.3333558146428443e-3f + p * f;
-    p = 9.6181291076284770e-3f + p * f;
-    p = 5.5504108664821580e-2f + p * f;
-    p = 2.4022650695910070e-1f + p * f;
-    p = 6.9314718055994530e-1f + p * f;
-    p = 1.0f + p * f;
-    const int e = (n == n) ? (int)n : 0;
-    return p * __int_as_float((e + 127) << 23);
-}
-
-// ---- 4-lane residue sums -------------------------------------------------------------
-constexpr int kChunk = 1024;              // elements staged per pass
-constexpr int kPitch = kChunk / 4 + 4;    // floats per residue row (16-byte rows, 4-bank offset)
-
-struct ResidueLds {
-    float p[2][4][kPitch];
-    float out[2];
-};
-
-__device__ __forceinline__ float chain_add(float s, const float* p, int cnt) {
-    int m = 0;
-#pragma unroll 4
-    for (; m + 4 <= cnt; m += 4) {
-        const float4 v = *reinterpret_cast<const float4*>(p + m);
-        s = s + v.x;
-        s = s + v.y;
-        s = s + v.z;
-        s = s + v.w;
-    }
-    for (; m < cnt; ++m) s = s + p[m];
-    return s;
-}
-
-// Sums over the vector part [0, 4*(n/4)) of one or two product sequences,
-// prod0(e) and prod1(e), in the 4-lane order; every thread of the block calls
-// it (same n) and gets (sum0, sum1).  Staging hands element e to thread
-// e % blockDim.x of each chunk.
-template <class F0, class F1>
-__device__ float2 residue_sums(int n, bool two, F0 prod0, F1 prod1, ResidueLds& L) {
-    const int tid = threadIdx.x, nthr = blockDim.x;
-    const int nv = n & ~3;
-    const int seq = tid >> 2, j = tid & 3;
-    const bool chains = tid < (two ? 8 : 4);
-    float s = 0.0f;
-    for (int base = 0; base < nv; base += kChunk) {
-        const int cnt = min(kChunk, nv - base);
-        for (int e = tid; e < cnt; e += nthr) {
-            L.p[0][e & 3][e >> 2] = prod0(base + e);
-            if (two) L.p[1][e & 3][e >> 2] = prod1(base + e);
-        }
-        __syncthreads();
-        if (chains) s = chain_add(s, &L.p[seq][j][0], cnt >> 2);
-        __syncthreads();
-    }
-    if (tid < 64) {
-        const int g = tid & ~3;
-        const float l0 = __shfl(s, g + 0, 64), l1 = __shfl(s, g + 1, 64);
-        const float l2 = __shfl(s, g + 2, 64), l3 = __shfl(s, g + 3, 64);
-        const float r = (l0 + l2) + (l1 + l3);
-        if (tid == 0) L.out[0] = r;
-        if (tid == 4) L.out[1] = r;
-    }
-    __syncthreads();
-    const float2 r = make_float2(L.out[0], L.out[1]);
-    __syncthreads();
-    return r;
-}
-
-// ---- per-element pieces --------------------------------------------------------------
-// swiglu element: vector part s = g / (1 + exp_neon(-g)) (scalar division of
-// div_neon), y = s * up; scalar tail with expf.
-__device__ __forceinline__ float swiglu_elem(float g, float u, bool vec) {
-    if (vec) return ieee_div(g, 1.0f + exp_neon(-g)) * u;
-    return ieee_mul(ieee_div(g, ieee_add(1.0f, libm_expf(-g))), u);
-}
-
-// conv1d + SiLU of one channel; shifts the three taps.
-__device__ __forceinline__ float conv_elem(float xc, float* s0, float* s1, float* s2, const float* w, bool vec) {
-    const float t0 = *s0, t1 = *s1, t2 = *s2;
-    float y;
-    if (vec) {
-        float d = w[0] * t0;
-        d = d + w[1] * t1;
-        d = d + w[2] * t2;
-        d = d + w[3] * xc;
-        y = ieee_div(d, 1.0f + exp_neon(-d));
-    } else {
-        float dot = ieee_add(ieee_mul(w[0], t0), ieee_mul(w[1], t1));
-        dot = ieee_add(dot, ieee_mul(w[2], t2));
-        dot = ieee_add(dot, ieee_mul(w[3], xc));
-        y = ieee_div(dot, ieee_add(1.0f, libm_expf(-dot)));
-    }
-    *s0 = t1;
-    *s1 = t2;
-    *s2 = xc;
-    return y;
-}
-
-// 1 / sqrtf(ss / n + eps), scalar
-__device__ __forceinline__ float rms_scale(float ss, int n, float eps) {
-    return ieee_div(1.0f, ieee_sqrt(ieee_add(ieee_div(ss, (float)n), eps)));
-}
-
-// gated RMSNorm element: ((x * r) * w) * (z / (1 + expf(-z))), scalar
-__device__ __forceinline__ float gated_elem(float x, float r, float w, float z) {
-    const float silu = ieee_div(z, ieee_add(1.0f, libm_expf(-z)));
-    return ieee_mul(ieee_mul(ieee_mul(x, r), w), silu);
-}
-
-// gdn gates of one head from the two dot products: beta = 1/(1 + expf(-bv)),
-// alpha = expf(nea * log1pf(expf(av + dt))).
-__device__ __forceinline__ void gates_scalar(float av, float bv, float nea, float dt, float* alpha, float* beta) {
-    *beta = ieee_div(1.0f, ieee_add(1.0f, libm_expf(-bv)));
-    const float z = ieee_add(av, dt);
-    *alpha = libm_expf(ieee_mul(nea, libm_log1pf(libm_expf(z))));
-}
-
-// One state column j of one head, both passes of the reference's blocked
-// kernel: kv = sum_i k[i] S[i][j], qs = sum_i q[i] S[i][j] (ascending i),
-// d = (v - kv*a) * b, out = qs*a + qk*d, then S[i][j] = S[i][j]*a + d*k[i].
-// S = the head's blocked state; qh, kh = the head's q and k (LDS).  kNG > 0:
-// ng == kNG and the column stays in registers between the passes.
-template <int kNG>
-__device__ __forceinline__ float gdn_column(float* S, int ng, int j, const float* qh, const float* kh, float vj,
-                                            float a, float b, float qk) {
-    float* col = S + ((size_t)(j >> 2) * ng * 4 + (j & 3)) * 4;
-    float kv = 0.0f, qs = 0.0f;
-    if constexpr (kNG > 0) {
-        float4 s[kNG];
-#pragma unroll
-        for (int ig = 0; ig < kNG; ++ig) s[ig] = *reinterpret_cast<const float4*>(col + ig * 16);
-#pragma unroll
-        for (int ig = 0; ig < kNG; ++ig) {
-            const float4 k4 = *reinterpret_cast<const float4*>(kh + 4 * ig);
-            const float4 q4 = *reinterpret_cast<const float4*>(qh + 4 * ig);
-            kv = kv + s[ig].x * k4.x;
-            qs = qs + s[ig].x * q4.x;
-            kv = kv + s[ig].y * k4.y;
-            qs = qs + s[ig].y * q4.y;
-            kv = kv + s[ig].z * k4.z;
-            qs = qs + s[ig].z * q4.z;
-            kv = kv + s[ig].w * k4.w;
-            qs = qs + s[ig].w * q4.w;
-        }
-        const float d = (vj - kv * a) * b;
-        const float out = qs * a + qk * d;
-#pragma unroll
-        for (int ig = 0; ig < kNG; ++ig) {
-            const float4 k4 = *reinterpret_cast<const float4*>(kh + 4 * ig);
-            float4 nv;
-            nv.x = s[ig].x * a + d * k4.x;
-            nv.y = s[ig].y * a + d * k4.y;
-            nv.z = s[ig].z * a + d * k4.z;
-            nv.w = s[ig].w * a + d * k4.w;
-            *reinterpret_cast<float4*>(col + ig * 16) = nv;
-        }
-        return out;
-    } else {
-        for (int ig = 0; ig < ng; ++ig) {
-            const float4 s4 = *reinterpret_cast<const float4*>(col + ig * 16);
-            const float4 k4 = *reinterpret_cast<const float4*>(kh + 4 * ig);
-            const float4 q4 = *reinterpret_cast<const float4*>(qh + 4 * ig);
-            kv = kv + s4.x * k4.x;
-            qs = qs + s4.x * q4.x;
-            kv = kv + s4.y * k4.y;
-            qs = qs + s4.y * q4.y;
-            kv = kv + s4.z * k4.z;
-            qs = qs + s4.z * q4.z;
-            kv = kv + s4.w * k4.w;
-            qs = qs + s4.w * q4.w;
-        }
-        const float d = (vj - kv * a) * b;
-        const float out = qs * a + qk * d;
-        for (int ig = 0; ig < ng; ++ig) {
-            const float4 s4 = *reinterpret_cast<const float4*>(col + ig * 16);
-            const float4 k4 = *reinterpret_cast<const float4*>(kh + 4 * ig);
-            float4 nv;
-            nv.x = s4.x * a + d * k4.x;
-            nv.y = s4.y * a + d * k4.y;
-            nv.z = s4.z * a + d * k4.z;
-            nv.w = s4.w * a + d * k4.w;
-            *reinterpret_cast<float4*>(col + ig * 16) = nv;
-        }
-        return out;
-    }
-}
-
-__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
-__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
-
-}  // namespace
 
 // ---- rmsnorm (+ residual, + quantize): one workgroup of 256 ----------------------------
 extern "C" __global__ __launch_bounds__(256) void rt_rmsnorm_kernel(RtNormArgs a) {
@@ -433,77 +198,158 @@ extern "C" __global__ __launch_bounds__(256) void rt_embed_kernel(float* h, cons
 }
 
 // ---- the model's linear-attention block, one workgroup per head ---------------------------
+// Work that does not depend on each other overlaps.  Wavefronts 2-3 own the
+// state columns and issue their loads first (a wavefront's loads complete in
+// order, so nothing else is queued behind them); wavefronts 0-1 stage the
+// gates' products, then wavefront 0 runs the gates' two 256-step sums while
+// wavefront 1 runs the conv over the head's q, k, v channels; the short
+// 32-step sums (q/k norms, q.k, the gated norm) then share one staging
+// buffer between barriers.
 extern "C" __global__ __launch_bounds__(256) void rt_linear_attn_kernel(RtLinearAttnArgs a) {
-    constexpr int D = RT_HEAD_DIM, C = RT_CONV_CH, HD = RT_HEADS * RT_HEAD_DIM;
+    constexpr int D = RT_HEAD_DIM, NG = D / 4, C = RT_CONV_CH, HD = RT_HEADS * RT_HEAD_DIM, KG = RT_HIDDEN;
+    static_assert(D == 128 && KG / 4 <= kPitch, "staging sized for 16 heads of 128 and a 1024 gate input");
     __shared__ ResidueLds L;
     __shared__ uint32_t rec[4][32];
     __shared__ __attribute__((aligned(16))) float qv[D];
     __shared__ __attribute__((aligned(16))) float kv[D];
     __shared__ float vv[D];
     __shared__ float ov[D];
-    __shared__ float sc[4];
-    const int h = blockIdx.x, tid = threadIdx.x;
+    __shared__ float sc[6];
+    const int h = blockIdx.x, tid = threadIdx.x, w = wave_id(), lane = lane_id();
+    const bool col_thread = tid >= 128;  // wavefronts 2-3: column j = tid - 128
+    const int j = tid - 128;
 
-    // conv1d + SiLU over this head's q, k and v channels (all in the vector part)
-    for (int i = tid; i < 3 * D; i += 256) {
-        const int part = i / D, jj = i - part * D;
-        const int c = part * HD + h * D + jj;
-        const float y = conv_elem(a.qkv[c], a.conv_s + c, a.conv_s + C + c, a.conv_s + 2 * C + c,
-                                  a.conv_w + (size_t)c * 4, c < (C & ~3));
-        (part == 0 ? qv : part == 1 ? kv : vv)[jj] = y;
-        if (part == 2 && a.mixed) a.mixed[c] = y;
-    }
-    __syncthreads();
-
-    // gates from the input-norm output
-    const float* ra = a.wa + (size_t)h * RT_HIDDEN;
-    const float* rb = a.wb + (size_t)h * RT_HIDDEN;
-    const float* x = a.normed;
-    const float2 ab = residue_sums(RT_HIDDEN, true, [&](int e) { return ra[e] * x[e]; },
-                                   [&](int e) { return rb[e] * x[e]; }, L);
-    // q/k L2 norm sums
-    const float2 sq = residue_sums(D, true, [&](int e) { return kv[e] * kv[e]; },
-                                   [&](int e) { return qv[e] * qv[e]; }, L);
-    if (tid == 0) {
-        gates_scalar(ab.x, ab.y, a.nea[h], a.dt[h], &sc[0], &sc[1]);
-        const float q_scale = ieee_div(1.0f, ieee_sqrt((float)D));
-        sc[2] = ieee_div(1.0f, ieee_sqrt(ieee_add(sq.x, 1e-6f)));
-        sc[3] = ieee_div(q_scale, ieee_sqrt(ieee_add(sq.y, 1e-6f)));
-        if (a.alpha_beta) {
-            a.alpha_beta[h] = sc[0];
-            a.alpha_beta[RT_HEADS + h] = sc[1];
+    // the state column, in flight from the start
+    float* col = a.state + (size_t)h * D * D + ((size_t)(j >> 2) * NG * 4 + (j & 3)) * 4;
+    float4 st[NG];
+    if (col_thread) {
+#pragma unroll
+        for (int ig = 0; ig < NG; ++ig) st[ig] = *reinterpret_cast<const float4*>(col + ig * 16);
+    } else {
+        // gates' products wa[h] * x, wb[h] * x over the input-norm output
+        const float* ra = a.wa + (size_t)h * KG;
+        const float* rb = a.wb + (size_t)h * KG;
+#pragma unroll
+        for (int k = 0; k < KG / 128; ++k) {
+            const int e = tid + 128 * k;
+            const float x = a.normed[e];
+            L.p[0][e & 3][e >> 2] = ra[e] * x;
+            L.p[1][e & 3][e >> 2] = rb[e] * x;
         }
     }
     __syncthreads();
-    const float alpha = sc[0], beta = sc[1];
+    if (w == 0) {
+        // av = wa[h] . x, bv = wb[h] . x in the 4-lane order, then the scalar part
+        float s = 0.0f;
+        if (lane < 8) s = chain_add(0.0f, &L.p[lane >> 2][lane & 3][0], KG / 4);
+        const float r = lanes4_combine(s);
+        const float bv = __shfl(r, 4, 64);
+        if (lane == 0) gates_scalar(r, bv, a.nea[h], a.dt[h], &sc[0], &sc[1]);
+    } else if (w == 1) {
+        // conv1d + SiLU over the head's q, k and v channels (all in the vector part)
+#pragma unroll
+        for (int k = 0; k < 3 * D / 64; ++k) {
+            const int i = lane + 64 * k;
+            const int part = i / D, jj = i - part * D;
+            const int c = part * HD + h * D + jj;
+            const float y = conv_elem(a.qkv[c], a.conv_s + c, a.conv_s + C + c, a.conv_s + 2 * C + c,
+                                      a.conv_w + (size_t)c * 4, c < (C & ~3));
+            (part == 0 ? qv : part == 1 ? kv : vv)[jj] = y;
+            if (part == 2 && a.mixed) a.mixed[c] = y;
+        }
+    }
+    __syncthreads();
+
+    // q/k L2 norm
     if (tid < D) {
-        kv[tid] = kv[tid] * sc[2];
-        qv[tid] = qv[tid] * sc[3];
+        const int e = tid;
+        L.p[0][e & 3][e >> 2] = kv[e] * kv[e];
+        L.p[1][e & 3][e >> 2] = qv[e] * qv[e];
+    }
+    __syncthreads();
+    if (w == 0) {
+        float s = 0.0f;
+        if (lane < 8) s = chain_add(0.0f, &L.p[lane >> 2][lane & 3][0], NG);
+        const float r = lanes4_combine(s);
+        const float q_sq = __shfl(r, 4, 64);
+        if (lane == 0) {
+            const float q_scale = ieee_div(1.0f, ieee_sqrt((float)D));
+            sc[2] = ieee_div(1.0f, ieee_sqrt(ieee_add(r, 1e-6f)));
+            sc[3] = ieee_div(q_scale, ieee_sqrt(ieee_add(q_sq, 1e-6f)));
+            if (a.alpha_beta) {
+                a.alpha_beta[h] = sc[0];
+                a.alpha_beta[RT_HEADS + h] = sc[1];
+            }
+        }
+    }
+    __syncthreads();
+    if (tid < D) {
+        const float k = kv[tid] * sc[2], q = qv[tid] * sc[3];
+        kv[tid] = k;
+        qv[tid] = q;
+        L.p[0][tid & 3][tid >> 2] = q * k;  // the q.k sum's products
         if (a.mixed) {
-            a.mixed[h * D + tid] = qv[tid];
-            a.mixed[HD + h * D + tid] = kv[tid];
+            a.mixed[h * D + tid] = q;
+            a.mixed[HD + h * D + tid] = k;
         }
     }
     __syncthreads();
+    if (w == 0) {
+        float s = 0.0f;
+        if (lane < 4) s = chain_add(0.0f, &L.p[0][lane][0], NG);
+        const float r = lanes4_combine(s);
+        if (lane == 0) sc[4] = r;
+    }
+    __syncthreads();
 
-    // recurrent step
-    const float qk = residue_sums(D, false, [&](int e) { return qv[e] * kv[e]; }, [](int) { return 0.0f; }, L).x;
-    if (tid < D) {
-        const float o = gdn_column<D / 4>(a.state + (size_t)h * D * D, D / 4, tid, qv, kv, vv[tid], alpha, beta, qk);
-        ov[tid] = o;
-        if (a.attn) a.attn[h * D + tid] = o;
+    // recurrent step on the column held in registers
+    if (col_thread) {
+        const float alpha = sc[0], beta = sc[1], qk = sc[4];
+        float kvs = 0.0f, qss = 0.0f;
+#pragma unroll
+        for (int ig = 0; ig < NG; ++ig) {
+            const float4 k4 = *reinterpret_cast<const float4*>(kv + 4 * ig);
+            const float4 q4 = *reinterpret_cast<const float4*>(qv + 4 * ig);
+            kvs = kvs + st[ig].x * k4.x;
+            qss = qss + st[ig].x * q4.x;
+            kvs = kvs + st[ig].y * k4.y;
+            qss = qss + st[ig].y * q4.y;
+            kvs = kvs + st[ig].z * k4.z;
+            qss = qss + st[ig].z * q4.z;
+            kvs = kvs + st[ig].w * k4.w;
+            qss = qss + st[ig].w * q4.w;
+        }
+        const float d = (vv[j] - kvs * alpha) * beta;
+        const float o = qss * alpha + qk * d;
+#pragma unroll
+        for (int ig = 0; ig < NG; ++ig) {
+            const float4 k4 = *reinterpret_cast<const float4*>(kv + 4 * ig);
+            float4 nv;
+            nv.x = st[ig].x * alpha + d * k4.x;
+            nv.y = st[ig].y * alpha + d * k4.y;
+            nv.z = st[ig].z * alpha + d * k4.z;
+            nv.w = st[ig].w * alpha + d * k4.w;
+            *reinterpret_cast<float4*>(col + ig * 16) = nv;
+        }
+        ov[j] = o;
+        L.p[1][j & 3][j >> 2] = o * o;  // the gated norm's products
+        if (a.attn) a.attn[h * D + j] = o;
     }
     __syncthreads();
 
     // gated RMSNorm + quantizer of the o GEMV's input (two blocks per head)
-    const float ss = residue_sums(D, false, [&](int e) { return ov[e] * ov[e]; }, [](int) { return 0.0f; }, L).x;
-    if (tid == 0) sc[0] = rms_scale(ss, D, 1e-6f);
+    if (w == 0) {
+        float s = 0.0f;
+        if (lane < 4) s = chain_add(0.0f, &L.p[1][lane][0], NG);
+        const float r = lanes4_combine(s);
+        if (lane == 0) sc[5] = rms_scale(r, D, 1e-6f);
+    }
     __syncthreads();
-    if (tid < D) {
-        const float y = gated_elem(ov[tid], sc[0], a.norm_w[tid], a.zbuf[h * D + tid]);
-        if (a.gated) a.gated[h * D + tid] = y;
-        const int b = h * (D / 64) + wave_id();
-        bfp8_quant_block_wave(y, lane_id(), nullptr, a.xscale + b, a.xsplit + (size_t)b * 32, rec[wave_id()]);
+    if (col_thread) {
+        const float y = gated_elem(ov[j], sc[5], a.norm_w[j], a.zbuf[h * D + j]);
+        if (a.gated) a.gated[h * D + j] = y;
+        const int b = h * (D / 64) + (w - 2);
+        bfp8_quant_block_wave(y, lane, nullptr, a.xscale + b, a.xsplit + (size_t)b * 32, rec[w]);
     }
 }
 

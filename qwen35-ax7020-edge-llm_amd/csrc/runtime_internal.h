@@ -105,6 +105,39 @@ struct RtLinearAttnArgs {
     float* alpha_beta;    // optional [32]: alpha[16], beta[16]
 };
 
+// The forward's GEMVs (fused_gemv.hip): one or two GEMVs sharing one
+// activation, 16 rows per workgroup; the activation is given quantized or is
+// computed by every workgroup from its inputs.
+#define RT_ROWS_QUANTIZED 0  // xsplit / xscale given
+#define RT_ROWS_NORM 1       // rmsnorm(h + res) with weight w, eps
+#define RT_ROWS_SWIGLU 2     // swiglu(gate, up)
+#define RT_ROWS_MAX_K 4096
+struct RtRowsGemv {
+    const uint8_t* mant;  // GPU planes (bfp8_layout.h)
+    const uint8_t* exps;
+    float* y;
+    int M;
+    int pair_rows;        // rows written: M & ~1 (an odd last row takes the tail kernel)
+};
+struct RtRowsArgs {
+    RtRowsGemv g[2];
+    int ngemv;            // 1 or 2
+    int split;            // workgroups of g[0]: ceil(g[0].M / 16)
+    int K;
+    int mode;
+    const uint32_t* xsplit;  // RT_ROWS_QUANTIZED
+    const float* xscale;
+    const float* h;          // RT_ROWS_NORM: x = h (+ res)
+    const float* res;
+    const float* w;
+    float eps;
+    float* h_out;            // optional: workgroup 0 writes x (must not alias h)
+    float* y_norm;           // optional: workgroup 0 writes the normalised vector
+    const float* gate;       // RT_ROWS_SWIGLU
+    const float* up;
+};
+hipError_t rt_launch_rows(const RtRowsArgs& a, hipStream_t s);
+
 hipError_t rt_launch_rmsnorm(const RtNormArgs& a, hipStream_t s);
 hipError_t rt_launch_swiglu(const RtSwigluArgs& a, hipStream_t s);
 hipError_t rt_launch_conv1d(const RtConvArgs& a, hipStream_t s);

@@ -403,4 +403,5 @@ def test_profiler_slots(gpu, model):
     finally:
         lib.qwen_prof_enable(0)
     t = [lib.qwen_prof_get(i) for i in range(15)]
-    assert t[0] > 0 and t[2] > 0 and t[5] > 0 and t[12] > 0 and t[14] == 0
+    # norms and swiglu run inside the GEMV launches (booked to bfp8_gemv)
+    assert t[0] > 0 and t[2] > 0 and t[12] > 0 and t[14] == 0
