@@ -41,6 +41,8 @@ struct RowsLds {
     float xsc[kMaxNb];                                       // block scales
     float terms[kMaxNb][64];                                 // t2 per block and lane
     ResidueLds res;             // rmsnorm's sum of squares
+    float gp[RT_HEADS][4][36];  // the gated norm's per-head products (16-byte rows)
+    float gr[RT_HEADS];         // ... and per-head scales
     uint32_t rec[kWaves][32];   // quantizer scratch, one per wavefront
     float scale;
 };
@@ -77,6 +79,14 @@ __device__ __forceinline__ void load_prologue(const RtRowsArgs& a, PrologueIn<kE
             const int e = min(tid + kThreads * k, n - 1);
             in.a[k] = a.gate[e];
             in.b[k] = a.up[e];
+        }
+    } else if constexpr (kMode == RT_ROWS_GATED) {
+#pragma unroll
+        for (int k = 0; k < kE; ++k) {
+            const int e = min(tid + kThreads * k, n - 1);
+            in.a[k] = a.attn[e];
+            in.b[k] = a.zsilu[e];
+            in.c[k] = a.w[e & (RT_HEAD_DIM - 1)];
         }
     } else {
         const int nb = n >> 6;
@@ -131,6 +141,47 @@ __device__ __forceinline__ void norm_prologue(const RtRowsArgs& a, const Prologu
     }
 }
 
+// rmsnorm_gated(attn, z) over heads of 128 (04/qwen_kernels_opt.c:818-847)
+// into the LDS activation (n = 16 * 128).  Per head: the 4-lane sum of
+// squares (one lane per head and residue, all 64 lanes of wavefront 0), the
+// scalar scale, then ((x * r) * w) * silu(z) per element in IEEE arithmetic
+// (silu(z) computed once by the attention kernel).
+template <int kE>
+__device__ __forceinline__ void gated_prologue(const RtRowsArgs& a, const PrologueIn<kE>& in, RowsLds& L) {
+    const int tid = threadIdx.x, n = a.K, nb = n >> 6;
+#pragma unroll
+    for (int k = 0; k < kE; ++k) {
+        const int e = tid + kThreads * k;
+        if (e < n) {
+            const int i = e & (RT_HEAD_DIM - 1);
+            L.gp[e / RT_HEAD_DIM][i & 3][i >> 2] = in.a[k] * in.a[k];
+        }
+    }
+    __syncthreads();
+    if (tid < 64) {
+        float s = 0.0f;
+#pragma unroll
+        for (int m = 0; m < RT_HEAD_DIM / 4; m += 4) {
+            const float4 v = *reinterpret_cast<const float4*>(&L.gp[tid >> 2][tid & 3][m]);
+            s = s + v.x;
+            s = s + v.y;
+            s = s + v.z;
+            s = s + v.w;
+        }
+        const float r = lanes4_combine(s);
+        if ((tid & 3) == 0) L.gr[tid >> 2] = rms_scale(r, RT_HEAD_DIM, a.eps);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kE; ++k) {
+        const int e = tid + kThreads * k;
+        float y = 0.0f;
+        if (e < n) y = gated_mul(in.a[k], L.gr[e / RT_HEAD_DIM], in.c[k], in.b[k]);
+        const int b = e >> 6;
+        if (b < nb) bfp8_quant_block_wave(y, lane_id(), nullptr, &L.xsc[b], &L.xs[b * 32], L.rec[wave_id()]);
+    }
+}
+
 // swiglu(gate, up) into the LDS activation.
 template <int kE>
 __device__ __forceinline__ void swiglu_prologue(const RtRowsArgs& a, const PrologueIn<kE>& in, RowsLds& L) {
@@ -179,6 +230,8 @@ __global__ __launch_bounds__(kThreads) void rt_rows_gemv_kernel(RtRowsArgs a) {
         norm_prologue(a, in, L);
     } else if constexpr (kMode == RT_ROWS_SWIGLU) {
         swiglu_prologue(a, in, L);
+    } else if constexpr (kMode == RT_ROWS_GATED) {
+        gated_prologue(a, in, L);
     } else {
 #pragma unroll
         for (int k = 0; k < kPer; ++k) {
@@ -235,6 +288,7 @@ __global__ __launch_bounds__(kThreads) void rt_rows_gemv_kernel(RtRowsArgs a) {
 
 hipError_t rt_launch_rows(const RtRowsArgs& a, hipStream_t s) {
     if (a.K < 64 || a.K > RT_ROWS_MAX_K || (a.K & 63) || a.ngemv < 1 || a.ngemv > 2) return hipErrorInvalidValue;
+    if (a.mode == RT_ROWS_GATED && a.K != RT_HEADS * RT_HEAD_DIM) return hipErrorInvalidValue;
     const int n0 = (a.g[0].M + 15) / 16, n1 = a.ngemv > 1 ? (a.g[1].M + 15) / 16 : 0;
     if (a.ngemv > 1 && a.split != n0) return hipErrorInvalidValue;
     const dim3 grid((unsigned)(n0 + n1)), block(kThreads);
@@ -253,6 +307,7 @@ hipError_t rt_launch_rows(const RtRowsArgs& a, hipStream_t s) {
     else RT_ROWS_CASE(RT_ROWS_QUANTIZED, 2);
     else RT_ROWS_CASE(RT_ROWS_QUANTIZED, 3);
     else RT_ROWS_CASE(RT_ROWS_QUANTIZED, 4);
+    else RT_ROWS_CASE(RT_ROWS_GATED, 2);
     else return hipErrorInvalidValue;
 #undef RT_ROWS_CASE
     return hipGetLastError();

@@ -90,7 +90,8 @@ struct ParamKey {
 };
 
 struct DevState {
-    DevBuf conv, rec;     // [3][6144] taps, [16][128*128] blocked state
+    DevBuf conv[2], rec;  // [3][6144] taps (the current one conv[cur]), [16][128*128] blocked state
+    int cur = 0;
     float* host_conv;     // the caller's buffers
     float* host_rec;
     bool resident_used = false;  // advanced on the device while resident
@@ -113,10 +114,8 @@ struct FwdLayer {
 struct Workspace {
     DevBuf buf;
     float *h, *h2;  // the hidden state ping-pongs between these (see RtRowsArgs::h_out)
-    float *normed, *qkv, *z, *o, *gate, *up, *down;
-    float* xs_gated;     // the o GEMV's activation scales ...
-    uint32_t* xr_gated;  // ... and records (the other GEMVs quantize in their prologue)
-    int* lm;             // [ids 1, scores 1, count, argmax]
+    float *normed, *qkv, *z, *zsilu, *attn, *o, *gate, *up, *down;
+    int* lm;  // [ids 1, scores 1, count, argmax]
 };
 
 struct Forward {
@@ -180,11 +179,9 @@ int fwd_planes(const int8_t* mant, const uint8_t* exps, int M, int K, DevWeights
 int ensure_workspace() {
     if (F.ws_ready) return BFP8_OK;
     Workspace& w = F.ws;
-    const int nf[] = {kHidden, kHidden, kHidden, kConv, kHD, kHidden, kMlp, kMlp, kHidden};
-    const int nbk = kHD / 64;
-    size_t total = 0;
+    const int nf[] = {kHidden, kHidden, kHidden, kConv, kHD, kHD, kHD, kHidden, kMlp, kMlp, kHidden};
+    size_t total = 256;
     for (int n : nf) total += ((size_t)n * 4 + 255) & ~(size_t)255;
-    total += (((size_t)nbk * 4 + 255) & ~(size_t)255) + (size_t)nbk * 128 + 256;
     int rc;
     if ((rc = w.buf.reserve(total))) return rc;
     char* p = w.buf.as<char>();
@@ -193,10 +190,8 @@ int ensure_workspace() {
         p += (bytes + 255) & ~(size_t)255;
         return r;
     };
-    float** fl[] = {&w.h, &w.h2, &w.normed, &w.qkv, &w.z, &w.o, &w.gate, &w.up, &w.down};
-    for (int i = 0; i < 9; ++i) *fl[i] = reinterpret_cast<float*>(take((size_t)nf[i] * 4));
-    w.xs_gated = reinterpret_cast<float*>(take((size_t)nbk * 4));
-    w.xr_gated = reinterpret_cast<uint32_t*>(take((size_t)nbk * 128));
+    float** fl[] = {&w.h, &w.h2, &w.normed, &w.qkv, &w.z, &w.zsilu, &w.attn, &w.o, &w.gate, &w.up, &w.down};
+    for (int i = 0; i < 11; ++i) *fl[i] = reinterpret_cast<float*>(take((size_t)nf[i] * 4));
     w.lm = reinterpret_cast<int*>(take(16));
     F.ws_ready = true;
     return BFP8_OK;
@@ -224,12 +219,12 @@ int fwd_state(float* conv_s, float* state, DevState** out) {
     }
     std::unique_ptr<DevState> st(new DevState());
     int rc;
-    if ((rc = st->conv.reserve((size_t)3 * kConv * 4)) ||
+    if ((rc = st->conv[0].reserve((size_t)3 * kConv * 4)) || (rc = st->conv[1].reserve((size_t)3 * kConv * 4)) ||
         (rc = st->rec.reserve((size_t)RT_HEADS * RT_HEAD_DIM * RT_HEAD_DIM * 4)))
         return rc;
     st->host_conv = conv_s;
     st->host_rec = state;
-    HIP_OK(hipMemcpy(st->conv.p, conv_s, (size_t)3 * kConv * 4, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(st->conv[0].p, conv_s, (size_t)3 * kConv * 4, hipMemcpyHostToDevice));
     HIP_OK(hipMemcpy(st->rec.p, state, (size_t)RT_HEADS * RT_HEAD_DIM * RT_HEAD_DIM * 4, hipMemcpyHostToDevice));
     *out = st.get();
     F.states[key] = std::move(st);
@@ -237,14 +232,14 @@ int fwd_state(float* conv_s, float* state, DevState** out) {
 }
 
 int state_in(DevState* st) {
-    HIP_OK(hipMemcpyAsync(st->conv.p, st->host_conv, (size_t)3 * kConv * 4, hipMemcpyHostToDevice, g.stream));
+    HIP_OK(hipMemcpyAsync(st->conv[st->cur].p, st->host_conv, (size_t)3 * kConv * 4, hipMemcpyHostToDevice, g.stream));
     HIP_OK(hipMemcpyAsync(st->rec.p, st->host_rec, (size_t)RT_HEADS * RT_HEAD_DIM * RT_HEAD_DIM * 4,
                           hipMemcpyHostToDevice, g.stream));
     return BFP8_OK;
 }
 
 int state_out(DevState* st) {
-    HIP_OK(hipMemcpyAsync(st->host_conv, st->conv.p, (size_t)3 * kConv * 4, hipMemcpyDeviceToHost, g.stream));
+    HIP_OK(hipMemcpyAsync(st->host_conv, st->conv[st->cur].p, (size_t)3 * kConv * 4, hipMemcpyDeviceToHost, g.stream));
     HIP_OK(hipMemcpyAsync(st->host_rec, st->rec.p, (size_t)RT_HEADS * RT_HEAD_DIM * RT_HEAD_DIM * 4,
                           hipMemcpyDeviceToHost, g.stream));
     return BFP8_OK;
@@ -421,31 +416,36 @@ int linear_steps(const FwdLayer& L, float** h, const float* res) {
     if (res) *h = a.h_out;
     {
         Step s(QP_GDN);
+        DevState* st = L.st;
         RtLinearAttnArgs la{};
         la.qkv = w.qkv;
-        la.zbuf = w.z;
         la.normed = w.normed;
-        la.conv_s = L.st->conv.as<float>();
+        la.conv_in = st->conv[st->cur].as<float>();
+        la.conv_out = st->conv[st->cur ^ 1].as<float>();
         la.conv_w = L.conv_w;
         la.wa = L.wa;
         la.wb = L.wb;
         la.nea = L.nea;
         la.dt = L.dt;
-        la.state = L.st->rec.as<float>();
-        la.norm_w = L.norm_w;
-        la.xscale = w.xs_gated;
-        la.xsplit = w.xr_gated;
+        la.state = st->rec.as<float>();
+        la.attn = w.attn;
+        la.z = w.z;
+        la.zsilu = w.zsilu;
         RT_LAUNCH(rt_launch_linear_attn(la, g.stream));
+        st->cur ^= 1;
         if ((rc = s.done())) return rc;
     }
+    // the gated RMSNorm runs in the o GEMV's prologue
     RtRowsArgs o{};
     o.g[0] = rows_gemv(L.w[2], w.o, kHidden);
     o.ngemv = 1;
     o.split = kHidden / 16;
     o.K = kHD;
-    o.mode = RT_ROWS_QUANTIZED;
-    o.xsplit = w.xr_gated;
-    o.xscale = w.xs_gated;
+    o.mode = RT_ROWS_GATED;
+    o.attn = w.attn;
+    o.zsilu = w.zsilu;
+    o.w = L.norm_w;
+    o.eps = 1e-6f;
     if ((rc = rows_step(o))) return rc;
     return mlp_steps(L, &L.w[3], h, w.o);
 }
@@ -531,7 +531,8 @@ void drop_forward() {
     }
     F.planes.clear();
     for (auto& kv : F.states) {
-        kv.second->conv.release();
+        kv.second->conv[0].release();
+        kv.second->conv[1].release();
         kv.second->rec.release();
     }
     F.states.clear();
@@ -851,7 +852,7 @@ void qwen_forward_reset_state(void) {
     for (auto& kv : F.states) {
         DevState* st = kv.second.get();
         // hipMemsetAsync is fine here: this call is never captured in a graph
-        if (hipMemsetAsync(st->conv.p, 0, st->conv.n, g.stream) != hipSuccess ||
+        if (hipMemsetAsync(st->conv[st->cur].p, 0, st->conv[st->cur].n, g.stream) != hipSuccess ||
             hipMemsetAsync(st->rec.p, 0, st->rec.n, g.stream) != hipSuccess) {
             set_error("state reset failed");
             fatal("qwen_forward_reset_state");

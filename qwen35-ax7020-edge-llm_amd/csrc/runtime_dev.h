@@ -176,10 +176,15 @@ __device__ __forceinline__ float rms_scale(float ss, int n, float eps) {
     return ieee_div(1.0f, ieee_sqrt(ieee_add(ieee_div(ss, (float)n), eps)));
 }
 
-// gated RMSNorm element: ((x * r) * w) * (z / (1 + expf(-z))), scalar
-__device__ __forceinline__ float gated_elem(float x, float r, float w, float z) {
-    const float silu = ieee_div(z, ieee_add(1.0f, libm_expf(-z)));
+// silu(z) = z / (1 + expf(-z)), scalar
+__device__ __forceinline__ float silu_scalar(float z) { return ieee_div(z, ieee_add(1.0f, libm_expf(-z))); }
+
+// gated RMSNorm element: ((x * r) * w) * silu(z), scalar
+__device__ __forceinline__ float gated_mul(float x, float r, float w, float silu) {
     return ieee_mul(ieee_mul(ieee_mul(x, r), w), silu);
+}
+__device__ __forceinline__ float gated_elem(float x, float r, float w, float z) {
+    return gated_mul(x, r, w, silu_scalar(z));
 }
 
 // gdn gates of one head from the two dot products: beta = 1/(1 + expf(-bv)),

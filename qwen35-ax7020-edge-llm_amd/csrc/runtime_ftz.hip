@@ -197,65 +197,112 @@ extern "C" __global__ __launch_bounds__(256) void rt_embed_kernel(float* h, cons
     if (e < hidden) h[e] = __uint_as_float((uint32_t)table[(size_t)row * hidden + e] << 16);
 }
 
-// ---- the model's linear-attention block, one workgroup per head ---------------------------
-// Work that does not depend on each other overlaps.  Wavefronts 2-3 own the
-// state columns and issue their loads first (a wavefront's loads complete in
-// order, so nothing else is queued behind them); wavefronts 0-1 stage the
-// gates' products, then wavefront 0 runs the gates' two 256-step sums while
-// wavefront 1 runs the conv over the head's q, k, v channels; the short
-// 32-step sums (q/k norms, q.k, the gated norm) then share one staging
-// buffer between barriers.
+// ---- the model's linear-attention block ----------------------------------------------------
+// RT_ATTN_SPLIT workgroups per head; workgroup (h, part) owns state columns
+// [part*32, part*32 + 32).  Independent work overlaps: wavefront 3 owns the
+// columns (two lanes per column: one sums k.S, the other q.S) and issues its
+// state loads first; wavefront 0 forms the gates (two 256-step sums over the
+// input-norm output, then the scalar part); wavefronts 1-2 run the conv over
+// the head's q, k, v channels with every load issued before any use.  Every
+// workgroup of a head computes the same conv, norms and gates.
+template <int N>
+__device__ __forceinline__ float chain_add_n(float s, const float* p) {
+    // N % 4 == 0 and p 16-byte aligned; fully unrolled so the LDS reads run ahead of the adds
+#pragma unroll
+    for (int m = 0; m < N; m += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(p + m);
+        s = s + v.x;
+        s = s + v.y;
+        s = s + v.z;
+        s = s + v.w;
+    }
+    return s;
+}
+
 extern "C" __global__ __launch_bounds__(256) void rt_linear_attn_kernel(RtLinearAttnArgs a) {
     constexpr int D = RT_HEAD_DIM, NG = D / 4, C = RT_CONV_CH, HD = RT_HEADS * RT_HEAD_DIM, KG = RT_HIDDEN;
-    static_assert(D == 128 && KG / 4 <= kPitch, "staging sized for 16 heads of 128 and a 1024 gate input");
+    constexpr int COLS = D / RT_ATTN_SPLIT;
+    static_assert(D == 128 && COLS == 32 && KG / 4 <= kPitch, "sized for 16 heads of 128 and a 1024 gate input");
     __shared__ ResidueLds L;
-    __shared__ uint32_t rec[4][32];
     __shared__ __attribute__((aligned(16))) float qv[D];
     __shared__ __attribute__((aligned(16))) float kv[D];
     __shared__ float vv[D];
-    __shared__ float ov[D];
-    __shared__ float sc[6];
-    const int h = blockIdx.x, tid = threadIdx.x, w = wave_id(), lane = lane_id();
-    const bool col_thread = tid >= 128;  // wavefronts 2-3: column j = tid - 128
-    const int j = tid - 128;
+    __shared__ float sc[5];
+    const int h = blockIdx.x / RT_ATTN_SPLIT, part = blockIdx.x % RT_ATTN_SPLIT;
+    const int tid = threadIdx.x, w = wave_id(), lane = lane_id();
 
-    // the state column, in flight from the start
-    float* col = a.state + (size_t)h * D * D + ((size_t)(j >> 2) * NG * 4 + (j & 3)) * 4;
+    // wavefront 3: lane = (role, column): role 0 sums k[i] S[i][j], role 1 q[i] S[i][j]
+    const int cj = part * COLS + (lane & 31), role = lane >> 5;
+    float* col = a.state + (size_t)h * D * D + ((size_t)(cj >> 2) * NG * 4 + (cj & 3)) * 4;
     float4 st[NG];
-    if (col_thread) {
+    if (w == 3) {
 #pragma unroll
         for (int ig = 0; ig < NG; ++ig) st[ig] = *reinterpret_cast<const float4*>(col + ig * 16);
-    } else {
-        // gates' products wa[h] * x, wb[h] * x over the input-norm output
+    } else if (w == 0) {
+        // gates' products wa[h] * x, wb[h] * x (all loads first)
         const float* ra = a.wa + (size_t)h * KG;
         const float* rb = a.wb + (size_t)h * KG;
+        float xs[KG / 64], pa[KG / 64], pb[KG / 64];
 #pragma unroll
-        for (int k = 0; k < KG / 128; ++k) {
-            const int e = tid + 128 * k;
-            const float x = a.normed[e];
-            L.p[0][e & 3][e >> 2] = ra[e] * x;
-            L.p[1][e & 3][e >> 2] = rb[e] * x;
+        for (int k = 0; k < KG / 64; ++k) {
+            const int e = lane + 64 * k;
+            xs[k] = a.normed[e];
+            pa[k] = ra[e];
+            pb[k] = rb[e];
         }
-    }
-    __syncthreads();
-    if (w == 0) {
-        // av = wa[h] . x, bv = wb[h] . x in the 4-lane order, then the scalar part
+#pragma unroll
+        for (int k = 0; k < KG / 64; ++k) {
+            const int e = lane + 64 * k;
+            L.p[0][e & 3][e >> 2] = pa[k] * xs[k];
+            L.p[1][e & 3][e >> 2] = pb[k] * xs[k];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         float s = 0.0f;
-        if (lane < 8) s = chain_add(0.0f, &L.p[lane >> 2][lane & 3][0], KG / 4);
+        if (lane < 8) s = chain_add_n<KG / 4>(0.0f, &L.p[lane >> 2][lane & 3][0]);
         const float r = lanes4_combine(s);
         const float bv = __shfl(r, 4, 64);
         if (lane == 0) gates_scalar(r, bv, a.nea[h], a.dt[h], &sc[0], &sc[1]);
-    } else if (w == 1) {
-        // conv1d + SiLU over the head's q, k and v channels (all in the vector part)
+    } else {
+        // conv1d + SiLU over the head's q, k and v channels (all in the vector
+        // part): 128 lanes x 3 channels, loads first
+        const int t = tid - 64;
+        float xc[3], t0[3], t1[3], t2[3];
+        float4 wt[3];
+        int cc[3];
 #pragma unroll
-        for (int k = 0; k < 3 * D / 64; ++k) {
-            const int i = lane + 64 * k;
-            const int part = i / D, jj = i - part * D;
-            const int c = part * HD + h * D + jj;
-            const float y = conv_elem(a.qkv[c], a.conv_s + c, a.conv_s + C + c, a.conv_s + 2 * C + c,
-                                      a.conv_w + (size_t)c * 4, c < (C & ~3));
-            (part == 0 ? qv : part == 1 ? kv : vv)[jj] = y;
-            if (part == 2 && a.mixed) a.mixed[c] = y;
+        for (int k = 0; k < 3; ++k) {
+            const int i = t + 128 * k;  // channel i of the head's 384: part i / 128 of q, k, v
+            const int c = (i >> 7) * HD + h * D + (i & 127);
+            cc[k] = c;
+            xc[k] = a.qkv[c];
+            t0[k] = a.conv_in[c];
+            t1[k] = a.conv_in[C + c];
+            t2[k] = a.conv_in[2 * C + c];
+            wt[k] = *reinterpret_cast<const float4*>(a.conv_w + (size_t)c * 4);
+        }
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            float d = wt[k].x * t0[k];
+            d = d + wt[k].y * t1[k];
+            d = d + wt[k].z * t2[k];
+            d = d + wt[k].w * xc[k];
+            const float y = ieee_div(d, 1.0f + exp_neon(-d));
+            const int i = t + 128 * k, jj = i & 127;
+            (k == 0 ? qv : k == 1 ? kv : vv)[jj] = y;
+            if (part == 0) {  // one writer for the shifted taps
+                const int c = cc[k];
+                a.conv_out[c] = t1[k];
+                a.conv_out[C + c] = t2[k];
+                a.conv_out[2 * C + c] = xc[k];
+                if (k == 2 && a.mixed) a.mixed[c] = y;
+            }
+        }
+        // silu(z) of this workgroup's columns, for the gated norm in the o GEMV
+        if (t < COLS) {
+            const int e = h * D + part * COLS + t;
+            a.zsilu[e] = silu_scalar(a.z[e]);
         }
     }
     __syncthreads();
@@ -267,19 +314,15 @@ extern "C" __global__ __launch_bounds__(256) void rt_linear_attn_kernel(RtLinear
         L.p[1][e & 3][e >> 2] = qv[e] * qv[e];
     }
     __syncthreads();
-    if (w == 0) {
+    if (w == 1) {  // wavefront 0 may still be in the gates' scalar part
         float s = 0.0f;
-        if (lane < 8) s = chain_add(0.0f, &L.p[lane >> 2][lane & 3][0], NG);
+        if (lane < 8) s = chain_add_n<NG>(0.0f, &L.p[lane >> 2][lane & 3][0]);
         const float r = lanes4_combine(s);
         const float q_sq = __shfl(r, 4, 64);
         if (lane == 0) {
             const float q_scale = ieee_div(1.0f, ieee_sqrt((float)D));
             sc[2] = ieee_div(1.0f, ieee_sqrt(ieee_add(r, 1e-6f)));
             sc[3] = ieee_div(q_scale, ieee_sqrt(ieee_add(q_sq, 1e-6f)));
-            if (a.alpha_beta) {
-                a.alpha_beta[h] = sc[0];
-                a.alpha_beta[RT_HEADS + h] = sc[1];
-            }
         }
     }
     __syncthreads();
@@ -288,68 +331,57 @@ extern "C" __global__ __launch_bounds__(256) void rt_linear_attn_kernel(RtLinear
         kv[tid] = k;
         qv[tid] = q;
         L.p[0][tid & 3][tid >> 2] = q * k;  // the q.k sum's products
-        if (a.mixed) {
+        if (a.mixed && part == 0) {
             a.mixed[h * D + tid] = q;
             a.mixed[HD + h * D + tid] = k;
         }
     }
     __syncthreads();
-    if (w == 0) {
+    if (w == 1) {
         float s = 0.0f;
-        if (lane < 4) s = chain_add(0.0f, &L.p[0][lane][0], NG);
+        if (lane < 4) s = chain_add_n<NG>(0.0f, &L.p[0][lane][0]);
         const float r = lanes4_combine(s);
         if (lane == 0) sc[4] = r;
     }
     __syncthreads();
+    if (w == 0 && lane == 0 && a.alpha_beta && part == 0) {
+        a.alpha_beta[h] = sc[0];
+        a.alpha_beta[RT_HEADS + h] = sc[1];
+    }
 
-    // recurrent step on the column held in registers
-    if (col_thread) {
+    // recurrent step on the columns held in registers
+    if (w == 3) {
         const float alpha = sc[0], beta = sc[1], qk = sc[4];
-        float kvs = 0.0f, qss = 0.0f;
+        const float* vec = role ? qv : kv;
+        float4 vr[NG];
+#pragma unroll
+        for (int ig = 0; ig < NG; ++ig) vr[ig] = *reinterpret_cast<const float4*>(vec + 4 * ig);
+        float acc = 0.0f;  // kv (role 0) or qs (role 1), ascending i
 #pragma unroll
         for (int ig = 0; ig < NG; ++ig) {
-            const float4 k4 = *reinterpret_cast<const float4*>(kv + 4 * ig);
-            const float4 q4 = *reinterpret_cast<const float4*>(qv + 4 * ig);
-            kvs = kvs + st[ig].x * k4.x;
-            qss = qss + st[ig].x * q4.x;
-            kvs = kvs + st[ig].y * k4.y;
-            qss = qss + st[ig].y * q4.y;
-            kvs = kvs + st[ig].z * k4.z;
-            qss = qss + st[ig].z * q4.z;
-            kvs = kvs + st[ig].w * k4.w;
-            qss = qss + st[ig].w * q4.w;
+            acc = acc + st[ig].x * vr[ig].x;
+            acc = acc + st[ig].y * vr[ig].y;
+            acc = acc + st[ig].z * vr[ig].z;
+            acc = acc + st[ig].w * vr[ig].w;
         }
-        const float d = (vv[j] - kvs * alpha) * beta;
+        const int c = lane & 31;
+        const float kvs = __shfl(acc, c, 64), qss = __shfl(acc, 32 + c, 64);
+        const float d = (vv[cj] - kvs * alpha) * beta;
         const float o = qss * alpha + qk * d;
+        // S[i][j] = S[i][j] * a + d * k[i]: role 0 the first 16 row groups, role 1 the rest
 #pragma unroll
         for (int ig = 0; ig < NG; ++ig) {
-            const float4 k4 = *reinterpret_cast<const float4*>(kv + 4 * ig);
-            float4 nv;
-            nv.x = st[ig].x * alpha + d * k4.x;
-            nv.y = st[ig].y * alpha + d * k4.y;
-            nv.z = st[ig].z * alpha + d * k4.z;
-            nv.w = st[ig].w * alpha + d * k4.w;
-            *reinterpret_cast<float4*>(col + ig * 16) = nv;
+            if ((ig < NG / 2) == (role == 0)) {
+                const float4 k4 = *reinterpret_cast<const float4*>(kv + 4 * ig);
+                float4 nv;
+                nv.x = st[ig].x * alpha + d * k4.x;
+                nv.y = st[ig].y * alpha + d * k4.y;
+                nv.z = st[ig].z * alpha + d * k4.z;
+                nv.w = st[ig].w * alpha + d * k4.w;
+                *reinterpret_cast<float4*>(col + ig * 16) = nv;
+            }
         }
-        ov[j] = o;
-        L.p[1][j & 3][j >> 2] = o * o;  // the gated norm's products
-        if (a.attn) a.attn[h * D + j] = o;
-    }
-    __syncthreads();
-
-    // gated RMSNorm + quantizer of the o GEMV's input (two blocks per head)
-    if (w == 0) {
-        float s = 0.0f;
-        if (lane < 4) s = chain_add(0.0f, &L.p[1][lane][0], NG);
-        const float r = lanes4_combine(s);
-        if (lane == 0) sc[5] = rms_scale(r, D, 1e-6f);
-    }
-    __syncthreads();
-    if (col_thread) {
-        const float y = gated_elem(ov[j], sc[5], a.norm_w[j], a.zbuf[h * D + j]);
-        if (a.gated) a.gated[h * D + j] = y;
-        const int b = h * (D / 64) + (w - 2);
-        bfp8_quant_block_wave(y, lane, nullptr, a.xscale + b, a.xsplit + (size_t)b * 32, rec[w]);
+        if (role == 0) a.attn[h * D + cj] = o;
     }
 }
 
@@ -412,7 +444,8 @@ hipError_t rt_launch_add_residual(float* x, const float* res, int n, hipStream_t
 }
 
 hipError_t rt_launch_linear_attn(const RtLinearAttnArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL(rt_linear_attn_kernel, dim3(RT_HEADS), dim3(256), 0, s, a);
+    if (a.conv_in == a.conv_out) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rt_linear_attn_kernel, dim3(RT_HEADS * RT_ATTN_SPLIT), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

@@ -77,32 +77,35 @@ struct RtGatedArgs {
 };
 
 // The model's linear-attention block between the qkv/z GEMVs and the o GEMV
-// (04/qwen_kernels_opt.c:943-987, steps 3-8) for 16 heads of 128: conv1d +
-// SiLU over the head's q/k/v channels, q/k L2 norm, gates, recurrent step,
-// gated RMSNorm and the quantizer of the o GEMV's input; one workgroup per
-// head.
+// (04/qwen_kernels_opt.c:943-967, steps 3-6) for 16 heads of 128: conv1d +
+// SiLU over the head's q/k/v channels, q/k L2 norm, gates and the recurrent
+// step; RT_ATTN_SPLIT workgroups per head, each owning 128 / RT_ATTN_SPLIT
+// state columns (and computing the head's conv, norms and gates itself).
+// The conv taps are read from conv_in and the shifted taps written to
+// conv_out (a different buffer: every workgroup of a head reads the taps).
+// The gated RMSNorm that follows is the o GEMV's prologue (RT_ROWS_GATED);
+// each workgroup writes silu(z) of its columns for it.
 #define RT_HEADS 16
 #define RT_HEAD_DIM 128
 #define RT_CONV_CH 6144
 #define RT_HIDDEN 1024
+#define RT_ATTN_SPLIT 4
 struct RtLinearAttnArgs {
-    const float* qkv;     // [6144] qkv GEMV output
-    const float* zbuf;    // [2048] z GEMV output
-    const float* normed;  // [1024] input-norm output (gate input)
-    float* conv_s;        // [3][6144]
-    const float* conv_w;  // [6144][4]
-    const float* wa;      // [16][1024]
-    const float* wb;      // [16][1024]
-    const float* nea;     // [16]
-    const float* dt;      // [16]
-    float* state;         // [16][128*128], blocked
-    const float* norm_w;  // [128]
-    float* xscale;        // [32] o-GEMV activation scales
-    uint32_t* xsplit;     // [32][32] o-GEMV activation records
-    float* mixed;         // optional [6144]: q, k after L2 norm, v
-    float* attn;          // optional [2048]: recurrent-step output
-    float* gated;         // optional [2048]: gated RMSNorm output
-    float* alpha_beta;    // optional [32]: alpha[16], beta[16]
+    const float* qkv;      // [6144] qkv GEMV output
+    const float* normed;   // [1024] input-norm output (gate input)
+    const float* conv_in;  // [3][6144] taps, oldest first
+    float* conv_out;       // [3][6144] shifted taps
+    const float* conv_w;   // [6144][4]
+    const float* wa;       // [16][1024]
+    const float* wb;       // [16][1024]
+    const float* nea;      // [16]
+    const float* dt;       // [16]
+    float* state;          // [16][128*128], blocked
+    float* attn;           // [2048] recurrent-step output
+    const float* z;        // [2048] z GEMV output ...
+    float* zsilu;          // ... and silu(z), for the gated norm
+    float* mixed;          // optional [6144]: q, k after L2 norm, v
+    float* alpha_beta;     // optional [32]: alpha[16], beta[16]
 };
 
 // The forward's GEMVs (fused_gemv.hip): one or two GEMVs sharing one
@@ -111,6 +114,7 @@ struct RtLinearAttnArgs {
 #define RT_ROWS_QUANTIZED 0  // xsplit / xscale given
 #define RT_ROWS_NORM 1       // rmsnorm(h + res) with weight w, eps
 #define RT_ROWS_SWIGLU 2     // swiglu(gate, up)
+#define RT_ROWS_GATED 3      // rmsnorm_gated(attn, z) over 16 heads of 128 with weight w, eps (silu(z) given)
 #define RT_ROWS_MAX_K 4096
 struct RtRowsGemv {
     const uint8_t* mant;  // GPU planes (bfp8_layout.h)
@@ -135,6 +139,8 @@ struct RtRowsArgs {
     float* y_norm;           // optional: workgroup 0 writes the normalised vector
     const float* gate;       // RT_ROWS_SWIGLU
     const float* up;
+    const float* attn;       // RT_ROWS_GATED (with w, eps)
+    const float* zsilu;      // silu(z), elementwise
 };
 hipError_t rt_launch_rows(const RtRowsArgs& a, hipStream_t s);
 
