@@ -28,6 +28,7 @@
 
 #include "bfp8_internal.h"
 #include "gemv_dev.h"
+#include "runtime_internal.h"
 #include "wave_topk.h"
 
 namespace {
@@ -642,6 +643,22 @@ static size_t wide_lds_bytes(int max_nb) {
 hipError_t bfp8_launch_gemv(const Bfp8GemvDesc& d, hipStream_t s) {
     const int nt = bfp8_ntiles(d.M);
     if (nt == 0) return hipSuccess;
+    if (d.topk <= 0 && nt <= BFP8_WIDE_MAX_TILES && !d.lanes && d.K <= RT_ROWS_MAX_K) {
+        // few row tiles: 16 rows per workgroup (fused_gemv.hip)
+        RtRowsArgs a{};
+        a.g[0].mant = d.mant;
+        a.g[0].exps = d.exps;
+        a.g[0].y = d.y;
+        a.g[0].M = d.M;
+        a.g[0].pair_rows = d.pair_rows;
+        a.ngemv = 1;
+        a.split = (d.M + 15) / 16;
+        a.K = d.K;
+        a.mode = RT_ROWS_QUANTIZED;
+        a.xsplit = d.xsplit;
+        a.xscale = d.xscale;
+        return rt_launch_rows(a, s);
+    }
     if (d.topk <= 0 && nt <= BFP8_WIDE_MAX_TILES) {
         const size_t lds = wide_lds_bytes(d.K >> 6);
         if (d.lanes)

@@ -88,8 +88,9 @@ struct Bfp8TileRef {
 #endif
 
 // ---- bfp8_ftz.hip --------------------------------------------------------
-// Single GEMV: up to BFP8_WIDE_MAX_TILES row tiles one tile per 16-wavefront
-// workgroup, else the persistent streaming kernel (for topk > 0 always, then
+// Single GEMV: up to BFP8_WIDE_MAX_TILES row tiles 16 rows per workgroup
+// (fused_gemv.hip; one tile per 16-wavefront workgroup when per-lane sums are
+// asked for), else the persistent streaming kernel (for topk > 0 always, then
 // followed by the stand-alone merge kernel).
 hipError_t bfp8_launch_gemv(const Bfp8GemvDesc& d, hipStream_t s);
 // One tile per 16-wavefront workgroup over a tile table (small plans);

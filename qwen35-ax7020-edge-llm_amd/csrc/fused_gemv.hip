@@ -287,7 +287,11 @@ __global__ __launch_bounds__(kThreads) void rt_rows_gemv_kernel(RtRowsArgs a) {
 }
 
 hipError_t rt_launch_rows(const RtRowsArgs& a, hipStream_t s) {
-    if (a.K < 64 || a.K > RT_ROWS_MAX_K || (a.K & 63) || a.ngemv < 1 || a.ngemv > 2) return hipErrorInvalidValue;
+    // a given activation uses the K / 64 whole blocks (as the reference does);
+    // one computed here covers exactly K elements
+    if (a.K < 64 || a.K > RT_ROWS_MAX_K || ((a.K & 63) && a.mode != RT_ROWS_QUANTIZED) || a.ngemv < 1 ||
+        a.ngemv > 2)
+        return hipErrorInvalidValue;
     if (a.mode == RT_ROWS_GATED && a.K != RT_HEADS * RT_HEAD_DIM) return hipErrorInvalidValue;
     const int n0 = (a.g[0].M + 15) / 16, n1 = a.ngemv > 1 ? (a.g[1].M + 15) / 16 : 0;
     if (a.ngemv > 1 && a.split != n0) return hipErrorInvalidValue;

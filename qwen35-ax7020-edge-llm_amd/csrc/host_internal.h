@@ -154,6 +154,7 @@ struct Launch {
     int nwg = 0;
     bool wide = false;
     int ntiles = 0, max_nb = 0;
+    int rows[2] = {-1, -1};  // >= 0: one or two GEMVs sharing an activation, 16 rows per workgroup
 };
 
 // Drops the forward's device copies (qwen_runtime_api.cpp); g.mu held.

@@ -20,6 +20,7 @@
 #include <vector>
 
 #include "host_internal.h"
+#include "runtime_internal.h"
 
 namespace qhost {
 
@@ -910,7 +911,14 @@ void* bfp8_plan_create(const bfp8_plan_item* items, int n) {
     std::stable_sort(rest_idx.begin(), rest_idx.end(), [&](int a, int b) { return items[a].K > items[b].K; });
     const bool fold = p->topk_desc >= 0 && !rest_idx.empty();
     rc = rc ? rc : deal_tiles(p->head, head_idx, items, 0, false);
-    rc = rc ? rc : deal_tiles(p->rest, rest_idx, items, fold ? BFP8_MERGE_COST_BLOCKS : 0, !fold);
+    // one GEMV, or two reading the same activation: 16 rows per workgroup
+    const bool rows = !fold && !rest_idx.empty() && rest_idx.size() <= 2 &&
+                      (rest_idx.size() == 1 || (items[rest_idx[0]].x == items[rest_idx[1]].x &&
+                                                items[rest_idx[0]].K == items[rest_idx[1]].K));
+    if (rows)
+        for (size_t i = 0; i < rest_idx.size(); ++i) p->rest.rows[i] = rest_idx[i];
+    else
+        rc = rc ? rc : deal_tiles(p->rest, rest_idx, items, fold ? BFP8_MERGE_COST_BLOCKS : 0, !fold);
     p->nq = (int)hq.size();
     rc = rc ? rc : p->descs.reserve(p->hdesc.size() * sizeof(Bfp8GemvDesc));
     rc = rc ? rc : p->qdescs.reserve(hq.size() * sizeof(Bfp8QuantDesc));
@@ -943,7 +951,25 @@ int bfp8_plan_launch(void* plan, int stage, void* stream) {
         HIP_OK(bfp8_launch_gemv_grouped(descs, p->head.tiles.as<Bfp8TileRef>(), p->head.wg_off.as<int>(),
                                         p->head.nwg, -1, s));
     } else if (stage == 1) {
-        if (p->rest.wide)
+        if (p->rest.rows[0] >= 0) {
+            RtRowsArgs a{};
+            for (int i = 0; i < 2 && p->rest.rows[i] >= 0; ++i) {
+                const Bfp8GemvDesc& d = p->hdesc[p->rest.rows[i]];
+                a.g[i].mant = d.mant;
+                a.g[i].exps = d.exps;
+                a.g[i].y = d.y;
+                a.g[i].M = d.M;
+                a.g[i].pair_rows = d.pair_rows;
+                a.ngemv = i + 1;
+            }
+            const Bfp8GemvDesc& d0 = p->hdesc[p->rest.rows[0]];
+            a.split = (d0.M + 15) / 16;
+            a.K = d0.K;
+            a.mode = RT_ROWS_QUANTIZED;
+            a.xsplit = d0.xsplit;
+            a.xscale = d0.xscale;
+            HIP_OK(rt_launch_rows(a, s));
+        } else if (p->rest.wide)
             HIP_OK(bfp8_launch_gemv_wide_grouped(descs, p->rest.tiles.as<Bfp8TileRef>(), p->rest.ntiles,
                                                  p->rest.max_nb, s));
         else
@@ -969,6 +995,7 @@ const char* bfp8_plan_kernel_name(void* plan, int stage) {
     const bool fold = p->topk_desc >= 0 && p->rest.nwg > 0;
     if (stage == 0) return p->head.nwg > 0 ? "bfp8_gemv_grouped_kernel" : "";
     if (stage == 1) {
+        if (p->rest.rows[0] >= 0) return "rt_rows_gemv_kernel";
         if (p->rest.wide) return "bfp8_gemv_wide_grouped_kernel";
         if (fold) return "bfp8_gemv_grouped_merge_kernel";
         if (p->rest.nwg > 0) return "bfp8_gemv_grouped_kernel";
