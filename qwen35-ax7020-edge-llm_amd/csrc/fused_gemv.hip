@@ -40,10 +40,9 @@ struct RowsLds {
     __attribute__((aligned(16))) uint32_t xs[kMaxNb * 32];  // split activation records
     float xsc[kMaxNb];                                       // block scales
     float terms[kMaxNb][64];                                 // t2 per block and lane
-    ResidueLds res;             // rmsnorm's sum of squares
+    __attribute__((aligned(16))) float sq[4][kChunk / 4 + 4];  // rmsnorm's squares, one row per residue
     float gp[RT_HEADS][4][36];  // the gated norm's per-head products (16-byte rows)
     float gr[RT_HEADS];         // ... and per-head scales
-    uint32_t rec[kWaves][32];   // quantizer scratch, one per wavefront
     float scale;
 };
 
@@ -102,25 +101,31 @@ __device__ __forceinline__ void load_prologue(const RtRowsArgs& a, PrologueIn<kE
 // rmsnorm of x = h (+ res) into the LDS activation (n = K, a multiple of 64).
 template <int kE>
 __device__ __forceinline__ void norm_prologue(const RtRowsArgs& a, const PrologueIn<kE>& in, RowsLds& L) {
-    const int tid = threadIdx.x, n = a.K, nb = n >> 6;
+    const int tid = threadIdx.x, n = a.K, nb = n >> 6, lane = lane_id();
+    const bool w0 = tid < 64;
     float x[kE];
 #pragma unroll
     for (int k = 0; k < kE; ++k) x[k] = a.res ? in.a[k] + in.b[k] : in.a[k];  // add_residual's vector add
-    // sum of squares in the 4-lane order: element e = 4m + j feeds lane j
+    // sum of squares in the 4-lane order (element e = 4m + j feeds lane j, m
+    // ascending), kChunk elements per pass; lanes 0-3 of wavefront 0 keep the
+    // four sums
     float s = 0.0f;
     for (int base = 0; base < n; base += kChunk) {
 #pragma unroll
         for (int k = 0; k < kE; ++k) {
             const int e = tid + kThreads * k;
-            if (e >= base && e < base + kChunk && e < n) L.res.p[0][e & 3][(e - base) >> 2] = x[k] * x[k];
+            if (e >= base && e < base + kChunk && e < n) L.sq[e & 3][(e - base) >> 2] = x[k] * x[k];
         }
         __syncthreads();
-        if (tid < 4) s = chain_add(s, &L.res.p[0][tid][0], min(kChunk, n - base) >> 2);
-        __syncthreads();
+        if (tid < 4) {
+            const int cnt = min(kChunk, n - base) >> 2;
+            s = (cnt == kChunk / 4) ? chain_add256(s, &L.sq[tid][0]) : chain_add(s, &L.sq[tid][0], cnt);
+        }
+        if (base + kChunk < n) __syncthreads();
     }
-    if (tid < 64) {
-        const float r = lanes4_combine(s);
-        if (tid == 0) L.scale = rms_scale(r, n, a.eps);
+    if (w0) {
+        const float r = (readlane_f(s, 0) + readlane_f(s, 2)) + (readlane_f(s, 1) + readlane_f(s, 3));
+        if (lane == 0) L.scale = rms_scale(r, n, a.eps);
     }
     __syncthreads();
     const float r = L.scale;
@@ -137,7 +142,7 @@ __device__ __forceinline__ void norm_prologue(const RtRowsArgs& a, const Prologu
             }
         }
         const int b = e >> 6;  // one block per wavefront
-        if (b < nb) bfp8_quant_block_wave(y, lane_id(), nullptr, &L.xsc[b], &L.xs[b * 32], L.rec[wave_id()]);
+        if (b < nb) bfp8_quant_block_lds(y, lane, &L.xsc[b], &L.xs[b * 32]);
     }
 }
 
@@ -178,7 +183,7 @@ __device__ __forceinline__ void gated_prologue(const RtRowsArgs& a, const Prolog
         float y = 0.0f;
         if (e < n) y = gated_mul(in.a[k], L.gr[e / RT_HEAD_DIM], in.c[k], in.b[k]);
         const int b = e >> 6;
-        if (b < nb) bfp8_quant_block_wave(y, lane_id(), nullptr, &L.xsc[b], &L.xs[b * 32], L.rec[wave_id()]);
+        if (b < nb) bfp8_quant_block_lds(y, lane_id(), &L.xsc[b], &L.xs[b * 32]);
     }
 }
 
@@ -192,7 +197,7 @@ __device__ __forceinline__ void swiglu_prologue(const RtRowsArgs& a, const Prolo
         float y = 0.0f;
         if (e < n) y = swiglu_elem(in.a[k], in.b[k], true);  // n % 4 == 0: all vector part
         const int b = e >> 6;
-        if (b < nb) bfp8_quant_block_wave(y, lane_id(), nullptr, &L.xsc[b], &L.xs[b * 32], L.rec[wave_id()]);
+        if (b < nb) bfp8_quant_block_lds(y, lane_id(), &L.xsc[b], &L.xs[b * 32]);
     }
 }
 

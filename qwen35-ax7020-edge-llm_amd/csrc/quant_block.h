@@ -13,33 +13,74 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-// lane = this thread's element (0..63) of the block, xv its value; rec = 32
-// dwords of LDS owned by the calling wavefront.  Every lane of the wavefront
-// calls this.
-__device__ __forceinline__ void bfp8_quant_block_wave(float xv, int lane, int16_t* xq_b, float* xscale_b,
-                                                      uint32_t* xsplit_b, uint32_t* rec) {
+// Maximum over the wavefront of a float that is neither negative nor NaN, in
+// every lane (such floats order as their bit patterns): DPP exchanges within
+// each row of 16 lanes (quad_perm [1,0,3,2], quad_perm [2,3,0,1],
+// row_half_mirror, row_mirror), then the four row maxima.  Every lane of the
+// wavefront must be active.
+__device__ __forceinline__ float wave_max_nonneg(float v) {
+    int x = __float_as_int(v);
+    x = max(x, __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false));
+    x = max(x, __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false));
+    x = max(x, __builtin_amdgcn_mov_dpp(x, 0x141, 0xF, 0xF, false));
+    x = max(x, __builtin_amdgcn_mov_dpp(x, 0x140, 0xF, 0xF, false));
+    const int r0 = __builtin_amdgcn_readlane(x, 0), r1 = __builtin_amdgcn_readlane(x, 16);
+    const int r2 = __builtin_amdgcn_readlane(x, 32), r3 = __builtin_amdgcn_readlane(x, 48);
+    return __int_as_float(max(max(r0, r1), max(r2, r3)));
+}
+
+// The block's scale and this lane's int16 value.
+struct Bfp8QuantLane {
+    float xs;
+    int xq;
+};
+__device__ __forceinline__ Bfp8QuantLane bfp8_quant_lane(float xv) {
     const float v = fabsf(xv);
-    float amax = (v > 0.0f) ? v : 0.0f;
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-        const float o = __shfl_xor(amax, m, 64);
-        amax = (o > amax) ? o : amax;
-    }
-    int xq = 0;
-    float xs = 0.0f;
+    const float amax = wave_max_nonneg((v > 0.0f) ? v : 0.0f);  // a NaN never wins `v > amax`
+    Bfp8QuantLane r{0.0f, 0};
     if (amax > 1e-20f) {
         const float q = __fdiv_rn(16384.0f, amax);
-        xs = __fdiv_rn(amax, 16384.0f);
+        r.xs = amax * 0x1p-14f;  // = amax / 16384 exactly: the quotient of amax > 1e-20 by 2^14 is normal
         const float p = __fmul_rn(xv, q);
         // lrintf rounds half to even; a NaN product (x NaN, or inf*0) gives 0.
-        xq = (p == p) ? (int)__builtin_rintf(p) : 0;
+        r.xq = (p == p) ? (int)__builtin_rintf(p) : 0;
     }
-    if (xq_b) xq_b[lane] = (int16_t)xq;
-    if (lane == 0) *xscale_b = xs;
-    const int xl = (int)(int8_t)(xq & 0xff);
-    const int xh = (xq - xl) >> 8;
+    return r;
+}
+
+// Byte offset of lane's high byte in the block's 128-byte split record (its
+// low byte is 16 further on).
+__device__ __forceinline__ int bfp8_split_pos(int lane) {
     const int res = lane & 3, ii = lane >> 2;
-    const int pos = res * 32 + (ii >> 2) * 4 + (ii & 3);
+    return res * 32 + (ii >> 2) * 4 + (ii & 3);
+}
+
+// Quantizes into LDS: the record's bytes and the scale are stored straight
+// into xsplit_b / xscale_b (__shared__), and the caller's next barrier
+// publishes them.  Every lane of the wavefront calls this.
+__device__ __forceinline__ void bfp8_quant_block_lds(float xv, int lane, float* xscale_b, uint32_t* xsplit_b) {
+    const Bfp8QuantLane r = bfp8_quant_lane(xv);
+    if (lane == 0) *xscale_b = r.xs;
+    const int xl = (int)(int8_t)(r.xq & 0xff);
+    const int xh = (r.xq - xl) >> 8;
+    uint8_t* rb = reinterpret_cast<uint8_t*>(xsplit_b);
+    const int pos = bfp8_split_pos(lane);
+    rb[pos] = (uint8_t)xh;
+    rb[pos + 16] = (uint8_t)xl;
+}
+
+// lane = this thread's element (0..63) of the block, xv its value; rec = 32
+// dwords of LDS owned by the calling wavefront (the record is assembled there
+// and stored to xsplit_b, which may be global memory, as 32 dwords).  Every
+// lane of the wavefront calls this.
+__device__ __forceinline__ void bfp8_quant_block_wave(float xv, int lane, int16_t* xq_b, float* xscale_b,
+                                                      uint32_t* xsplit_b, uint32_t* rec) {
+    const Bfp8QuantLane r = bfp8_quant_lane(xv);
+    if (xq_b) xq_b[lane] = (int16_t)r.xq;
+    if (lane == 0) *xscale_b = r.xs;
+    const int xl = (int)(int8_t)(r.xq & 0xff);
+    const int xh = (r.xq - xl) >> 8;
+    const int pos = bfp8_split_pos(lane);
     uint8_t* rb = reinterpret_cast<uint8_t*>(rec);
     rb[pos] = (uint8_t)xh;
     rb[pos + 16] = (uint8_t)xl;

@@ -106,6 +106,29 @@ __device__ __forceinline__ float chain_add(float s, const float* p, int cnt) {
     return s;
 }
 
+// s + p[0] + ... + p[255] (LDS, 16-byte aligned), one rounding per add, in
+// this order.  A wavefront issues LDS reads and adds in order and a 16-byte
+// read holds its issue for about as long as four adds, so the reads are
+// spread evenly: one after every four adds, kAhead reads ahead of their use
+// (an empty asm statement that takes s and clobbers memory pins each step).
+__device__ __forceinline__ float chain_add256(float s, const float* p) {
+    constexpr int kAhead = 8;
+    const float4* p4 = reinterpret_cast<const float4*>(p);
+    float4 buf[64];
+#pragma unroll
+    for (int i = 0; i < kAhead; ++i) buf[i] = p4[i];
+#pragma unroll
+    for (int i = 0; i < 64; ++i) {
+        if (i + kAhead < 64) buf[i + kAhead] = p4[i + kAhead];
+        s = s + buf[i].x;
+        s = s + buf[i].y;
+        s = s + buf[i].z;
+        s = s + buf[i].w;
+        asm volatile("" : "+v"(s)::"memory");
+    }
+    return s;
+}
+
 // Sums over the vector part [0, 4*(n/4)) of one or two product sequences,
 // prod0(e) and prod1(e), in the 4-lane order; every thread of the block calls
 // it (same n) and gets (sum0, sum1).  Staging hands element e to thread
@@ -124,7 +147,7 @@ __device__ float2 residue_sums(int n, bool two, F0 prod0, F1 prod1, ResidueLds& 
             if (two) L.p[1][e & 3][e >> 2] = prod1(base + e);
         }
         __syncthreads();
-        if (chains) s = chain_add(s, &L.p[seq][j][0], cnt >> 2);
+        if (chains) s = (cnt == kChunk) ? chain_add256(s, &L.p[seq][j][0]) : chain_add(s, &L.p[seq][j][0], cnt >> 2);
         __syncthreads();
     }
     if (tid < 64) {
@@ -172,8 +195,18 @@ __device__ __forceinline__ float conv_elem(float xc, float* s0, float* s1, float
 }
 
 // 1 / sqrtf(ss / n + eps), scalar
+// Each step is one IEEE operation.  The float instructions answer when every
+// operand and intermediate is normal (one combined test, no branch per step;
+// the square root of a normal positive float is normal), else the exact
+// helpers do; a power-of-two n divides exactly as a product with 1/n.
 __device__ __forceinline__ float rms_scale(float ss, int n, float eps) {
-    return ieee_div(1.0f, ieee_sqrt(ieee_add(ieee_div(ss, (float)n), eps)));
+    const float fn = (float)n;
+    const float m = ((n & (n - 1)) == 0) ? ss * (1.0f / fn) : __fdiv_rn(ss, fn);
+    const float t = m + eps;
+    const float q = (float)__builtin_sqrt((double)t);
+    const float r = __fdiv_rn(1.0f, q);
+    if (normal_f(ss) & normal_f(fn) & normal_f(m) & normal_f(eps) & normal_f(t) & normal_f(r)) return r;
+    return ieee_div(1.0f, ieee_sqrt(ieee_add(ieee_div(ss, fn), eps)));
 }
 
 // silu(z) = z / (1 + expf(-z)), scalar
@@ -181,6 +214,8 @@ __device__ __forceinline__ float silu_scalar(float z) { return ieee_div(z, ieee_
 
 // gated RMSNorm element: ((x * r) * w) * silu(z), scalar
 __device__ __forceinline__ float gated_mul(float x, float r, float w, float silu) {
+    const float a = x * r, b = a * w, c = b * silu;  // one combined normality test, as in rms_scale
+    if (normal_f(x) & normal_f(r) & normal_f(a) & normal_f(w) & normal_f(b) & normal_f(silu) & normal_f(c)) return c;
     return ieee_mul(ieee_mul(ieee_mul(x, r), w), silu);
 }
 __device__ __forceinline__ float gated_elem(float x, float r, float w, float z) {
@@ -272,10 +307,50 @@ __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
 // lane's group (vadd of the halves, then vpadd); every lane of the
 // wavefront calls it.
 __device__ __forceinline__ float lanes4_combine(float s) {
-    const int g = lane_id() & ~3;
-    const float l0 = __shfl(s, g + 0, 64), l1 = __shfl(s, g + 1, 64);
-    const float l2 = __shfl(s, g + 2, 64), l3 = __shfl(s, g + 3, 64);
+    // quad_perm [j,j,j,j] hands lane j of the quad to all four (every lane active)
+    const int x = __float_as_int(s);
+    const float l0 = __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x00, 0xF, 0xF, false));
+    const float l1 = __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x55, 0xF, 0xF, false));
+    const float l2 = __int_as_float(__builtin_amdgcn_mov_dpp(x, 0xAA, 0xF, 0xF, false));
+    const float l3 = __int_as_float(__builtin_amdgcn_mov_dpp(x, 0xFF, 0xF, 0xF, false));
     return (l0 + l2) + (l1 + l3);
+}
+
+// A long 4-lane chain with its operands in registers: row j of a wavefront
+// (lanes 16j .. 16j+15) holds residue j's products, product m = 16r + i in
+// v[r] of lane 16j + i, and lane 16j adds products 0 .. 16*nr - 1 to s in
+// ascending m, one rounding per add.  Lane 16j reads lane 16j + i through a
+// DPP row shift (row_shl:i), so no add waits on memory.  nr (<= 16) is
+// uniform; the other lanes' results are meaningless.
+#define RT_ROW_ADD(k) s = s + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x100 + (k), 0xF, 0xF, true))
+__device__ __forceinline__ float row_chain(float s, const float (&v)[16], int nr) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        if (r < nr) {
+            const float x = v[r];
+            s = s + x;
+            RT_ROW_ADD(1);
+            RT_ROW_ADD(2);
+            RT_ROW_ADD(3);
+            RT_ROW_ADD(4);
+            RT_ROW_ADD(5);
+            RT_ROW_ADD(6);
+            RT_ROW_ADD(7);
+            RT_ROW_ADD(8);
+            RT_ROW_ADD(9);
+            RT_ROW_ADD(10);
+            RT_ROW_ADD(11);
+            RT_ROW_ADD(12);
+            RT_ROW_ADD(13);
+            RT_ROW_ADD(14);
+            RT_ROW_ADD(15);
+        }
+    }
+    return s;
+}
+#undef RT_ROW_ADD
+__device__ __forceinline__ float readlane_f(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
 
 }  // namespace
