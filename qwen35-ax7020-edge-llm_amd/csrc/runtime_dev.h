@@ -209,8 +209,25 @@ __device__ __forceinline__ float rms_scale(float ss, int n, float eps) {
     return ieee_div(1.0f, ieee_sqrt(ieee_add(ieee_div(ss, fn), eps)));
 }
 
-// silu(z) = z / (1 + expf(-z)), scalar
-__device__ __forceinline__ float silu_scalar(float z) { return ieee_div(z, ieee_add(1.0f, libm_expf(-z))); }
+// num / sqrtf(x + eps), scalar, with one combined normality test as in rms_scale
+__device__ __forceinline__ float div_sqrt_add(float num, float x, float eps) {
+    const float t = x + eps;
+    const float q = (float)__builtin_sqrt((double)t);
+    const float r = __fdiv_rn(num, q);
+    if (normal_f(num) & normal_f(x) & normal_f(eps) & normal_f(t) & normal_f(r)) return r;
+    return ieee_div(num, ieee_sqrt(ieee_add(x, eps)));
+}
+
+// silu(z) = z / (1 + expf(-z)), scalar.  For a normal argument whose result
+// is normal, expf is the double exp rounded once (libm_expf without its
+// subnormal handling); one combined test as in rms_scale.
+__device__ __forceinline__ float silu_scalar(float z) {
+    const float e = (float)exp(-(double)z);
+    const float d = 1.0f + e;
+    const float r = __fdiv_rn(z, d);
+    if (normal_f(z) & normal_f(e) & normal_f(d) & normal_f(r)) return r;
+    return ieee_div(z, ieee_add(1.0f, libm_expf(-z)));
+}
 
 // gated RMSNorm element: ((x * r) * w) * silu(z), scalar
 __device__ __forceinline__ float gated_mul(float x, float r, float w, float silu) {
@@ -224,10 +241,26 @@ __device__ __forceinline__ float gated_elem(float x, float r, float w, float z) 
 
 // gdn gates of one head from the two dot products: beta = 1/(1 + expf(-bv)),
 // alpha = expf(nea * log1pf(expf(av + dt))).
+// Every step is one IEEE operation or one libm call (the double function
+// rounded once); one combined normality test as in silu_scalar.
 __device__ __forceinline__ void gates_scalar(float av, float bv, float nea, float dt, float* alpha, float* beta) {
+    const float e1 = (float)exp(-(double)bv);
+    const float d1 = 1.0f + e1;
+    const float b = __fdiv_rn(1.0f, d1);
+    const float z = av + dt;
+    const float e2 = (float)exp((double)z);
+    const float l = (float)log1p((double)e2);
+    const float m = nea * l;
+    const float al = (float)exp((double)m);
+    if (normal_f(bv) & normal_f(e1) & normal_f(d1) & normal_f(b) & normal_f(av) & normal_f(dt) & normal_f(z) &
+        normal_f(e2) & normal_f(l) & normal_f(nea) & normal_f(m) & normal_f(al)) {
+        *beta = b;
+        *alpha = al;
+        return;
+    }
     *beta = ieee_div(1.0f, ieee_add(1.0f, libm_expf(-bv)));
-    const float z = ieee_add(av, dt);
-    *alpha = libm_expf(ieee_mul(nea, libm_log1pf(libm_expf(z))));
+    const float ze = ieee_add(av, dt);
+    *alpha = libm_expf(ieee_mul(nea, libm_log1pf(libm_expf(ze))));
 }
 
 // One state column j of one head, both passes of the reference's blocked

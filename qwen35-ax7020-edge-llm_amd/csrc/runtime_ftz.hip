@@ -224,8 +224,9 @@ extern "C" __global__ __launch_bounds__(256) void rt_linear_attn_kernel(RtLinear
     constexpr int COLS = D / RT_ATTN_SPLIT;
     static_assert(D == 128 && COLS == 32 && KG / 4 <= kPitch, "sized for 16 heads of 128 and a 1024 gate input");
     __shared__ ResidueLds L;
-    __shared__ __attribute__((aligned(16))) float qv[D];
-    __shared__ __attribute__((aligned(16))) float kv[D];
+    __shared__ __attribute__((aligned(16))) float kq[2][D];  // k, q: one array, so a lane's vector is one address
+    float* const kv = kq[0];
+    float* const qv = kq[1];
     __shared__ float vv[D];
     __shared__ float sc[5];
     const int h = blockIdx.x / RT_ATTN_SPLIT, part = blockIdx.x % RT_ATTN_SPLIT;
@@ -236,8 +237,13 @@ extern "C" __global__ __launch_bounds__(256) void rt_linear_attn_kernel(RtLinear
     float* col = a.state + (size_t)h * D * D + ((size_t)(cj >> 2) * NG * 4 + (cj & 3)) * 4;
     float4 st[NG];
     if (w == 3) {
+        // silu(z) of this workgroup's columns, for the gated norm in the o GEMV
+        // (z loaded ahead of the state, so its wait does not wait for the state)
+        const int ez = h * D + cj;
+        const float zv = a.z[ez];
 #pragma unroll
         for (int ig = 0; ig < NG; ++ig) st[ig] = *reinterpret_cast<const float4*>(col + ig * 16);
+        if (lane < COLS) a.zsilu[ez] = silu_scalar(zv);
     } else if (w == 0) {
         // gates' products wa[h] * x, wb[h] * x (all loads first)
         const float* ra = a.wa + (size_t)h * KG;
@@ -260,9 +266,9 @@ extern "C" __global__ __launch_bounds__(256) void rt_linear_attn_kernel(RtLinear
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         float s = 0.0f;
-        if (lane < 8) s = chain_add_n<KG / 4>(0.0f, &L.p[lane >> 2][lane & 3][0]);
+        if (lane < 8) s = chain_add256(0.0f, &L.p[lane >> 2][lane & 3][0]);
         const float r = lanes4_combine(s);
-        const float bv = __shfl(r, 4, 64);
+        const float bv = readlane_f(r, 4);
         if (lane == 0) gates_scalar(r, bv, a.nea[h], a.dt[h], &sc[0], &sc[1]);
     } else {
         // conv1d + SiLU over the head's q, k and v channels (all in the vector
@@ -299,11 +305,6 @@ extern "C" __global__ __launch_bounds__(256) void rt_linear_attn_kernel(RtLinear
                 if (k == 2 && a.mixed) a.mixed[c] = y;
             }
         }
-        // silu(z) of this workgroup's columns, for the gated norm in the o GEMV
-        if (t < COLS) {
-            const int e = h * D + part * COLS + t;
-            a.zsilu[e] = silu_scalar(a.z[e]);
-        }
     }
     __syncthreads();
 
@@ -318,11 +319,12 @@ extern "C" __global__ __launch_bounds__(256) void rt_linear_attn_kernel(RtLinear
         float s = 0.0f;
         if (lane < 8) s = chain_add_n<NG>(0.0f, &L.p[lane >> 2][lane & 3][0]);
         const float r = lanes4_combine(s);
-        const float q_sq = __shfl(r, 4, 64);
+        const float q_sq = readlane_f(r, 4);
         if (lane == 0) {
-            const float q_scale = ieee_div(1.0f, ieee_sqrt((float)D));
-            sc[2] = ieee_div(1.0f, ieee_sqrt(ieee_add(r, 1e-6f)));
-            sc[3] = ieee_div(q_scale, ieee_sqrt(ieee_add(q_sq, 1e-6f)));
+            // 1 / sqrtf(D): both steps of normal constants, so the instructions are exact
+            const float q_scale = __fdiv_rn(1.0f, (float)__builtin_sqrt((double)D));
+            sc[2] = div_sqrt_add(1.0f, r, 1e-6f);
+            sc[3] = div_sqrt_add(q_scale, q_sq, 1e-6f);
         }
     }
     __syncthreads();
@@ -352,34 +354,42 @@ extern "C" __global__ __launch_bounds__(256) void rt_linear_attn_kernel(RtLinear
     // recurrent step on the columns held in registers
     if (w == 3) {
         const float alpha = sc[0], beta = sc[1], qk = sc[4];
-        const float* vec = role ? qv : kv;
+        // kv (role 0) or qs (role 1), ascending i; the vector's 16-byte groups
+        // are read a few steps ahead (an empty asm statement pins each step,
+        // so the reads do not all land in registers at once)
+        const float4* vec = reinterpret_cast<const float4*>(&kq[role][0]);
+        constexpr int kAhead = 4;
         float4 vr[NG];
 #pragma unroll
-        for (int ig = 0; ig < NG; ++ig) vr[ig] = *reinterpret_cast<const float4*>(vec + 4 * ig);
-        float acc = 0.0f;  // kv (role 0) or qs (role 1), ascending i
+        for (int ig = 0; ig < kAhead; ++ig) vr[ig] = vec[ig];
+        float acc = 0.0f;
 #pragma unroll
         for (int ig = 0; ig < NG; ++ig) {
+            if (ig + kAhead < NG) vr[ig + kAhead] = vec[ig + kAhead];
             acc = acc + st[ig].x * vr[ig].x;
             acc = acc + st[ig].y * vr[ig].y;
             acc = acc + st[ig].z * vr[ig].z;
             acc = acc + st[ig].w * vr[ig].w;
+            asm volatile("" : "+v"(acc)::"memory");
         }
         const int c = lane & 31;
         const float kvs = __shfl(acc, c, 64), qss = __shfl(acc, 32 + c, 64);
         const float d = (vv[cj] - kvs * alpha) * beta;
         const float o = qss * alpha + qk * d;
-        // S[i][j] = S[i][j] * a + d * k[i]: role 0 the first 16 row groups, role 1 the rest
+        // S[i][j] = S[i][j] * a + d * k[i]: role 0 the first 16 row groups, role 1
+        // the rest, in the same instructions (the lane's half chosen by select)
+        const float4* k4v = reinterpret_cast<const float4*>(kv) + role * (NG / 2);
+        float* colr = col + role * (NG / 2) * 16;
 #pragma unroll
-        for (int ig = 0; ig < NG; ++ig) {
-            if ((ig < NG / 2) == (role == 0)) {
-                const float4 k4 = *reinterpret_cast<const float4*>(kv + 4 * ig);
-                float4 nv;
-                nv.x = st[ig].x * alpha + d * k4.x;
-                nv.y = st[ig].y * alpha + d * k4.y;
-                nv.z = st[ig].z * alpha + d * k4.z;
-                nv.w = st[ig].w * alpha + d * k4.w;
-                *reinterpret_cast<float4*>(col + ig * 16) = nv;
-            }
+        for (int g = 0; g < NG / 2; ++g) {
+            const float4 s4 = role ? st[g + NG / 2] : st[g];
+            const float4 k4 = k4v[g];
+            float4 nv;
+            nv.x = s4.x * alpha + d * k4.x;
+            nv.y = s4.y * alpha + d * k4.y;
+            nv.z = s4.z * alpha + d * k4.z;
+            nv.w = s4.w * alpha + d * k4.w;
+            *reinterpret_cast<float4*>(colr + g * 16) = nv;
         }
         if (role == 0) a.attn[h * D + cj] = o;
     }
