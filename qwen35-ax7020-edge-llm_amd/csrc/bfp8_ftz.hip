@@ -28,6 +28,7 @@
 
 #include "bfp8_internal.h"
 #include "gemv_dev.h"
+#include "quant_block.h"
 #include "runtime_internal.h"
 #include "wave_topk.h"
 
@@ -479,7 +480,165 @@ __device__ __forceinline__ void wide_tile(const Bfp8GemvDesc& d, int t, float* t
     }
 }
 
+// ---- the lm_head launch with the plan's activation quantization folded in ------------
+// A plan step was a quantize launch (every activation) and then the lm_head's
+// streaming launch.  Here one launch does both: every workgroup quantizes the
+// lm_head's activation (K <= 1024) into LDS while its tile's weights are in
+// flight, and each wavefront one 64-element block of the plan's other
+// activations (a task) into the records the next launch reads -- the launch
+// boundary publishes them.  Tiles are reduced as in the streaming kernel:
+// wavefront q computes residue q of the tile's 64 rows (lane = row), fs_q in
+// block order, y = (fs0 + fs2) + (fs1 + fs3), with the split activation words
+// broadcast from registers by v_readlane.
+struct HeadLds {
+    __attribute__((aligned(16))) uint32_t xs[BFP8_HEAD_MAX_NB * 32];
+    float xsc[BFP8_HEAD_MAX_NB];
+    uint32_t rec[kWaves][32];
+    float red[256];
+};
+
+// bfp8_quant_block_wave with the records written through global-address-space
+// pointers (flat stores would also count on the LDS counter).
+typedef __attribute__((address_space(1))) uint32_t* g_u32_ptr;
+typedef __attribute__((address_space(1))) float* g_f32_ptr;
+typedef __attribute__((address_space(1))) int16_t* g_i16_ptr;
+__device__ __forceinline__ void quantize_task(const Bfp8QuantDesc& d, int b, float xv, int lane, uint32_t* rec) {
+    const Bfp8QuantLane r = bfp8_quant_lane(xv);
+    if (d.xq) ((g_i16_ptr)d.xq)[(size_t)b * 64 + lane] = (int16_t)r.xq;
+    if (lane == 0) ((g_f32_ptr)d.xscale)[b] = r.xs;
+    const int xl = (int)(int8_t)(r.xq & 0xff);
+    const int xh = (r.xq - xl) >> 8;
+    const int pos = bfp8_split_pos(lane);
+    uint8_t* rb = reinterpret_cast<uint8_t*>(rec);
+    rb[pos] = (uint8_t)xh;
+    rb[pos + 16] = (uint8_t)xl;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane < 32) ((g_u32_ptr)d.xsplit)[(size_t)b * 32 + lane] = rec[lane];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 }  // namespace
+
+// Every load is unconditional (indices clamped): the compiler can then count
+// them and wait for each block's weights alone.  qtasks holds at least one
+// entry (ntasks may be 0) and every workgroup has at least one tile.
+struct HeadTile {
+    u32x4 w[BFP8_HEAD_MAX_NB];
+    uint32_t e[BFP8_HEAD_MAX_NB / 4];
+};
+
+__device__ __forceinline__ void head_issue(HeadTile& T, const Bfp8GemvDesc& d, int t, int nb, int q, int lane) {
+    const int nb4 = (nb + 3) >> 2;
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(d.mant + (size_t)t * nb * 4096u, (uint32_t)nb * 4096u);
+    const __amdgpu_buffer_rsrc_t ers = make_rsrc(d.exps + (size_t)t * nb4 * 256u, (uint32_t)nb4 * 256u);
+#pragma unroll
+    for (int u = 0; u < BFP8_HEAD_MAX_NB; ++u) T.w[u] = load_w(wrs, q * 1024 + lane * 16, min(u, nb - 1) * 4096);
+#pragma unroll
+    for (int m = 0; m < BFP8_HEAD_MAX_NB / 4; ++m) T.e[m] = load_e(ers, lane * 4, min(m, nb4 - 1) * 256);
+}
+
+// fs_q of one tile (blocks in order), then y = (fs0 + fs2) + (fs1 + fs3) and
+// the tile's top-k partial
+__device__ __forceinline__ void head_reduce(const HeadTile& T, const Bfp8GemvDesc& d, int t, int nb, int q,
+                                            int lane, uint32_t xr0, uint32_t xr1, uint32_t xsv, HeadLds& L) {
+    float fs = 0.0f;
+#pragma unroll
+    for (int b = 0; b < BFP8_HEAD_MAX_NB; ++b) {
+        if (b < nb) {
+            const uint32_t src = b < 8 ? xr0 : xr1;
+            uint32_t x[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) x[k] = __builtin_amdgcn_readlane(src, (b & 7) * 8 + k);
+            const u32x4 w = T.w[b];
+            int S = __builtin_amdgcn_sdot4((int)w.x, (int)x[0], 0, false);
+            S = __builtin_amdgcn_sdot4((int)w.y, (int)x[1], S, false);
+            S = __builtin_amdgcn_sdot4((int)w.z, (int)x[2], S, false);
+            S = __builtin_amdgcn_sdot4((int)w.w, (int)x[3], S, false);
+            S = (int)((uint32_t)S << 8);
+            S = __builtin_amdgcn_sdot4((int)w.x, (int)x[4], S, false);
+            S = __builtin_amdgcn_sdot4((int)w.y, (int)x[5], S, false);
+            S = __builtin_amdgcn_sdot4((int)w.z, (int)x[6], S, false);
+            S = __builtin_amdgcn_sdot4((int)w.w, (int)x[7], S, false);
+            const uint32_t e = (T.e[b >> 2] >> (8 * (b & 3))) & 0xffu;
+            fs = epilogue(fs, S, e, __uint_as_float(__builtin_amdgcn_readlane(xsv, b)));
+        }
+    }
+    L.red[q * 64 + lane] = fs;
+    __syncthreads();
+    float y = 0.0f;
+    if (q == 0) {
+        // vadd_f32(low, high) then vpadd_f32: y = (fs0 + fs2) + (fs1 + fs3)
+        y = (L.red[lane] + L.red[128 + lane]) + (L.red[64 + lane] + L.red[192 + lane]);
+        const int row = t * BFP8_TILE_ROWS + lane;
+        if (d.y && row < d.pair_rows) d.y[row] = y;
+    }
+    if (d.topk > 0) topk_partial(d.partials, d.topk, d.pair_rows, t, y);
+    __syncthreads();  // L.red is reused by the next tile
+}
+
+extern "C" __global__ __launch_bounds__(256) void bfp8_gemv_head_kernel(
+    const Bfp8GemvDesc* __restrict__ descs, const Bfp8TileRef* __restrict__ tiles, const int* __restrict__ wg_off,
+    int head_desc, const float* __restrict__ hx, const Bfp8QuantDesc* __restrict__ qdescs,
+    const int2* __restrict__ qtasks, int ntasks) {
+    constexpr int kPerWave = BFP8_HEAD_MAX_NB / kWaves;
+    __shared__ HeadLds L;
+    const int q = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const Bfp8GemvDesc& d = descs[head_desc];
+    const int nb = d.K >> 6;  // 1 .. BFP8_HEAD_MAX_NB (host-checked)
+    const int beg = wg_off[blockIdx.x], end = wg_off[blockIdx.x + 1];
+
+    // 0. loads in the order they are needed: the lm_head activation's blocks
+    // q, q + 4, ... (one element per lane), this wavefront's first task, then
+    // the first tile's weights
+    float hv[kPerWave];
+#pragma unroll
+    for (int k = 0; k < kPerWave; ++k) hv[k] = hx[min(q + kWaves * k, nb - 1) * 64 + lane];
+    const int wid = (int)blockIdx.x * kWaves + q, nw = (int)gridDim.x * kWaves;
+    const int2 tk = qtasks[min(wid, max(ntasks - 1, 0))];
+    const int tq = __builtin_amdgcn_readfirstlane(tk.x), tb = __builtin_amdgcn_readfirstlane(tk.y);
+    // (a global-address-space pointer: a flat load would count on both counters)
+    const float tv = ((const __attribute__((address_space(1))) float*)qdescs[tq].x)[(size_t)tb * 64 + lane];
+    HeadTile T;
+    int t = tiles[beg].tile;
+    head_issue(T, d, t, nb, q, lane);
+
+    // 1. the lm_head activation, quantized into LDS (slots b >= nb hold a
+    // copy of block nb - 1 and are never read); this wavefront's tasks
+#pragma unroll
+    for (int k = 0; k < kPerWave; ++k) {
+        const int b = q + kWaves * k;
+        bfp8_quant_block_lds(hv[k], lane, &L.xsc[b], &L.xs[b * 32]);
+    }
+    if (wid < ntasks) quantize_task(qdescs[tq], tb, tv, lane, L.rec[q]);
+    __syncthreads();
+
+    // 2. residue q's split words in registers: lane l holds word l & 7 of
+    // block l >> 3 (xr0) and of block 8 + (l >> 3) (xr1), and the scale of block l
+    const int xbk = lane >> 3, xw = lane & 7;
+    const uint32_t xr0 = xbk < nb ? L.xs[(xbk * 4 + q) * 8 + xw] : 0u;
+    const uint32_t xr1 = xbk + 8 < nb ? L.xs[((xbk + 8) * 4 + q) * 8 + xw] : 0u;
+    const uint32_t xsv = lane < nb ? __float_as_uint(L.xsc[lane]) : 0u;
+
+    // 3. the tiles
+    head_reduce(T, d, t, nb, q, lane, xr0, xr1, xsv, L);
+    for (int i = beg + 1; i < end; ++i) {
+        t = tiles[i].tile;
+        head_issue(T, d, t, nb, q, lane);
+        head_reduce(T, d, t, nb, q, lane, xr0, xr1, xsv, L);
+    }
+    // 4. tasks beyond one per wavefront (more tasks than wavefronts)
+    for (int j = wid + nw; j < ntasks; j += nw) {
+        const int jq = __builtin_amdgcn_readfirstlane(qtasks[j].x);
+        const int jb = __builtin_amdgcn_readfirstlane(qtasks[j].y);
+        const Bfp8QuantDesc& dj = qdescs[jq];
+        quantize_task(dj, jb, dj.x[(size_t)jb * 64 + lane], lane, L.rec[q]);
+    }
+}
 
 // Single GEMV, persistent: workgroup w takes tiles w, w + gridDim, ...
 // kLanes also writes the int32 residue-lane block sums.
@@ -694,6 +853,15 @@ hipError_t bfp8_launch_gemv_grouped(const Bfp8GemvDesc* descs_dev, const Bfp8Til
     else
         hipLaunchKernelGGL(bfp8_gemv_grouped_kernel, dim3(nwg), dim3(256), 0, s, descs_dev, tiles_dev,
                            wg_off_dev);
+    return hipGetLastError();
+}
+
+hipError_t bfp8_launch_gemv_head(const Bfp8GemvDesc* descs_dev, const Bfp8TileRef* tiles_dev, const int* wg_off_dev,
+                                 int nwg, int head_desc, const float* hx, const Bfp8QuantDesc* qdescs_dev,
+                                 const int* qtasks_dev, int ntasks, hipStream_t s) {
+    if (nwg <= 0) return hipSuccess;
+    hipLaunchKernelGGL(bfp8_gemv_head_kernel, dim3(nwg), dim3(256), 0, s, descs_dev, tiles_dev, wg_off_dev,
+                       head_desc, hx, qdescs_dev, reinterpret_cast<const int2*>(qtasks_dev), ntasks);
     return hipGetLastError();
 }
 

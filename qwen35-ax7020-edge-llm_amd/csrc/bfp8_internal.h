@@ -105,6 +105,14 @@ hipError_t bfp8_launch_topk_merge(const Bfp8GemvDesc& d, hipStream_t s);
 // earlier launch on the stream).
 hipError_t bfp8_launch_gemv_grouped(const Bfp8GemvDesc* descs_dev, const Bfp8TileRef* tiles_dev,
                                     const int* wg_off_dev, int nwg, int merge_desc, hipStream_t s);
+// The lm_head's persistent launch with the plan's quantization folded in:
+// every workgroup quantizes the lm_head activation hx (K <= 64 *
+// BFP8_HEAD_MAX_NB, K % 64 == 0) itself, and wavefront task j quantizes block
+// qtasks[2j+1] of qdescs_dev[qtasks[2j]] into that descriptor's records.
+#define BFP8_HEAD_MAX_NB 16
+hipError_t bfp8_launch_gemv_head(const Bfp8GemvDesc* descs_dev, const Bfp8TileRef* tiles_dev, const int* wg_off_dev,
+                                 int nwg, int head_desc, const float* hx, const Bfp8QuantDesc* qdescs_dev,
+                                 const int* qtasks_dev, int ntasks, hipStream_t s);
 // Extra load, in blocks of the byte-balanced dealing, that a folded merge
 // puts on workgroup 0 of a grouped launch.
 #define BFP8_MERGE_COST_BLOCKS 16

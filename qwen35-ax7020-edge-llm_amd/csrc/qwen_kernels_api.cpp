@@ -760,8 +760,10 @@ struct Plan {
     std::vector<int> odd_items;    // items needing the odd-row kernel
     std::vector<int> float_items;  // K > 4096 items (float path, own launches)
     DevBuf descs, qdescs, xq, xscale, xsplit, partials;
+    DevBuf qtasks;                 // fused head: (quantize descriptor, block) pairs
     Launch head, rest;             // lm_head tiles, then every other GEMV's
-    int nq = 0, max_nb = 0;
+    int nq = 0, max_nb = 0, ntasks = 0;
+    bool fused_head = false;       // the lm_head launch quantizes every activation
     int topk_desc = -1;            // the lm_head item, if any
     std::vector<Bfp8GemvDesc> hdesc;
 };
@@ -814,7 +816,7 @@ int deal_tiles(Launch& L, const std::vector<int>& idx, const bfp8_plan_item* ite
 
 void release_plan(Plan* p) {
     p->descs.release(); p->qdescs.release(); p->xq.release(); p->xscale.release(); p->xsplit.release();
-    p->partials.release();
+    p->partials.release(); p->qtasks.release();
     p->head.tiles.release(); p->head.wg_off.release(); p->rest.tiles.release(); p->rest.wg_off.release();
 }
 
@@ -864,6 +866,7 @@ void* bfp8_plan_create(const bfp8_plan_item* items, int n) {
     rc = rc ? rc : p->xscale.reserve(xsc_floats * 4);
     rc = rc ? rc : p->xq.reserve(xq_elems * 2);
     std::vector<Bfp8QuantDesc> hq;
+    std::vector<int> hq_of_item(n, -1);
     size_t ow = 0, of = 0, oq = 0;
     for (int i = 0; i < n && !rc; ++i) {
         const bfp8_plan_item& it = items[i];
@@ -880,6 +883,7 @@ void* bfp8_plan_create(const bfp8_plan_item* items, int n) {
         q.xscale = p->xscale.as<float>() + of;
         q.xsplit = p->xsplit.as<uint32_t>() + ow;
         q.K = it.K;
+        hq_of_item[i] = (int)hq.size();
         hq.push_back(q);
         d = plain_desc(it.y, q.xsplit, q.xscale, (const uint8_t*)it.mant_gpu, it.exps_gpu, it.M, it.K, nullptr);
         if (it.topk > 0) {
@@ -920,6 +924,33 @@ void* bfp8_plan_create(const bfp8_plan_item* items, int n) {
     else
         rc = rc ? rc : deal_tiles(p->rest, rest_idx, items, fold ? BFP8_MERGE_COST_BLOCKS : 0, !fold);
     p->nq = (int)hq.size();
+    // An lm_head of K <= 1024 (whole blocks) quantizes in its own launch: its
+    // own activation per workgroup, every other one block per wavefront task.
+    if (p->topk_desc >= 0 && !rc) {
+        const bfp8_plan_item& ht = items[p->topk_desc];
+        if ((ht.K & 63) == 0 && (ht.K >> 6) <= BFP8_HEAD_MAX_NB && p->head.nwg > 0) {
+            std::vector<int> tasks;
+            for (int qi = 0; qi < (int)hq.size(); ++qi) {
+                if (qi == hq_of_item[p->topk_desc]) continue;  // quantized by every workgroup
+                for (int b = 0; b < bfp8_nblocks(hq[qi].K); ++b) {
+                    tasks.push_back(qi);
+                    tasks.push_back(b);
+                }
+            }
+            p->ntasks = (int)tasks.size() / 2;
+            if (tasks.empty()) {  // the kernel always reads one entry
+                tasks.push_back(hq_of_item[p->topk_desc]);
+                tasks.push_back(0);
+            }
+            {
+                rc = p->qtasks.reserve(tasks.size() * sizeof(int));
+                if (!rc && hipMemcpy(p->qtasks.p, tasks.data(), tasks.size() * sizeof(int), hipMemcpyHostToDevice) !=
+                               hipSuccess)
+                    rc = BFP8_EHIP;
+            }
+            p->fused_head = !rc;
+        }
+    }
     rc = rc ? rc : p->descs.reserve(p->hdesc.size() * sizeof(Bfp8GemvDesc));
     rc = rc ? rc : p->qdescs.reserve(hq.size() * sizeof(Bfp8QuantDesc));
     if (!rc && (hipMemcpy(p->descs.p, p->hdesc.data(), p->hdesc.size() * sizeof(Bfp8GemvDesc), hipMemcpyHostToDevice) != hipSuccess ||
@@ -948,8 +979,13 @@ int bfp8_plan_launch(void* plan, int stage, void* stream) {
     const Bfp8GemvDesc* descs = p->descs.as<Bfp8GemvDesc>();
     const bool fold = p->topk_desc >= 0 && p->rest.nwg > 0;
     if (stage == 0) {
-        HIP_OK(bfp8_launch_gemv_grouped(descs, p->head.tiles.as<Bfp8TileRef>(), p->head.wg_off.as<int>(),
-                                        p->head.nwg, -1, s));
+        if (p->fused_head)
+            HIP_OK(bfp8_launch_gemv_head(descs, p->head.tiles.as<Bfp8TileRef>(), p->head.wg_off.as<int>(),
+                                         p->head.nwg, p->topk_desc, p->items[p->topk_desc].x,
+                                         p->qdescs.as<Bfp8QuantDesc>(), p->qtasks.as<int>(), p->ntasks, s));
+        else
+            HIP_OK(bfp8_launch_gemv_grouped(descs, p->head.tiles.as<Bfp8TileRef>(), p->head.wg_off.as<int>(),
+                                            p->head.nwg, -1, s));
     } else if (stage == 1) {
         if (p->rest.rows[0] >= 0) {
             RtRowsArgs a{};
@@ -993,7 +1029,7 @@ const char* bfp8_plan_kernel_name(void* plan, int stage) {
     const Plan* p = static_cast<const Plan*>(plan);
     if (!p) return "";
     const bool fold = p->topk_desc >= 0 && p->rest.nwg > 0;
-    if (stage == 0) return p->head.nwg > 0 ? "bfp8_gemv_grouped_kernel" : "";
+    if (stage == 0) return p->head.nwg > 0 ? (p->fused_head ? "bfp8_gemv_head_kernel" : "bfp8_gemv_grouped_kernel") : "";
     if (stage == 1) {
         if (p->rest.rows[0] >= 0) return "rt_rows_gemv_kernel";
         if (p->rest.wide) return "bfp8_gemv_wide_grouped_kernel";
@@ -1015,7 +1051,9 @@ int bfp8_plan_run_gemv(void* plan, void* stream) {
 }
 
 int bfp8_plan_run(void* plan, void* stream) {
-    int rc = bfp8_plan_quantize(plan, stream);
+    const Plan* p = static_cast<const Plan*>(plan);
+    // a fused lm_head launch quantizes every activation itself
+    int rc = (p && p->fused_head) ? BFP8_OK : bfp8_plan_quantize(plan, stream);
     return rc ? rc : bfp8_plan_run_gemv(plan, stream);
 }
 

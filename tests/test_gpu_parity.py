@@ -396,12 +396,44 @@ def test_small_plan_one_tile_per_workgroup(gpu, torch_mod):
     plan.close()
 
 
+@pytest.mark.parametrize("case", ["one", "one_ragged_odd", "pair_shared_x"])
+def test_plan_rows_kernel_paths(gpu, torch_mod, case):
+    """Plans of one GEMV, or of two reading the same activation, run on the
+    16-row kernel (quantized activation): odd M adds the tail-row kernel, a
+    ragged K uses its K / 64 whole blocks."""
+    qk, torch = gpu, torch_mod
+    shapes = {"one": [(3584, 1024)], "one_ragged_odd": [(1023, 1000)],
+              "pair_shared_x": [(3584, 1024), (3584, 1024)]}[case]
+    K = shapes[0][1]
+    x = qk.synth_normal(K, 5150)
+    xd = torch.from_numpy(x).cuda()
+    items, refs = [], []
+    for j, (M, K) in enumerate(shapes):
+        dm = qk.DeviceMatrix.synth(M, K, 5100 + j, 124, 130)
+        items.append({"mat": dm, "x": xd, "y": torch.empty(M, dtype=torch.float32, device="cuda")})
+        refs.append((M, K, 5100 + j))
+    plan = qk.SweepPlan(items)
+    assert plan.kernel_name(1) == "rt_rows_gemv_kernel"
+    say("rows plan", case)
+    for rep in range(2):
+        for it in items:
+            it["y"].fill_(np.nan)
+        plan.run()
+        torch.cuda.synchronize()
+        for it, (M, K, seed) in zip(items, refs):
+            mant, exps = qk.synth_planes(M, K, seed, 124, 130)
+            y_ref = ol.gemv_neon(x, mant, exps)[0]
+            assert same_f32(it["y"].cpu().numpy(), y_ref), (rep, M, K, mismatch(it["y"].cpu().numpy(), y_ref))
+    plan.close()
+
+
 @pytest.mark.parametrize("shape", ["alone", "with_small_gemv", "ragged_2049_tiles"])
 def test_plan_lm_head_merge_paths(gpu, torch_mod, shape):
     """A plan's lm_head merge runs as the stand-alone merge kernel (lm_head
     alone) or folded into workgroup 0 of the second launch (other GEMVs
     present, here a 2-tile one); a 2049-tile ragged vocabulary takes several
-    passes over the list heads."""
+    passes over the list heads.  The second run uses new activations written
+    in place: the lm_head launch quantizes them all again (no stale records)."""
     qk, torch = gpu, torch_mod
     V, H, k = {"alone": (16384, 1024, 64), "with_small_gemv": (65536, 1024, 40),
                "ragged_2049_tiles": (131074, 1024, 40)}[shape]
@@ -417,9 +449,15 @@ def test_plan_lm_head_merge_paths(gpu, torch_mod, shape):
                       "y": torch.empty(128, dtype=torch.float32, device="cuda")})
     plan = qk.SweepPlan(items)
     mant, exps = qk.synth_planes(V, H, 777, 122, 128)
-    y_ref, *_ = ol.gemv_neon(xl, mant, exps)
-    ids_ref, sc_ref = ol.topk(y_ref, k)
     for rep in range(2):
+        if rep == 1:  # new activations, same device buffers
+            xl = qk.synth_normal(H, 878)
+            items[0]["x"].copy_(torch.from_numpy(xl))
+            if small:
+                xs = qk.synth_normal(256, 880)
+                items[1]["x"].copy_(torch.from_numpy(xs))
+        y_ref, *_ = ol.gemv_neon(xl, mant, exps)
+        ids_ref, sc_ref = ol.topk(y_ref, k)
         plan.run()
         torch.cuda.synchronize()
         ids, sc, cnt = plan.topk_out
@@ -427,7 +465,7 @@ def test_plan_lm_head_merge_paths(gpu, torch_mod, shape):
         assert np.array_equal(ids.cpu().numpy(), ids_ref) and same_f32(sc.cpu().numpy(), sc_ref), rep
         if small:
             sm, se = qk.synth_planes(128, 256, 779, 124, 130)
-            assert same_f32(items[1]["y"].cpu().numpy(), ol.gemv_neon(xs, sm, se)[0])
+            assert same_f32(items[1]["y"].cpu().numpy(), ol.gemv_neon(xs, sm, se)[0]), rep
     plan.close()
 
 
