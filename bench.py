@@ -7,10 +7,12 @@ weight sweep at batch 1 -- per layer gate 3584x1024, up 3584x1024, down
 the 65536x1024 lm_head with fused greedy argmax + top-40.  Mantissas uniform
 in [-127, 127], exponents uniform in [124, 130] ([122, 128] for the lm_head),
 a fresh N(0,1) activation per GEMV (silu(a)*b with 1% +-20 outliers for the
-down projection).  One step = quantize every activation (one launch) + two
-persistent streaming launches (the lm_head's 1024 tiles, then the other 120
-GEMVs' tiles, whose workgroup 0 first merges the lm_head top-k), weights
-resident in HBM.  Weight copies rotate (2 sweeps = 1.08 GB) so the 256 MB
+down projection).  One step = two persistent streaming launches: the
+lm_head's 1024 tiles (that launch also quantizes every activation: the
+lm_head's in each workgroup, the others one block per wavefront), then the
+other 120 GEMVs' tiles, whose workgroup 0 first merges the lm_head top-k;
+weights resident in HBM.  Plans without an lm_head quantize in a launch of
+their own first.  Weight copies rotate (2 sweeps = 1.08 GB) so the 256 MB
 Infinity Cache cannot serve repeats.
 
 roofline: the launch that moves the most bytes (the 120-GEMV launch for the
@@ -196,7 +198,7 @@ def main():
         keep.append(plan_items)
     torch.cuda.synchronize()
 
-    # warmup, then the timed steps (one quantize + one grouped GEMV launch each)
+    # warmup, then the timed steps (plan.run(): every launch of one step)
     for i in range(args.warmup):
         plans[i % copies].run()
     torch.cuda.synchronize()

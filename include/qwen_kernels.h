@@ -298,12 +298,15 @@ int qwen_weights_find(const char* name, const int8_t** mant_gpu, const uint8_t**
 int bfp8_dev_pack_rows(int8_t* mant_gpu, uint8_t* exps_gpu, const uint8_t* row_stream, int M, int K, void* stream);
 
 /* A sweep plan: many independent GEMVs (and at most one fused lm_head)
- * executed as one quantize launch plus two streaming launches: the lm_head's
- * tiles, then every other GEMV's (larger K first), whose workgroup 0 first
- * merges the lm_head's per-tile top-k partials.  A plan without an lm_head
- * and with few row tiles runs its GEMVs one tile per 16-wavefront workgroup.
- * Item i reads x (device, K floats) and writes y (device, M floats), or, for
- * the lm_head item (topk > 0), the four top-k outputs. */
+ * executed as two streaming launches: the lm_head's tiles, then every other
+ * GEMV's (larger K first), whose workgroup 0 first merges the lm_head's
+ * per-tile top-k partials.  When the lm_head's K is a multiple of 64 and at
+ * most 1024 its launch also quantizes every activation of the plan (else, and
+ * without an lm_head, a quantize launch comes first).  A plan without an
+ * lm_head runs one GEMV, or two reading the same x, 16 rows per workgroup, and
+ * other plans of few row tiles one tile per 16-wavefront workgroup.  Item i
+ * reads x (device, K floats) and writes y (device, M floats), or, for the
+ * lm_head item (topk > 0), the four top-k outputs. */
 typedef struct bfp8_plan_item {
     const float* x;
     float* y;
@@ -321,7 +324,8 @@ typedef struct bfp8_plan_item {
 void* bfp8_plan_create(const bfp8_plan_item* items, int n);
 int bfp8_plan_run(void* plan, void* stream);
 /* Only the GEMV launches (activations already quantized by a previous
- * bfp8_plan_run or bfp8_plan_quantize). */
+ * bfp8_plan_run or bfp8_plan_quantize; a plan whose lm_head launch quantizes
+ * does so here too). */
 int bfp8_plan_run_gemv(void* plan, void* stream);
 /* One stage of bfp8_plan_run_gemv, for timing each launch on its own:
  * 0 = the lm_head's tiles, 1 = the other GEMVs' tiles with the top-k merge

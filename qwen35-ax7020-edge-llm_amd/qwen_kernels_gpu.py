@@ -423,9 +423,10 @@ def lm_head_topk(mat: DeviceMatrix, xsplit, xscale, k: int):
 
 
 class SweepPlan:
-    """Grouped GEMV plan: per run one quantize launch, then the persistent
-    streaming launches (the lm_head's tiles, then every other GEMV's, whose
-    workgroup 0 also merges the lm_head's top-k).
+    """Grouped GEMV plan: per run the persistent streaming launches (the
+    lm_head's tiles, a launch that also quantizes every activation, then every
+    other GEMV's, whose workgroup 0 also merges the lm_head's top-k); plans
+    without an lm_head quantize in a launch of their own first.
 
     items: sequence of dicts with keys x (device f32 [K]), mat (DeviceMatrix) and either
     y (device f32 [M]) or topk (int) for the fused lm_head (outputs allocated here).
