@@ -322,6 +322,46 @@ def test_forward_linear_layer_bit_exact(gpu, model):
             assert same(gc, rc) and same(ol.gdn_state_from_blocked(gs, 16, 128), rs.reshape(16, 128, 128)), step
 
 
+def test_forward_linear_layer_exact_fallbacks(gpu, fresh_cache):
+    """Inputs that send the fused kernels' scalar chains to their exact paths
+    (the float fast path applies only to normal operands and results): head 0's
+    z rows are zero (silu(0), gated products of zero), head 1's k is zero (its
+    L2 scale of a zero sum), heads 2 and 3 have zero gate rows (softplus and
+    sigmoid of 0), dt of head 4 is zero, h holds zeros and subnormals, and a
+    second step runs on h = 0 (the rms scale of a zero sum, all-zero blocks).
+    Bit-exact against the oracle with correctly rounded libm."""
+    lib = gpu.load()
+    lib.bfp8_cache_clear()
+    m = Model(2027, n_layers=1, full=(), embed=False)
+    by_addr = {a.ctypes.data: a for a in m.keep}
+    plan = m.gpu_lin[0]
+    mz, _, _, _ = m.planes["z"]
+    mz.reshape(2048, 1024)[0:128] = 0
+    mq, _, _, _ = m.planes["qkv"]
+    kch = slice(2048 + 128, 2048 + 256)  # head 1's k channels
+    mq.reshape(6144, 1024)[kch] = 0
+    for conv in (m.gpu_states[0][0], m.ref_states[0][0]):
+        conv.reshape(3, 6144)[:, kch] = 0
+    by_addr[plan.wa].reshape(16, 1024)[2] = 0
+    by_addr[plan.wb].reshape(16, 1024)[3] = 0
+    by_addr[plan.dt][4] = 0
+    rng = np.random.default_rng(23)
+    h = normal(rng, 1024, 2.0)
+    h[:64] = 0
+    h[64:72] = np.float32(1e-40)
+    want = h.copy()
+    with ol.cr_libm():
+        for step in range(2):
+            if step == 1:
+                h[:] = 0
+                want[:] = 0
+            say("forward_linear_layer fallbacks", step)
+            lib.forward_linear_layer(ctypes.addressof(plan), ptr(h))
+            want = ol.forward_linear_layer(m.ref_lin[0], want)
+            assert same(h, want), (step, np.nonzero(h.view(np.uint32) != want.view(np.uint32))[0][:8])
+            assert m.states_match(), step
+
+
 def test_forward_token_c_with_callback(gpu, fresh_cache):
     """24 layers (18 linear-attention, 6 full-attention whose attention is a
     host callback that edits h), final norm, bf16 lm_head argmax; two tokens,
