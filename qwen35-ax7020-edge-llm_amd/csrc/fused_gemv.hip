@@ -87,6 +87,9 @@ __device__ __forceinline__ void load_prologue(const RtRowsArgs& a, PrologueIn<kE
             in.b[k] = a.zsilu[e];
             in.c[k] = a.w[e & (RT_HEAD_DIM - 1)];
         }
+    } else if constexpr (kMode == RT_ROWS_FLOAT) {
+#pragma unroll
+        for (int k = 0; k < kE; ++k) in.a[k] = a.x[min(tid + kThreads * k, n - 1)];
     } else {
         const int nb = n >> 6;
 #pragma unroll
@@ -201,6 +204,18 @@ __device__ __forceinline__ void swiglu_prologue(const RtRowsArgs& a, const Prolo
     }
 }
 
+// x as given (quant_x_blocks, 04/qwen_kernels_opt.c:182-205) into the LDS
+// activation: the K / 64 whole blocks.
+template <int kE>
+__device__ __forceinline__ void float_prologue(const RtRowsArgs& a, const PrologueIn<kE>& in, RowsLds& L) {
+    const int tid = threadIdx.x, nb = a.K >> 6;
+#pragma unroll
+    for (int k = 0; k < kE; ++k) {
+        const int b = (tid + kThreads * k) >> 6;
+        if (b < nb) bfp8_quant_block_lds(in.a[k], lane_id(), &L.xsc[b], &L.xs[b * 32]);
+    }
+}
+
 }  // namespace
 
 template <int kMode, int kPer>
@@ -237,6 +252,8 @@ __global__ __launch_bounds__(kThreads) void rt_rows_gemv_kernel(RtRowsArgs a) {
         swiglu_prologue(a, in, L);
     } else if constexpr (kMode == RT_ROWS_GATED) {
         gated_prologue(a, in, L);
+    } else if constexpr (kMode == RT_ROWS_FLOAT) {
+        float_prologue(a, in, L);
     } else {
 #pragma unroll
         for (int k = 0; k < kPer; ++k) {
@@ -246,6 +263,16 @@ __global__ __launch_bounds__(kThreads) void rt_rows_gemv_kernel(RtRowsArgs a) {
         }
     }
     __syncthreads();
+    if constexpr (kMode == RT_ROWS_FLOAT) {
+        if (blockIdx.x == 0 && a.xsplit_out) {
+#pragma unroll
+            for (int k = 0; k < kPer; ++k) {
+                const int e = threadIdx.x + kThreads * k;
+                if (e < nb * 32) a.xsplit_out[e] = L.xs[e];
+                if (e < nb) a.xscale_out[e] = L.xsc[e];
+            }
+        }
+    }
 
     // 3. per-block terms
 #pragma unroll
@@ -292,10 +319,10 @@ __global__ __launch_bounds__(kThreads) void rt_rows_gemv_kernel(RtRowsArgs a) {
 }
 
 hipError_t rt_launch_rows(const RtRowsArgs& a, hipStream_t s) {
-    // a given activation uses the K / 64 whole blocks (as the reference does);
-    // one computed here covers exactly K elements
-    if (a.K < 64 || a.K > RT_ROWS_MAX_K || ((a.K & 63) && a.mode != RT_ROWS_QUANTIZED) || a.ngemv < 1 ||
-        a.ngemv > 2)
+    // a given or float activation uses the K / 64 whole blocks (as the
+    // reference does); one computed from other inputs covers exactly K elements
+    if (a.K < 64 || a.K > RT_ROWS_MAX_K || ((a.K & 63) && a.mode != RT_ROWS_QUANTIZED && a.mode != RT_ROWS_FLOAT) ||
+        a.ngemv < 1 || a.ngemv > 2 || (a.mode == RT_ROWS_FLOAT && a.xsplit_out && !a.xscale_out))
         return hipErrorInvalidValue;
     if (a.mode == RT_ROWS_GATED && a.K != RT_HEADS * RT_HEAD_DIM) return hipErrorInvalidValue;
     const int n0 = (a.g[0].M + 15) / 16, n1 = a.ngemv > 1 ? (a.g[1].M + 15) / 16 : 0;
@@ -317,6 +344,10 @@ hipError_t rt_launch_rows(const RtRowsArgs& a, hipStream_t s) {
     else RT_ROWS_CASE(RT_ROWS_QUANTIZED, 3);
     else RT_ROWS_CASE(RT_ROWS_QUANTIZED, 4);
     else RT_ROWS_CASE(RT_ROWS_GATED, 2);
+    else RT_ROWS_CASE(RT_ROWS_FLOAT, 1);
+    else RT_ROWS_CASE(RT_ROWS_FLOAT, 2);
+    else RT_ROWS_CASE(RT_ROWS_FLOAT, 3);
+    else RT_ROWS_CASE(RT_ROWS_FLOAT, 4);
     else return hipErrorInvalidValue;
 #undef RT_ROWS_CASE
     return hipGetLastError();

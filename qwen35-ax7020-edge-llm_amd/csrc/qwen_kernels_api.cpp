@@ -285,6 +285,31 @@ int gemv_q(float* y, const uint32_t* xsplit, const float* xscale, const uint8_t*
     return BFP8_OK;
 }
 
+// A GEMV of at most BFP8_WIDE_MAX_TILES row tiles from float x on the device:
+// the 16-row kernel quantizes x itself, leaving the records for the odd last
+// row's kernel in xsplit_out / xscale_out (needed only for odd M).
+int rows_gemv_float(float* y, const float* x, const uint8_t* m, const uint8_t* e, int M, int K,
+                    uint32_t* xsplit_out, float* xscale_out, hipStream_t s) {
+    RtRowsArgs a{};
+    a.g[0].mant = m;
+    a.g[0].exps = e;
+    a.g[0].y = y;
+    a.g[0].M = M;
+    a.g[0].pair_rows = M & ~1;
+    a.ngemv = 1;
+    a.split = (M + 15) / 16;
+    a.K = K;
+    a.mode = RT_ROWS_FLOAT;
+    a.x = x;
+    if (M & 1) {
+        a.xsplit_out = xsplit_out;
+        a.xscale_out = xscale_out;
+    }
+    HIP_OK(rt_launch_rows(a, s));
+    HIP_OK(bfp8_launch_tail_row(y, xsplit_out, xscale_out, m, e, M, K, s));
+    return BFP8_OK;
+}
+
 int host_gemv(float* y, const float* x, const int8_t* mant, const uint8_t* exps, int M, int K) {
     const int nb = bfp8_nblocks(K);
     if (nb == 0) {  // no whole block: the reference's accumulators stay 0
@@ -296,7 +321,13 @@ int host_gemv(float* y, const float* x, const int8_t* mant, const uint8_t* exps,
     if ((rc = weights_for(mant, exps, M, K, &w))) return rc;
     if ((rc = upload_x(x, (size_t)nb * 64))) return rc;
     if ((rc = g.y.reserve((size_t)M * 4)) || (rc = g.h_out.reserve((size_t)M * 4))) return rc;
-    if (K <= 4096) {
+    if (K <= 4096 && bfp8_ntiles(M) <= BFP8_WIDE_MAX_TILES) {
+        // one launch: the 16-row kernel quantizes x itself
+        if ((rc = g.xscale.reserve((size_t)nb * 4)) || (rc = g.xsplit.reserve(bfp8_xsplit_bytes(K)))) return rc;
+        if ((rc = rows_gemv_float(g.y.as<float>(), g.x.as<float>(), w.mant, w.exps, M, K, g.xsplit.as<uint32_t>(),
+                                  g.xscale.as<float>(), g.stream)))
+            return rc;
+    } else if (K <= 4096) {
         if ((rc = quantize_ws(K, 1))) return rc;
         if ((rc = gemv_q(g.y.as<float>(), g.xsplit.as<uint32_t>(), g.xscale.as<float>(), w.mant, w.exps,
                          M, K, nullptr, g.stream)))
@@ -764,6 +795,7 @@ struct Plan {
     Launch head, rest;             // lm_head tiles, then every other GEMV's
     int nq = 0, max_nb = 0, ntasks = 0;
     bool fused_head = false;       // the lm_head launch quantizes every activation
+    bool rows_float = false;       // the 16-row launch quantizes its (shared) activation
     int topk_desc = -1;            // the lm_head item, if any
     std::vector<Bfp8GemvDesc> hdesc;
 };
@@ -919,9 +951,16 @@ void* bfp8_plan_create(const bfp8_plan_item* items, int n) {
     const bool rows = !fold && !rest_idx.empty() && rest_idx.size() <= 2 &&
                       (rest_idx.size() == 1 || (items[rest_idx[0]].x == items[rest_idx[1]].x &&
                                                 items[rest_idx[0]].K == items[rest_idx[1]].K));
-    if (rows)
+    if (rows) {
+        // the launch quantizes the shared x itself; its workgroup 0 leaves the
+        // records in the first item's slots, which both items' tail rows read
         for (size_t i = 0; i < rest_idx.size(); ++i) p->rest.rows[i] = rest_idx[i];
-    else
+        p->rows_float = true;
+        for (size_t i = 1; i < rest_idx.size(); ++i) {
+            p->hdesc[rest_idx[i]].xsplit = p->hdesc[rest_idx[0]].xsplit;
+            p->hdesc[rest_idx[i]].xscale = p->hdesc[rest_idx[0]].xscale;
+        }
+    } else
         rc = rc ? rc : deal_tiles(p->rest, rest_idx, items, fold ? BFP8_MERGE_COST_BLOCKS : 0, !fold);
     p->nq = (int)hq.size();
     // An lm_head of K <= 1024 (whole blocks) quantizes in its own launch: its
@@ -1001,9 +1040,10 @@ int bfp8_plan_launch(void* plan, int stage, void* stream) {
             const Bfp8GemvDesc& d0 = p->hdesc[p->rest.rows[0]];
             a.split = (d0.M + 15) / 16;
             a.K = d0.K;
-            a.mode = RT_ROWS_QUANTIZED;
-            a.xsplit = d0.xsplit;
-            a.xscale = d0.xscale;
+            a.mode = RT_ROWS_FLOAT;
+            a.x = p->items[p->rest.rows[0]].x;
+            a.xsplit_out = const_cast<uint32_t*>(d0.xsplit);
+            a.xscale_out = const_cast<float*>(d0.xscale);
             HIP_OK(rt_launch_rows(a, s));
         } else if (p->rest.wide)
             HIP_OK(bfp8_launch_gemv_wide_grouped(descs, p->rest.tiles.as<Bfp8TileRef>(), p->rest.ntiles,
@@ -1052,8 +1092,8 @@ int bfp8_plan_run_gemv(void* plan, void* stream) {
 
 int bfp8_plan_run(void* plan, void* stream) {
     const Plan* p = static_cast<const Plan*>(plan);
-    // a fused lm_head launch quantizes every activation itself
-    int rc = (p && p->fused_head) ? BFP8_OK : bfp8_plan_quantize(plan, stream);
+    // a fused lm_head launch, or a 16-row launch, quantizes its activations itself
+    int rc = (p && (p->fused_head || p->rows_float)) ? BFP8_OK : bfp8_plan_quantize(plan, stream);
     return rc ? rc : bfp8_plan_run_gemv(plan, stream);
 }
 

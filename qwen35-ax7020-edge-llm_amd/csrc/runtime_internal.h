@@ -115,6 +115,7 @@ struct RtLinearAttnArgs {
 #define RT_ROWS_NORM 1       // rmsnorm(h + res) with weight w, eps
 #define RT_ROWS_SWIGLU 2     // swiglu(gate, up)
 #define RT_ROWS_GATED 3      // rmsnorm_gated(attn, z) over 16 heads of 128 with weight w, eps (silu(z) given)
+#define RT_ROWS_FLOAT 4      // x given as floats, quantized here (K / 64 whole blocks)
 #define RT_ROWS_MAX_K 4096
 struct RtRowsGemv {
     const uint8_t* mant;  // GPU planes (bfp8_layout.h)
@@ -141,6 +142,9 @@ struct RtRowsArgs {
     const float* up;
     const float* attn;       // RT_ROWS_GATED (with w, eps)
     const float* zsilu;      // silu(z), elementwise
+    const float* x;          // RT_ROWS_FLOAT
+    uint32_t* xsplit_out;    // optional (RT_ROWS_FLOAT): workgroup 0 also writes the
+    float* xscale_out;       // activation's records here, for a later tail-row launch
 };
 hipError_t rt_launch_rows(const RtRowsArgs& a, hipStream_t s);
 
