@@ -39,7 +39,7 @@ constexpr int kMaxNb = RT_ROWS_MAX_K / 64;    // blocks per row
 struct RowsLds {
     __attribute__((aligned(16))) uint32_t xs[kMaxNb * 32];  // split activation records
     float xsc[kMaxNb];                                       // block scales
-    float terms[kMaxNb][64];                                 // t2 per block and lane
+    float terms[kMaxNb][128];                                // t2 per block and (sub-tile, lane)
     __attribute__((aligned(16))) float sq[4][kChunk / 4 + 4];  // rmsnorm's squares, one row per residue
     float gp[RT_HEADS][4][36];  // the gated norm's per-head products (16-byte rows)
     float gr[RT_HEADS];         // ... and per-head scales
@@ -218,31 +218,37 @@ __device__ __forceinline__ void float_prologue(const RtRowsArgs& a, const Prolog
 
 }  // namespace
 
-template <int kMode, int kPer>
+// kSub 16-row sub-tiles per workgroup (1, or 2 when a launch would otherwise
+// put more than one workgroup on a CU): the sub-tiles share the prologue.
+template <int kMode, int kPer, int kSub>
 __global__ __launch_bounds__(kThreads) void rt_rows_gemv_kernel(RtRowsArgs a) {
     __shared__ RowsLds L;
     const int w = __builtin_amdgcn_readfirstlane(wave_id());
     const int lane = lane_id();
     const bool second = a.ngemv > 1 && (int)blockIdx.x >= a.split;
     const RtRowsGemv G = second ? a.g[1] : a.g[0];
-    const int s = (int)blockIdx.x - (second ? a.split : 0);
-    const int t = s >> 2, g = s & 3;
+    const int s0 = ((int)blockIdx.x - (second ? a.split : 0)) * kSub;  // first sub-tile (one 64-row tile holds all)
+    const int t = s0 >> 2, g0 = s0 & 3;
     const int nb = a.K >> 6, nb4 = (nb + 3) >> 2;
-    const int q = lane >> 4, r = g * 16 + (lane & 15);
+    const int q = lane >> 4;
 
     // 0. the activation's inputs, then 1. this wavefront's weight blocks
-    // b = w, w + kWaves, ... all in flight
+    // b = w, w + kWaves, ... of every sub-tile, all in flight
     PrologueIn<kPer> in;
     load_prologue<kMode, kPer>(a, in);
     const __amdgpu_buffer_rsrc_t wrs = make_rsrc(G.mant + (size_t)t * nb * 4096u, (uint32_t)nb * 4096u);
     const __amdgpu_buffer_rsrc_t ers = make_rsrc(G.exps + (size_t)t * nb4 * 256u, (uint32_t)nb4 * 256u);
-    u32x4 wv[kPer];
-    uint32_t ev[kPer];
+    u32x4 wv[kSub][kPer];
+    uint32_t ev[kSub][kPer];
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-        const int b = min(w + kWaves * i, nb - 1);
-        wv[i] = load_w(wrs, q * 1024 + r * 16, b * 4096);
-        ev[i] = load_e(ers, r * 4, (b >> 2) * 256);
+    for (int j = 0; j < kSub; ++j) {
+        const int r = (g0 + j) * 16 + (lane & 15);
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int b = min(w + kWaves * i, nb - 1);
+            wv[j][i] = load_w(wrs, q * 1024 + r * 16, b * 4096);
+            ev[j][i] = load_e(ers, r * 4, (b >> 2) * 256);
+        }
     }
 
     // 2. the activation, quantized, into LDS
@@ -281,39 +287,45 @@ __global__ __launch_bounds__(kThreads) void rt_rows_gemv_kernel(RtRowsArgs a) {
         if (b < nb) {
             const uint4 xh = *reinterpret_cast<const uint4*>(&L.xs[(b * 4 + q) * 8]);
             const uint4 xl = *reinterpret_cast<const uint4*>(&L.xs[(b * 4 + q) * 8 + 4]);
-            const u32x4 wq = wv[i];
-            int S = __builtin_amdgcn_sdot4((int)wq.x, (int)xh.x, 0, false);
-            S = __builtin_amdgcn_sdot4((int)wq.y, (int)xh.y, S, false);
-            S = __builtin_amdgcn_sdot4((int)wq.z, (int)xh.z, S, false);
-            S = __builtin_amdgcn_sdot4((int)wq.w, (int)xh.w, S, false);
-            S = (int)((uint32_t)S << 8);
-            S = __builtin_amdgcn_sdot4((int)wq.x, (int)xl.x, S, false);
-            S = __builtin_amdgcn_sdot4((int)wq.y, (int)xl.y, S, false);
-            S = __builtin_amdgcn_sdot4((int)wq.z, (int)xl.z, S, false);
-            S = __builtin_amdgcn_sdot4((int)wq.w, (int)xl.w, S, false);
-            const uint32_t e = (ev[i] >> (8 * (b & 3))) & 0xffu;
-            const float t1 = (float)S * exp_scale_ftz(e);
-            L.terms[b][lane] = t1 * L.xsc[b];
+            const float xsb = L.xsc[b];
+#pragma unroll
+            for (int j = 0; j < kSub; ++j) {
+                const u32x4 wq = wv[j][i];
+                int S = __builtin_amdgcn_sdot4((int)wq.x, (int)xh.x, 0, false);
+                S = __builtin_amdgcn_sdot4((int)wq.y, (int)xh.y, S, false);
+                S = __builtin_amdgcn_sdot4((int)wq.z, (int)xh.z, S, false);
+                S = __builtin_amdgcn_sdot4((int)wq.w, (int)xh.w, S, false);
+                S = (int)((uint32_t)S << 8);
+                S = __builtin_amdgcn_sdot4((int)wq.x, (int)xl.x, S, false);
+                S = __builtin_amdgcn_sdot4((int)wq.y, (int)xl.y, S, false);
+                S = __builtin_amdgcn_sdot4((int)wq.z, (int)xl.z, S, false);
+                S = __builtin_amdgcn_sdot4((int)wq.w, (int)xl.w, S, false);
+                const uint32_t e = (ev[j][i] >> (8 * (b & 3))) & 0xffu;
+                const float t1 = (float)S * exp_scale_ftz(e);
+                L.terms[b][j * 64 + lane] = t1 * xsb;
+            }
         }
     }
     __syncthreads();
 
-    // 4. block-order sums per (row, q), then the reference's lane combination
-    if (w == 0) {
+    // 4. block-order sums per (row, q) -- wavefront j for sub-tile j -- then
+    // the reference's lane combination
+    if (w < kSub) {
         float fs = 0.0f;
         int b = 0;
+        const int c = w * 64 + lane;
         for (; b + 8 <= nb; b += 8) {
             float v[8];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) v[k] = L.terms[b + k][lane];
+            for (int k = 0; k < 8; ++k) v[k] = L.terms[b + k][c];
 #pragma unroll
             for (int k = 0; k < 8; ++k) fs = fs + v[k];
         }
-        for (; b < nb; ++b) fs = fs + L.terms[b][lane];
+        for (; b < nb; ++b) fs = fs + L.terms[b][c];
         const int rr = lane & 15;
         const float f0 = __shfl(fs, rr, 64), f1 = __shfl(fs, 16 + rr, 64);
         const float f2 = __shfl(fs, 32 + rr, 64), f3 = __shfl(fs, 48 + rr, 64);
-        const int row = t * 64 + g * 16 + lane;
+        const int row = t * 64 + (g0 + w) * 16 + lane;
         if (lane < 16 && row < G.pair_rows) G.y[row] = (f0 + f2) + (f1 + f3);
     }
 }
@@ -327,10 +339,19 @@ hipError_t rt_launch_rows(const RtRowsArgs& a, hipStream_t s) {
     if (a.mode == RT_ROWS_GATED && a.K != RT_HEADS * RT_HEAD_DIM) return hipErrorInvalidValue;
     const int n0 = (a.g[0].M + 15) / 16, n1 = a.ngemv > 1 ? (a.g[1].M + 15) / 16 : 0;
     if (a.ngemv > 1 && a.split != n0) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)(n0 + n1)), block(kThreads);
+    // more 16-row workgroups than CUs: two sub-tiles per workgroup, one
+    // workgroup per CU (a second one per CU finishes later)
+    const int sub = (n0 + n1 > bfp8_stream_grid() / 4) ? 2 : 1;
+    RtRowsArgs b = a;
+    b.split = (a.g[0].M + 16 * sub - 1) / (16 * sub);
+    const int n1s = a.ngemv > 1 ? (a.g[1].M + 16 * sub - 1) / (16 * sub) : 0;
+    const dim3 grid((unsigned)(b.split + n1s)), block(kThreads);
     const int per = (a.K + 1023) / 1024;
-#define RT_ROWS_CASE(MODE, PER) \
-    if (a.mode == MODE && per == PER) hipLaunchKernelGGL((rt_rows_gemv_kernel<MODE, PER>), grid, block, 0, s, a)
+#define RT_ROWS_CASE(MODE, PER)                                                                                \
+    if (a.mode == MODE && per == PER && sub == 1)                                                              \
+        hipLaunchKernelGGL((rt_rows_gemv_kernel<MODE, PER, 1>), grid, block, 0, s, b);                         \
+    else if (a.mode == MODE && per == PER && sub == 2)                                                         \
+        hipLaunchKernelGGL((rt_rows_gemv_kernel<MODE, PER, 2>), grid, block, 0, s, b)
     RT_ROWS_CASE(RT_ROWS_NORM, 1);
     else RT_ROWS_CASE(RT_ROWS_NORM, 2);
     else RT_ROWS_CASE(RT_ROWS_NORM, 3);

@@ -396,14 +396,17 @@ def test_small_plan_one_tile_per_workgroup(gpu, torch_mod):
     plan.close()
 
 
-@pytest.mark.parametrize("case", ["one", "one_ragged_odd", "pair_shared_x"])
+@pytest.mark.parametrize("case", ["one", "one_ragged_odd", "pair_shared_x", "pair_ragged_odd"])
 def test_plan_rows_kernel_paths(gpu, torch_mod, case):
     """Plans of one GEMV, or of two reading the same activation, run on the
-    16-row kernel (quantized activation): odd M adds the tail-row kernel, a
-    ragged K uses its K / 64 whole blocks."""
+    16-row kernel, which quantizes the activation itself: odd M adds the
+    tail-row kernel (reading the records the launch left), a ragged K uses its
+    K / 64 whole blocks, and more 16-row workgroups than CUs put two sub-tiles
+    in each workgroup (the pairs; the ragged pair ends in a half-used one)."""
     qk, torch = gpu, torch_mod
     shapes = {"one": [(3584, 1024)], "one_ragged_odd": [(1023, 1000)],
-              "pair_shared_x": [(3584, 1024), (3584, 1024)]}[case]
+              "pair_shared_x": [(3584, 1024), (3584, 1024)],
+              "pair_ragged_odd": [(4001, 1000), (4001, 1000)]}[case]
     K = shapes[0][1]
     x = qk.synth_normal(K, 5150)
     xd = torch.from_numpy(x).cuda()
