@@ -35,6 +35,7 @@ from __future__ import annotations
 import argparse
 import ctypes
 import json
+import mmap
 import os
 import re
 import sys
@@ -151,6 +152,8 @@ def main():
                     choices=["sweep", "layers", "lm_head", "lm_head_plain", "gemv", "down", "batch16", "lm_head_bf16",
                              "forward_token"])
     ap.add_argument("--rotate-gb", type=float, default=1.0, help="rotating weight copies totalling >= this")
+    ap.add_argument("--bf16-layout", choices=["tiles", "rows"], default="tiles",
+                    help="lm_head_bf16: the library's cached tile layout or a row-major device table")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -342,16 +345,27 @@ def bench_batch16(args, qk, torch, np):
 
 def bench_lm_head_bf16(args, qk, torch, np):
     """The reference's own lm_head: bf16 tied embedding 65536 x 1024 (134 MB)
-    with the fused top-64 (the chat sampler's k), rotating table copies."""
+    with the fused top-64 (the chat sampler's k), rotating table copies.
+    --bf16-layout tiles (default): the 64-row tile layout the library keeps
+    its cached tables in (lm_head_argmax / lm_head_topk / forward_token_c on
+    the engine's read-only image), converted once before timing; rows: a
+    caller's row-major device table (bf16_dev_lm_head)."""
     V, H, K = 65536, 1024, 64
     lib = qk.load()
+    tiled = args.bf16_layout == "tiles"
     per_copy = V * H * 2
     copies = max(1, int(np.ceil(args.rotate_gb * 1e9 / per_copy)))
     tables = []
     for c in range(copies):
         g = torch.Generator(device="cuda").manual_seed(100 + c)
-        t = (torch.randn((V, H), device="cuda", generator=g) * 0.05).to(torch.bfloat16)
-        tables.append(t.view(torch.int16))
+        t = (torch.randn((V, H), device="cuda", generator=g) * 0.05).to(torch.bfloat16).view(torch.int16)
+        if tiled:
+            tt = torch.empty(lib.bf16_dev_tiles_bytes(V, H) // 2, dtype=torch.int16, device="cuda")
+            qk.check(lib.bf16_dev_tile_table(tt.data_ptr(), t.data_ptr(), V, H, None))
+            torch.cuda.synchronize()
+            del t
+            t = tt
+        tables.append(t)
     h = torch.randn(H, device="cuda", dtype=torch.float32)
     ids = torch.empty(K, dtype=torch.int32, device="cuda")
     sc = torch.empty(K, dtype=torch.float32, device="cuda")
@@ -359,9 +373,17 @@ def bench_lm_head_bf16(args, qk, torch, np):
     stream = torch.cuda.current_stream()
     s = stream.cuda_stream
 
+    def head(i, k, logits):
+        if tiled:
+            return lib.bf16_dev_lm_head_tiles(ids.data_ptr() if k else None, sc.data_ptr() if k else None,
+                                              cnt.data_ptr() if k else None, cnt.data_ptr() + 4 if k else None,
+                                              logits, h.data_ptr(), tables[i % copies].data_ptr(), V, H, k, s)
+        return lib.bf16_dev_lm_head(ids.data_ptr() if k else None, sc.data_ptr() if k else None,
+                                    cnt.data_ptr() if k else None, cnt.data_ptr() + 4 if k else None, logits,
+                                    h.data_ptr(), tables[i % copies].data_ptr(), V, H, k, 1, s)
+
     def run(i, k):
-        qk.check(lib.bf16_dev_lm_head(ids.data_ptr(), sc.data_ptr(), cnt.data_ptr(), cnt.data_ptr() + 4, None,
-                                      h.data_ptr(), tables[i % copies].data_ptr(), V, H, k, 1, s))
+        qk.check(head(i, k, None))
 
     for i in range(args.warmup):
         run(i, K)
@@ -376,8 +398,7 @@ def bench_lm_head_bf16(args, qk, torch, np):
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record(stream)
     for i in range(args.steps):
-        qk.check(lib.bf16_dev_lm_head(None, None, None, None, logits.data_ptr(), h.data_ptr(),
-                                      tables[i % copies].data_ptr(), V, H, 0, 1, s))
+        qk.check(head(i, 0, logits.data_ptr()))
     b.record(stream)
     torch.cuda.synchronize()
     kus = a.elapsed_time(b) * 1e3 / args.steps
@@ -387,8 +408,9 @@ def bench_lm_head_bf16(args, qk, torch, np):
                       "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
                       "us_per_step": round(us, 2), "higher_is_better": True,
                       "config": {"workload": "lm_head_bf16", "vocab": V, "hidden": H, "topk": K,
-                                 "rotating_copies": copies},
-                      "kernel": {"name": "bf16_lm_head_kernel", "avg_us": round(kus, 2), "algorithmic_bytes": kbytes},
+                                 "layout": args.bf16_layout, "rotating_copies": copies},
+                      "kernel": {"name": "bf16_lm_head_tiles_kernel" if tiled else "bf16_lm_head_kernel",
+                                 "avg_us": round(kus, 2), "algorithmic_bytes": kbytes},
                       "roofline": {"bound": "hbm", "achieved": round(kbytes / kus / 1e3, 1), "peak": PEAK_HBM_GBPS,
                                    "unit": "GB/s", "frac": round(kbytes / kus / 1e3 / PEAK_HBM_GBPS, 4)}}), flush=True)
 
@@ -457,9 +479,18 @@ class _SynthModel:
             self.state_bytes += 4 * (3 * 6144 + 16 * 128 * 128)
             planes(p, ("qkv", "z", "o", "gate", "up", "down"))
         self.final_w = vec(1024, 0.1)
-        # bf16 table: random sign, exponent 119..123, random 7-bit mantissa
+        # bf16 table: random sign, exponent 119..123, random 7-bit mantissa,
+        # in read-only pages like the engine's mmap of its weight image
+        # (04/qwen_real_engine.py:745-751), which the library caches on the
+        # device in the lm_head's tile layout
         u = rng.integers(0, 2 ** 16, size=65536 * 1024, dtype=np.uint16)
-        self.embed = arr((u & 0x807F) | ((119 + (u >> 7) % 5).astype(np.uint16) << 7))
+        self._embed_map = mmap.mmap(-1, u.nbytes)
+        self.embed = np.frombuffer(self._embed_map, dtype=np.uint16)
+        self.embed[:] = (u & 0x807F) | ((119 + (u >> 7) % 5).astype(np.uint16) << 7)
+        libc = ctypes.CDLL(None)
+        libc.mprotect.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+        if libc.mprotect(self.embed.ctypes.data, u.nbytes, mmap.PROT_READ) != 0:
+            raise OSError("mprotect of the embedding table failed")
         self.h = arr(np.zeros(1024, dtype=np.float32))
 
     def token_bytes(self):

@@ -280,6 +280,24 @@ int bf16_dev_lm_head(int* out_ids, float* out_scores, int* out_count, int* out_a
                      const float* h, const uint16_t* embed_table, int vocab, int hidden, int k, int tail,
                      void* stream);
 
+/* The same lm_head over the table in its tile layout, which the library's
+ * own cached tables use (lm_head_argmax, lm_head_topk, forward_token_c,
+ * qwen_weights_preload) and which streams the table with one contiguous
+ * 2 KiB run per wavefront step and 16 rows per wavefront: rows in groups of
+ * 16, nT = 4 * ceil(vocab / 64) groups (rows past vocab zero); element
+ * e = 8c + j of row 16T + r, with c = 4q + cc, q = 2p + s and j = 4 hi + g,
+ * at uint16 offset (((p * nT + T) * 2 + s) * 64 + 4r + g) * 8 + 2 cc + hi.
+ * The model's width only: hidden == 1024.  No counterpart in the reference (its table is
+ * row-major in host memory).
+ * bf16_dev_tiles_bytes: bytes of the layout (0: width not supported);
+ * bf16_dev_tile_table: row-major device table -> tile layout (distinct
+ * buffers); bf16_dev_lm_head_tiles: bf16_dev_lm_head's results (no tail:
+ * hidden % 8 == 0) from the tile layout. */
+size_t bf16_dev_tiles_bytes(int vocab, int hidden);
+int bf16_dev_tile_table(uint16_t* tiles, const uint16_t* embed_table, int vocab, int hidden, void* stream);
+int bf16_dev_lm_head_tiles(int* out_ids, float* out_scores, int* out_count, int* out_argmax, float* logits,
+                           const float* h, const uint16_t* tiles, int vocab, int hidden, int k, void* stream);
+
 /* sample_from_topk (04/qwen_sampling.c:384-529) on the device: candidates
  * ids[]/scores[] (count from *count when count is not NULL, else n; n is the
  * capacity, at most 4096), xorshift32 state *rng_state updated in place

@@ -53,6 +53,7 @@ struct Bf16HeadDesc {
     int vocab, hidden;
     int topk;               // 0: scores only
     int tail;               // 1: add the hidden % 8 trailing elements (lm_head_topk)
+    int tiled;              // 1: table in the 64-row tile layout (bf16_launch_tile_table)
 };
 
 // The sampler over a sorted candidate list (bfp8_ieee.hip).
@@ -124,6 +125,14 @@ hipError_t bfp8_launch_gemv_batch(float* Y, const uint32_t* xsplit, const float*
 
 // ---- bf16_head.hip --------------------------------------------------------
 hipError_t bf16_launch_lm_head(const Bf16HeadDesc& d, hipStream_t s);
+// The lm_head's tile layout of a bf16 table [vocab][hidden] (bf16_tiled_ok:
+// the model's hidden 1024): rows in groups of 16, nT = 4 * ceil(vocab / 64)
+// groups (rows past vocab zero); element e = 8c + j of row 16T + r, with
+// c = 4q + cc, q = 2p + s and j = 4 hi + g, at uint16 offset
+// (((p * nT + T) * 2 + s) * 64 + 4r + g) * 8 + 2 cc + hi.
+bool bf16_tiled_ok(int hidden);
+size_t bf16_tiled_elems(int vocab, int hidden);
+hipError_t bf16_launch_tile_table(uint16_t* dst, const uint16_t* src, int vocab, int hidden, hipStream_t s);
 
 // ---- bfp8_ieee.hip -------------------------------------------------------
 hipError_t bfp8_launch_sample(const Bfp8SampleArgs& a, hipStream_t s);

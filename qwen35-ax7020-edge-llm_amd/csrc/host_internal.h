@@ -76,6 +76,13 @@ struct DevBuf {
     }
 };
 
+// A cached bf16 table: row-major, or the 64-row tile layout of
+// bf16_launch_tile_table (tiled) when the lm_head's tile kernel takes its width.
+struct Bf16Table {
+    DevBuf buf;
+    int tiled = 0;
+};
+
 struct PinnedBuf {
     void* p = nullptr;
     size_t n = 0;
@@ -112,7 +119,7 @@ struct State {
     DevBuf rt_dev;                              // runtime host-call arena (device)
     PinnedBuf rt_pin;                           // runtime host-call arena (pinned)
     std::map<WeightKey, CachedWeights> cache;
-    std::map<WeightKey, DevBuf> bf16_cache;     // read-only bf16 embedding tables
+    std::map<WeightKey, Bf16Table> bf16_cache;  // read-only bf16 embedding tables
     size_t cache_bytes = 0;
 };
 
@@ -136,14 +143,17 @@ int weights_for(const int8_t* mant, const uint8_t* exps, int M, int K, DevWeight
 // The same, cached whatever the memory's protection (force: the caller
 // declares the planes immutable until bfp8_cache_clear()).
 int weights_cached(const int8_t* mant, const uint8_t* exps, int M, int K, bool force, DevWeights* out);
-// Device copy of a host bf16 table [vocab][hidden] (cached when read-only or forced).
-int bf16_table_for(const uint16_t* table, int vocab, int hidden, const uint16_t** out);
-int bf16_table_cached(const uint16_t* table, int vocab, int hidden, bool force, const uint16_t** out);
+// Device copy of a host bf16 table [vocab][hidden] (cached when read-only or
+// forced; a cached copy is kept in the tile layout when bf16_tiled_ok(hidden),
+// and *tiled says which layout *out has).
+int bf16_table_for(const uint16_t* table, int vocab, int hidden, const uint16_t** out, int* tiled);
+int bf16_table_cached(const uint16_t* table, int vocab, int hidden, bool force, const uint16_t** out, int* tiled);
 // Pre-loads a float parameter the forward reads (host address, bytes); g.mu held.
 int forward_preload_param(const void* p, size_t bytes);
 // bf16 lm_head scores (+ fused top-k) on device buffers.
+// tiled: the table is in the tile layout (then tail is moot: hidden % 8 == 0).
 int bf16_lm_head_dev(int* ids, float* scores, int* count, int* argmax, float* logits, const float* h,
-                     const uint16_t* table, int vocab, int hidden, int k, int tail, hipStream_t s);
+                     const uint16_t* table, int tiled, int vocab, int hidden, int k, int tail, hipStream_t s);
 Bfp8GemvDesc plain_desc(float* y, const uint32_t* xsplit, const float* xscale, const uint8_t* m,
                         const uint8_t* e, int M, int K, int32_t* lanes);
 

@@ -154,35 +154,55 @@ int upload_x(const float* x, size_t nfloat);
 
 // Device copy of a host bf16 table [vocab][hidden]: cached when it lives in
 // read-only memory (the engine's mmap) or when forced, else uploaded per call.
-int bf16_table_cached(const uint16_t* table, int vocab, int hidden, bool force, const uint16_t** out) {
+// A cached table whose width the tile kernel takes is converted once, on the
+// device, into the tile layout (the row-major upload goes through bf16_ws).
+int bf16_table_cached(const uint16_t* table, int vocab, int hidden, bool force, const uint16_t** out, int* tiled) {
     const size_t bytes = (size_t)vocab * (size_t)hidden * 2;
     const WeightKey key{table, nullptr, vocab, hidden};
     auto it = g.bf16_cache.find(key);
     if (it != g.bf16_cache.end()) {
-        *out = it->second.as<uint16_t>();
+        *out = it->second.buf.as<uint16_t>();
+        *tiled = it->second.tiled;
         return BFP8_OK;
     }
-    const bool cacheable = g.cache_bytes + bytes <= kCacheLimit && (force || range_readonly(table, bytes));
-    DevBuf fresh;
-    DevBuf* d = cacheable ? &fresh : &g.bf16_ws;
+    const bool tile = bf16_tiled_ok(hidden);
+    const size_t kept = tile ? bf16_tiled_elems(vocab, hidden) * 2 : bytes;
+    const bool cacheable = g.cache_bytes + kept <= kCacheLimit && (force || range_readonly(table, bytes));
     int rc;
-    if ((rc = d->reserve(bytes))) return rc;
-    HIP_OK(hipMemcpyAsync(d->p, table, bytes, hipMemcpyHostToDevice, g.stream));
-    *out = d->as<uint16_t>();
-    if (cacheable) {
-        g.cache_bytes += fresh.n;
-        g.bf16_cache.emplace(key, fresh);
+    if (!cacheable) {
+        if ((rc = g.bf16_ws.reserve(bytes))) return rc;
+        HIP_OK(hipMemcpyAsync(g.bf16_ws.p, table, bytes, hipMemcpyHostToDevice, g.stream));
+        *out = g.bf16_ws.as<uint16_t>();
+        *tiled = 0;
+        return BFP8_OK;
     }
+    Bf16Table fresh;
+    if ((rc = fresh.buf.reserve(kept))) return rc;
+    if (tile) {
+        if ((rc = g.bf16_ws.reserve(bytes))) {
+            fresh.buf.release();
+            return rc;
+        }
+        HIP_OK(hipMemcpyAsync(g.bf16_ws.p, table, bytes, hipMemcpyHostToDevice, g.stream));
+        HIP_OK(bf16_launch_tile_table(fresh.buf.as<uint16_t>(), g.bf16_ws.as<uint16_t>(), vocab, hidden, g.stream));
+        fresh.tiled = 1;
+    } else {
+        HIP_OK(hipMemcpyAsync(fresh.buf.p, table, bytes, hipMemcpyHostToDevice, g.stream));
+    }
+    *out = fresh.buf.as<uint16_t>();
+    *tiled = fresh.tiled;
+    g.cache_bytes += fresh.buf.n;
+    g.bf16_cache.emplace(key, fresh);
     return BFP8_OK;
 }
 
-int bf16_table_for(const uint16_t* table, int vocab, int hidden, const uint16_t** out) {
-    return bf16_table_cached(table, vocab, hidden, false, out);
+int bf16_table_for(const uint16_t* table, int vocab, int hidden, const uint16_t** out, int* tiled) {
+    return bf16_table_cached(table, vocab, hidden, false, out, tiled);
 }
 
 // bf16 lm_head scores (+ fused top-k) on device buffers.
 int bf16_lm_head_dev(int* ids, float* scores, int* count, int* argmax, float* logits, const float* h,
-                     const uint16_t* table, int vocab, int hidden, int k, int tail, hipStream_t s) {
+                     const uint16_t* table, int tiled, int vocab, int hidden, int k, int tail, hipStream_t s) {
     const int kk = k > 0 ? std::min(k, vocab) : 0;
     int rc;
     if (kk > 0 && (rc = g.tk_partials.reserve((size_t)bfp8_ntiles(vocab) * kk * 8))) return rc;
@@ -195,6 +215,7 @@ int bf16_lm_head_dev(int* ids, float* scores, int* count, int* argmax, float* lo
     d.hidden = hidden;
     d.topk = kk;
     d.tail = tail;
+    d.tiled = tiled;
     HIP_OK(bf16_launch_lm_head(d, s));
     if (kk > 0) {
         Bfp8GemvDesc md{};
@@ -216,15 +237,16 @@ int host_bf16_lm_head(const float* h, const uint16_t* table, int vocab, int hidd
                       int* out_ids, float* out_scores, int* am) {
     int rc;
     const uint16_t* tdev;
-    if ((rc = bf16_table_for(table, vocab, hidden, &tdev)) || (rc = upload_x(h, (size_t)hidden))) return rc;
+    int tiled = 0;
+    if ((rc = bf16_table_for(table, vocab, hidden, &tdev, &tiled)) || (rc = upload_x(h, (size_t)hidden))) return rc;
     const int kk = std::min(k, vocab);
     if ((rc = g.tk_out.reserve((size_t)(2 * BFP8_TOPK_MAX + 2) * 4)) || (rc = g.h_out.reserve((size_t)(2 * BFP8_TOPK_MAX + 2) * 4)))
         return rc;
     int* d_ids = g.tk_out.as<int>();
     float* d_sc = reinterpret_cast<float*>(d_ids + BFP8_TOPK_MAX);
     int* d_cnt = d_ids + 2 * BFP8_TOPK_MAX;
-    if ((rc = bf16_lm_head_dev(d_ids, d_sc, d_cnt, d_cnt + 1, nullptr, g.x.as<float>(), tdev, vocab, hidden, kk, tail,
-                               g.stream)))
+    if ((rc = bf16_lm_head_dev(d_ids, d_sc, d_cnt, d_cnt + 1, nullptr, g.x.as<float>(), tdev, tiled, vocab, hidden,
+                               kk, tail, g.stream)))
         return rc;
     HIP_OK(hipMemcpyAsync(g.h_out.p, g.tk_out.p, (size_t)(2 * BFP8_TOPK_MAX + 2) * 4, hipMemcpyDeviceToHost, g.stream));
     HIP_OK(hipStreamSynchronize(g.stream));
@@ -582,7 +604,7 @@ void bfp8_cache_clear(void) {
     if (g.ready) (void)hipStreamSynchronize(g.stream);
     forward_cache_clear();
     weights_index_clear();
-    for (auto& kv : g.bf16_cache) kv.second.release();
+    for (auto& kv : g.bf16_cache) kv.second.buf.release();
     g.bf16_cache.clear();
     for (auto& kv : g.cache) {
         kv.second.mant.release();
@@ -753,8 +775,35 @@ int bf16_dev_lm_head(int* out_ids, float* out_scores, int* out_count, int* out_a
         set_error("bf16_dev_lm_head: invalid arguments");
         return BFP8_EINVAL;
     }
-    return bf16_lm_head_dev(out_ids, out_scores, out_count, out_argmax, logits, h, table, vocab, hidden, k,
+    return bf16_lm_head_dev(out_ids, out_scores, out_count, out_argmax, logits, h, table, 0, vocab, hidden, k,
                             tail ? 1 : 0, pick_stream(stream));
+}
+
+size_t bf16_dev_tiles_bytes(int vocab, int hidden) {
+    if (vocab <= 0 || !bf16_tiled_ok(hidden)) return 0;
+    return bf16_tiled_elems(vocab, hidden) * 2;
+}
+
+int bf16_dev_tile_table(uint16_t* tiles, const uint16_t* table, int vocab, int hidden, void* stream) {
+    DEV_PROLOGUE();
+    if (!tiles || !table || vocab <= 0 || !bf16_tiled_ok(hidden)) {
+        set_error("bf16_dev_tile_table: invalid arguments (hidden must be 1024)");
+        return BFP8_EINVAL;
+    }
+    HIP_OK(bf16_launch_tile_table(tiles, table, vocab, hidden, pick_stream(stream)));
+    return BFP8_OK;
+}
+
+int bf16_dev_lm_head_tiles(int* out_ids, float* out_scores, int* out_count, int* out_argmax, float* logits,
+                           const float* h, const uint16_t* tiles, int vocab, int hidden, int k, void* stream) {
+    DEV_PROLOGUE();
+    if (!h || !tiles || vocab <= 0 || !bf16_tiled_ok(hidden) || k < 0 || std::min(k, vocab) > BFP8_TOPK_MAX ||
+        (k > 0 && (!out_ids || !out_scores || !out_count || !out_argmax)) || (k == 0 && !logits)) {
+        set_error("bf16_dev_lm_head_tiles: invalid arguments");
+        return BFP8_EINVAL;
+    }
+    return bf16_lm_head_dev(out_ids, out_scores, out_count, out_argmax, logits, h, tiles, 1, vocab, hidden, k, 0,
+                            pick_stream(stream));
 }
 
 int bfp8_dev_sample_from_topk(int* out_id, const int* ids, const float* scores, const int* count, int n,

@@ -778,8 +778,9 @@ int forward_token_c(int token_id, float* h, const LinearLayerPlan* linear_plans,
     const uint16_t* table = nullptr;
     const size_t tbytes = (size_t)kVocab * kHidden * 2;
     RT_CHECK("forward_token_c", fwd_vec(final_norm_w, kHidden, &fnorm));
+    int tiled = 0;  // the cached table's layout
     if (range_readonly(embed_table, tbytes)) {
-        RT_CHECK("forward_token_c", bf16_table_for(embed_table, kVocab, kHidden, &table));
+        RT_CHECK("forward_token_c", bf16_table_for(embed_table, kVocab, kHidden, &table, &tiled));
     } else {
         RT_CHECK("forward_token_c", fwd_vec(embed_table, (size_t)kVocab * kHidden, &table));
     }
@@ -790,7 +791,7 @@ int forward_token_c(int token_id, float* h, const LinearLayerPlan* linear_plans,
         Step s(QP_EMBED);
         int row = token_id % kVocab;
         if (row < 0) row += kVocab;
-        if (rt_launch_embed(hd, table, row, kHidden, g.stream) != hipSuccess) {
+        if (rt_launch_embed(hd, table, tiled ? bfp8_ntiles(kVocab) : 0, row, kHidden, g.stream) != hipSuccess) {
             set_error("embedding launch failed");
             fatal("forward_token_c");
         }
@@ -824,7 +825,8 @@ int forward_token_c(int token_id, float* h, const LinearLayerPlan* linear_plans,
     {
         Step s(QP_LMHEAD);
         RT_CHECK("forward_token_c", bf16_lm_head_dev(w.lm, reinterpret_cast<float*>(w.lm + 1), w.lm + 2, w.lm + 3,
-                                                     nullptr, w.normed, table, kVocab, kHidden, 1, 0, g.stream));
+                                                     nullptr, w.normed, table, tiled, kVocab, kHidden, 1, 0,
+                                                     g.stream));
         RT_CHECK("forward_token_c", s.done());
     }
     int out[4] = {0, 0, 0, 0};

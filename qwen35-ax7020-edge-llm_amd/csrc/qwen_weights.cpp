@@ -349,8 +349,9 @@ int qwen_weights_preload(const void* image, size_t image_bytes, const char* mani
             ++n;
         } else if (e.type == T_BF16 && e.shape.size() == 2 && e.shape[0] <= INT32_MAX && e.shape[1] <= INT32_MAX) {
             const uint16_t* d;
+            int tiled;
             if ((rc = bf16_table_cached(reinterpret_cast<const uint16_t*>(p), (int)e.shape[0], (int)e.shape[1], true,
-                                        &d)))
+                                        &d, &tiled)))
                 return rc;
         } else if (e.type == T_F32) {
             if ((rc = forward_preload_param(p, e.bytes))) return rc;

@@ -191,10 +191,24 @@ extern "C" __global__ __launch_bounds__(256) void rt_add_residual_kernel(float* 
 }
 
 // ---- embedding row (bf16 -> f32) --------------------------------------------------------
-extern "C" __global__ __launch_bounds__(256) void rt_embed_kernel(float* h, const uint16_t* table, int row,
+// ntiles == 0: row-major, element e of the row at row * hidden + e.  Else
+// the lm_head's tile layout over ntiles 64-row tiles (nT = 4 * ntiles groups
+// of 16 rows): element e = 8c + j of row 16T + r, c = 4q + cc, q = 2p + s,
+// j = 4 hi + g, in 16-byte slot ((p * nT + T) * 2 + s) * 64 + 4r + g, word
+// cc, half hi.
+extern "C" __global__ __launch_bounds__(256) void rt_embed_kernel(float* h, const uint16_t* table, int ntiles, int row,
                                                                   int hidden) {
     const int e = blockIdx.x * 256 + threadIdx.x;
-    if (e < hidden) h[e] = __uint_as_float((uint32_t)table[(size_t)row * hidden + e] << 16);
+    if (e >= hidden) return;
+    size_t at = (size_t)row * hidden + e;
+    if (ntiles) {
+        const int c = e >> 3, j = e & 7;
+        const int q = c >> 2;
+        const size_t slot =
+            (((size_t)(q >> 1) * (size_t)(4 * ntiles) + (size_t)(row >> 4)) * 2 + (q & 1)) * 64 + 4 * (row & 15) + (j & 3);
+        at = slot * 8 + 2 * (c & 3) + (j >> 2);
+    }
+    h[e] = __uint_as_float((uint32_t)table[at] << 16);
 }
 
 // ---- the model's linear-attention block ----------------------------------------------------
@@ -459,8 +473,9 @@ hipError_t rt_launch_linear_attn(const RtLinearAttnArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t rt_launch_embed(float* h, const uint16_t* table, int row, int hidden, hipStream_t s) {
+hipError_t rt_launch_embed(float* h, const uint16_t* table, int ntiles, int row, int hidden, hipStream_t s) {
     if (hidden <= 0) return hipSuccess;
-    hipLaunchKernelGGL(rt_embed_kernel, dim3(blocks_for(hidden)), dim3(256), 0, s, h, table, row, hidden);
+    if (ntiles && ((hidden & 31) || row >= ntiles * 64)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rt_embed_kernel, dim3(blocks_for(hidden)), dim3(256), 0, s, h, table, ntiles, row, hidden);
     return hipGetLastError();
 }

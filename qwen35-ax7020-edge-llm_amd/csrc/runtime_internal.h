@@ -158,7 +158,9 @@ hipError_t rt_launch_gated(const RtGatedArgs& a, hipStream_t s);
 hipError_t rt_launch_add_residual(float* x, const float* res, int n, hipStream_t s);
 hipError_t rt_launch_linear_attn(const RtLinearAttnArgs& a, hipStream_t s);
 // h[i] = the float whose high half is table[row*hidden + i]
-hipError_t rt_launch_embed(float* h, const uint16_t* table, int row, int hidden, hipStream_t s);
+// ntiles > 0: the table is in the 64-row tile layout over ntiles tiles
+// (bf16_launch_tile_table); 0: row-major.
+hipError_t rt_launch_embed(float* h, const uint16_t* table, int ntiles, int row, int hidden, hipStream_t s);
 
 // Largest head_dim / gate input the per-head kernels stage in LDS.
 #define RT_MAX_HEAD_DIM 4096

@@ -160,8 +160,12 @@ def bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.bfp8_dev_read_probe.argtypes = [vp, c_size_t, vp, vp]
     lib.bfp8_dev_copy_probe.argtypes = [vp, vp, c_size_t, vp]
     lib.bf16_dev_lm_head.argtypes = [vp, vp, vp, vp, vp, vp, vp, i, i, i, i, vp]
+    lib.bf16_dev_tiles_bytes.argtypes = [i, i]
+    lib.bf16_dev_tiles_bytes.restype = c_size_t
+    lib.bf16_dev_tile_table.argtypes = [vp, vp, i, i, vp]
+    lib.bf16_dev_lm_head_tiles.argtypes = [vp, vp, vp, vp, vp, vp, vp, i, i, i, vp]
     lib.bfp8_dev_sample_from_topk.argtypes = [vp, vp, vp, vp, i, c_float, i, c_float, vp, vp, vp]
-    for name in ("bf16_dev_lm_head", "bfp8_dev_sample_from_topk", "bfp8_dev_pack", "bfp8_dev_unpack", "bfp8_dev_quantize", "bfp8_dev_gemv",
+    for name in ("bf16_dev_lm_head", "bf16_dev_tile_table", "bf16_dev_lm_head_tiles", "bfp8_dev_sample_from_topk", "bfp8_dev_pack", "bfp8_dev_unpack", "bfp8_dev_quantize", "bfp8_dev_gemv",
                  "bfp8_dev_gemv_float", "bfp8_dev_gemv_batch", "bfp8_dev_lm_head_topk",
                  "bfp8_dev_synth_planes", "bfp8_dev_read_probe", "bfp8_dev_copy_probe"):
         getattr(lib, name).restype = i

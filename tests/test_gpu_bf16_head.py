@@ -6,6 +6,7 @@ the reference engine and chat front end call them; the device-level entry
 points are checked on the same inputs.  Scores are compared bit for bit with
 the oracle's restatement of the board build's dot products."""
 import ctypes
+import mmap
 import sys
 
 import numpy as np
@@ -41,6 +42,27 @@ def host_topk(qk, h, table, k):
     sc = (ctypes.c_float * max(k, 1))()
     n = smp.lm_head_topk(h.ctypes.data, table.ctypes.data, table.shape[0], table.shape[1], k, ids, sc)
     return np.array(ids[:n], dtype=np.int32), np.array(sc[:n], dtype=F32)
+
+
+def tile_layout(table):
+    """The lm_head's tile layout: rows in groups of 16, nT = 4 * ceil(vocab /
+    64) groups (rows past vocab zero); element e = 8c + j of row 16T + r, with
+    c = 4q + cc, q = 2p + s and j = 4 hi + g, at uint16 offset
+    (((p * nT + T) * 2 + s) * 64 + 4r + g) * 8 + 2 cc + hi."""
+    vocab, hidden = table.shape
+    nT = 4 * -(-vocab // 64)
+    pad = np.zeros((nT * 16, hidden), dtype=np.uint16)
+    pad[:vocab] = table
+    # e = 64p + 32s + 8cc + 4hi + g: axes (T, r, p, s, cc, hi, g) -> (p, T, s, r, g, cc, hi)
+    return pad.reshape(nT, 16, hidden // 64, 2, 4, 2, 4).transpose(2, 0, 3, 1, 6, 4, 5).reshape(-1)
+
+
+def readonly_view(path, arr):
+    """arr's bytes in a file mapped PROT_READ, as the engine maps its image."""
+    arr.tofile(path)
+    with open(path, "rb") as f:
+        mm = mmap.mmap(f.fileno(), 0, prot=mmap.PROT_READ)
+    return np.frombuffer(mm, dtype=arr.dtype).reshape(arr.shape)
 
 
 @pytest.fixture(scope="module")
@@ -179,3 +201,90 @@ def test_device_topk_then_sample_chain(gpu, head_case):
         assert int(out.item()) == want, draw
         assert int(rng_dev.cpu().numpy().view(np.uint32)[0]) == state
         assert int(cnt[1].item()) == ol.argmax(logits1)
+
+
+def test_tile_layout_and_tiled_lm_head(gpu, head_case):
+    """bf16_dev_tile_table writes the documented layout byte for byte, and the
+    tile kernel's scores, top-64 and argmax equal the oracle's bit for bit:
+    the full vocabulary, a ragged one with duplicated rows (ties), a
+    single-tile one and NaN / inf hidden states."""
+    qk = gpu
+    import torch
+
+    lib = qk.load()
+    s = torch.cuda.current_stream().cuda_stream
+    assert lib.bf16_dev_tiles_bytes(65536, 1024) == 65536 * 1024 * 2
+    assert lib.bf16_dev_tiles_bytes(1000, 1024) == 1024 * 1024 * 2
+    assert lib.bf16_dev_tiles_bytes(1000, 1000) == 0 and lib.bf16_dev_tiles_bytes(0, 1024) == 0
+    table, h, logits0, _ = head_case
+    cases = [(table, h, logits0)]
+    for vocab, seed in ((1000, 5), (64, 6), (4099, 7)):
+        t2, h2 = table_and_h(vocab, 1024, seed)
+        l2 = ol.bf16_logits(h2, t2, tail=0)
+        for src in np.argsort(-l2, kind="stable")[:8]:
+            t2[(int(src) * 7 + 3) % vocab] = t2[src]
+        cases.append((t2, h2, ol.bf16_logits(h2, t2, tail=0)))
+    hn = h.copy()
+    hn[5] = np.inf
+    cases.append((table, hn, ol.bf16_logits(hn, table, tail=0)))
+    hn = h.copy()
+    hn[700] = np.nan
+    cases.append((table, hn, ol.bf16_logits(hn, table, tail=0)))
+    for tb, hv, ref in cases:
+        vocab = tb.shape[0]
+        say("bf16 tiles", vocab, "nonfinite" if not np.all(np.isfinite(hv)) else "")
+        t = torch.from_numpy(tb.view(np.int16)).cuda()
+        tiles = torch.empty(lib.bf16_dev_tiles_bytes(vocab, 1024) // 2, dtype=torch.int16, device="cuda")
+        qk.check(lib.bf16_dev_tile_table(tiles.data_ptr(), t.data_ptr(), vocab, 1024, s))
+        hd = torch.from_numpy(hv).cuda()
+        logits = torch.empty(vocab, dtype=torch.float32, device="cuda")
+        ids = torch.empty(64, dtype=torch.int32, device="cuda")
+        sc = torch.empty(64, dtype=torch.float32, device="cuda")
+        cnt = torch.empty(2, dtype=torch.int32, device="cuda")
+        qk.check(lib.bf16_dev_lm_head_tiles(None, None, None, None, logits.data_ptr(), hd.data_ptr(),
+                                            tiles.data_ptr(), vocab, 1024, 0, s))
+        torch.cuda.synchronize()
+        assert np.array_equal(tiles.cpu().numpy().view(np.uint16), tile_layout(tb)), vocab
+        assert same_f32(logits.cpu().numpy(), ref), vocab
+        for k in (1, 64):
+            qk.check(lib.bf16_dev_lm_head_tiles(ids.data_ptr(), sc.data_ptr(), cnt.data_ptr(), cnt.data_ptr() + 4,
+                                                None, hd.data_ptr(), tiles.data_ptr(), vocab, 1024, k, s))
+            torch.cuda.synchronize()
+            r_ids, r_sc = ol.topk(ref, k)
+            n = int(cnt[0].item())
+            assert n == r_ids.size, (vocab, k)
+            assert np.array_equal(ids[:n].cpu().numpy(), r_ids) and same_f32(sc[:n].cpu().numpy(), r_sc), (vocab, k)
+            assert int(cnt[1].item()) == ol.argmax(ref), (vocab, k)
+    assert lib.bf16_dev_tile_table(tiles.data_ptr(), t.data_ptr(), 64, 1000, s) != 0
+    assert lib.bf16_dev_lm_head_tiles(None, None, None, None, logits.data_ptr(), hd.data_ptr(), tiles.data_ptr(),
+                                      64, 1000, 0, s) != 0
+
+
+def test_host_lm_head_on_a_readonly_table_uses_the_cached_tiles(gpu, head_case, tmp_path):
+    """A read-only table (the engine's PROT_READ image) is cached on the device
+    in the tile layout: lm_head_argmax / lm_head_topk keep the oracle's
+    results on the first call (conversion) and on later calls (cache hit),
+    and after bfp8_cache_clear."""
+    qk = gpu
+    lib = qk.load()
+    table, h, logits0, logits1 = head_case
+    ro = readonly_view(tmp_path / "embed.bin", table)
+    lib.bfp8_cache_clear()
+    try:
+        for rep in range(2):
+            say("read-only table host lm_head", rep)
+            assert lib.lm_head_argmax(h.ctypes.data, ro.ctypes.data, 65536, 1024) == ol.argmax(logits0)
+            for k in (1, 64):
+                ids, sc = host_topk(qk, h, ro, k)
+                r_ids, r_sc = ol.topk(logits1, k)
+                assert np.array_equal(ids, r_ids) and same_f32(sc, r_sc), (rep, k)
+        t2, h2 = table_and_h(1000, 1024, 8)
+        ro2 = readonly_view(tmp_path / "embed2.bin", t2)
+        say("read-only ragged table")
+        l2 = ol.bf16_logits(h2, t2, tail=1)
+        assert lib.lm_head_argmax(h2.ctypes.data, ro2.ctypes.data, 1000, 1024) == ol.argmax(l2)
+        ids, sc = host_topk(qk, h2, ro2, 64)
+        r_ids, r_sc = ol.topk(l2, 64)
+        assert np.array_equal(ids, r_ids) and same_f32(sc, r_sc)
+    finally:
+        lib.bfp8_cache_clear()

@@ -13,6 +13,7 @@ definition the GPU implements) and within 2 ulp of the oracle on the host C
 library.  gdn states are held in the reference's blocked layout on the GPU
 side and converted for the oracle's logical layout.  NaN compares as NaN."""
 import ctypes
+import mmap
 import sys
 
 import numpy as np
@@ -362,10 +363,11 @@ def test_forward_linear_layer_exact_fallbacks(gpu, fresh_cache):
             assert m.states_match(), step
 
 
-def test_forward_token_c_with_callback(gpu, fresh_cache):
+def test_forward_token_c_with_callback(gpu, fresh_cache, tmp_path):
     """24 layers (18 linear-attention, 6 full-attention whose attention is a
-    host callback that edits h), final norm, bf16 lm_head argmax; two tokens,
-    states carried over; the library is re-entered from the callback."""
+    host callback that edits h), final norm, bf16 lm_head argmax; four tokens,
+    states carried over, the last two with the table read-only (cached in the
+    tile layout); the library is re-entered from the callback."""
     lib = gpu.load()
     m = Model(2026)
     seen = []
@@ -387,19 +389,25 @@ def test_forward_token_c_with_callback(gpu, fresh_cache):
     rt.orc_forward_token.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                      ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, gpu.FULL_ATTN_CALLBACK,
                                      ctypes.c_void_p, ctypes.c_int]
+    # a read-only mapping of the table (the engine's PROT_READ image) is
+    # cached in the lm_head's tile layout, so the embedding row is read
+    # from that layout too
+    m.embed.tofile(tmp_path / "embed.bin")
+    with open(tmp_path / "embed.bin", "rb") as f:
+        ro = np.frombuffer(mmap.mmap(f.fileno(), 0, prot=mmap.PROT_READ), dtype=np.uint16)
     with ol.cr_libm():
-        for token in (1234, 70001):
-            say("forward_token_c", token)
+        for token, table in ((1234, m.embed), (70001, m.embed), (65535, ro), (40000, ro)):
+            say("forward_token_c", token, "read-only table" if table is ro else "")
             h = np.zeros(1024, dtype=F32)
             got = lib.forward_token_c(token, ptr(h), ctypes.addressof(m.gpu_lin), ctypes.addressof(m.gpu_mlp),
-                                      ptr(m.is_full), ptr(m.final_w), ptr(m.embed), cb_gpu, None)
+                                      ptr(m.is_full), ptr(m.final_w), ptr(table), cb_gpu, None)
             h_ref = np.zeros(1024, dtype=F32)
             want = rt.orc_forward_token(token, ptr(h_ref), ctypes.addressof(m.ref_lin), ctypes.addressof(m.ref_mlp),
-                                        ptr(m.is_full), ptr(m.final_w), ptr(m.embed), cb_ref, None, 65536)
+                                        ptr(m.is_full), ptr(m.final_w), ptr(table), cb_ref, None, 65536)
             assert got == want, token
             assert same(h, h_ref), token
             assert m.states_match(), token
-    assert seen == [3, 7, 11, 15, 19, 23] * 4
+    assert seen == [3, 7, 11, 15, 19, 23] * 8
 
 
 def test_forward_state_resident_mode(gpu, fresh_cache):
