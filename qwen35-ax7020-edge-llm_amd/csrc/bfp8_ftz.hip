@@ -524,30 +524,40 @@ __device__ __forceinline__ void quantize_task(const Bfp8QuantDesc& d, int b, flo
 }  // namespace
 
 // Every load is unconditional (indices clamped): the compiler can then count
-// them and wait for each block's weights alone.  qtasks holds at least one
-// entry (ntasks may be 0) and every workgroup has at least one tile.
+// them and wait for each block's weights alone.  A tile's blocks are issued
+// kHeadDepth ahead of the block being reduced: with 4096 wavefronts streaming,
+// 4 KiB in flight per wavefront beat the whole tile at once (13.1 against
+// 15.1 us for the 65536 x 1024 lm_head launch; 2 KiB: 13.2-13.9 us).
+constexpr int kHeadDepth = 4;
 struct HeadTile {
     u32x4 w[BFP8_HEAD_MAX_NB];
     uint32_t e[BFP8_HEAD_MAX_NB / 4];
 };
 
-__device__ __forceinline__ void head_issue(HeadTile& T, const Bfp8GemvDesc& d, int t, int nb, int q, int lane) {
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t head_wrs(const Bfp8HeadArgs& a, int t, int nb) {
+    return make_rsrc(a.mant + (size_t)t * nb * 4096u, (uint32_t)nb * 4096u);
+}
+
+__device__ __forceinline__ void head_issue(HeadTile& T, const Bfp8HeadArgs& a, int t, int nb, int q, int lane) {
     const int nb4 = (nb + 3) >> 2;
-    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(d.mant + (size_t)t * nb * 4096u, (uint32_t)nb * 4096u);
-    const __amdgpu_buffer_rsrc_t ers = make_rsrc(d.exps + (size_t)t * nb4 * 256u, (uint32_t)nb4 * 256u);
+    const __amdgpu_buffer_rsrc_t wrs = head_wrs(a, t, nb);
+    const __amdgpu_buffer_rsrc_t ers = make_rsrc(a.exps + (size_t)t * nb4 * 256u, (uint32_t)nb4 * 256u);
 #pragma unroll
-    for (int u = 0; u < BFP8_HEAD_MAX_NB; ++u) T.w[u] = load_w(wrs, q * 1024 + lane * 16, min(u, nb - 1) * 4096);
+    for (int u = 0; u < kHeadDepth; ++u) T.w[u] = load_w(wrs, q * 1024 + lane * 16, min(u, nb - 1) * 4096);
 #pragma unroll
     for (int m = 0; m < BFP8_HEAD_MAX_NB / 4; ++m) T.e[m] = load_e(ers, lane * 4, min(m, nb4 - 1) * 256);
 }
 
 // fs_q of one tile (blocks in order), then y = (fs0 + fs2) + (fs1 + fs3) and
 // the tile's top-k partial
-__device__ __forceinline__ void head_reduce(const HeadTile& T, const Bfp8GemvDesc& d, int t, int nb, int q,
-                                            int lane, uint32_t xr0, uint32_t xr1, uint32_t xsv, HeadLds& L) {
+__device__ __forceinline__ void head_reduce(HeadTile& T, const Bfp8HeadArgs& a, int t, int nb, int q, int lane,
+                                            uint32_t xr0, uint32_t xr1, uint32_t xsv, HeadLds& L) {
+    const __amdgpu_buffer_rsrc_t wrs = head_wrs(a, t, nb);
     float fs = 0.0f;
 #pragma unroll
     for (int b = 0; b < BFP8_HEAD_MAX_NB; ++b) {
+        if (b + kHeadDepth < BFP8_HEAD_MAX_NB)
+            T.w[b + kHeadDepth] = load_w(wrs, q * 1024 + lane * 16, min(b + kHeadDepth, nb - 1) * 4096);
         if (b < nb) {
             const uint32_t src = b < 8 ? xr0 : xr1;
             uint32_t x[8];
@@ -567,6 +577,7 @@ __device__ __forceinline__ void head_reduce(const HeadTile& T, const Bfp8GemvDes
             fs = epilogue(fs, S, e, __uint_as_float(__builtin_amdgcn_readlane(xsv, b)));
         }
     }
+    const Bfp8GemvDesc& d = a.descs[a.head];
     L.red[q * 64 + lane] = fs;
     __syncthreads();
     float y = 0.0f;
@@ -580,41 +591,41 @@ __device__ __forceinline__ void head_reduce(const HeadTile& T, const Bfp8GemvDes
     __syncthreads();  // L.red is reused by the next tile
 }
 
-extern "C" __global__ __launch_bounds__(256) void bfp8_gemv_head_kernel(
-    const Bfp8GemvDesc* __restrict__ descs, const Bfp8TileRef* __restrict__ tiles, const int* __restrict__ wg_off,
-    int head_desc, const float* __restrict__ hx, const Bfp8QuantDesc* __restrict__ qdescs,
-    const int2* __restrict__ qtasks, int ntasks) {
+// Loads go out in the order they are needed, and nothing but the arguments
+// stands before the weights: a table lookup there would wait behind the
+// weight streams of the workgroups already running.  The quantization task's
+// descriptor (two scalar loads) and element follow the weights, so the task
+// runs last.
+extern "C" __global__ __launch_bounds__(256) void bfp8_gemv_head_kernel(Bfp8HeadArgs a) {
     constexpr int kPerWave = BFP8_HEAD_MAX_NB / kWaves;
     __shared__ HeadLds L;
     const int q = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    const Bfp8GemvDesc& d = descs[head_desc];
-    const int nb = d.K >> 6;  // 1 .. BFP8_HEAD_MAX_NB (host-checked)
-    const int beg = wg_off[blockIdx.x], end = wg_off[blockIdx.x + 1];
+    const int nb = a.K >> 6;  // 1 .. BFP8_HEAD_MAX_NB (host-checked)
 
-    // 0. loads in the order they are needed: the lm_head activation's blocks
-    // q, q + 4, ... (one element per lane), this wavefront's first task, then
-    // the first tile's weights
+    // 0. the lm_head activation's blocks q, q + 4, ... (one element per lane),
+    // the first tile's weights, then this wavefront's task
     float hv[kPerWave];
 #pragma unroll
-    for (int k = 0; k < kPerWave; ++k) hv[k] = hx[min(q + kWaves * k, nb - 1) * 64 + lane];
-    const int wid = (int)blockIdx.x * kWaves + q, nw = (int)gridDim.x * kWaves;
-    const int2 tk = qtasks[min(wid, max(ntasks - 1, 0))];
-    const int tq = __builtin_amdgcn_readfirstlane(tk.x), tb = __builtin_amdgcn_readfirstlane(tk.y);
-    // (a global-address-space pointer: a flat load would count on both counters)
-    const float tv = ((const __attribute__((address_space(1))) float*)qdescs[tq].x)[(size_t)tb * 64 + lane];
+    for (int k = 0; k < kPerWave; ++k) hv[k] = a.hx[min(q + kWaves * k, nb - 1) * 64 + lane];
     HeadTile T;
-    int t = tiles[beg].tile;
-    head_issue(T, d, t, nb, q, lane);
+    int t = blockIdx.x;
+    head_issue(T, a, t, nb, q, lane);
+    __builtin_amdgcn_sched_barrier(0);  // the task's dependent loads stay behind every weight load
+    const int wid = (int)blockIdx.x * kWaves + q, nw = (int)gridDim.x * kWaves;
+    typedef const __attribute__((address_space(4))) int* s_int_ptr;  // scalar loads
+    const int ti = min(wid, max(a.ntasks - 1, 0));
+    const int tq = ((s_int_ptr)a.qtasks)[2 * ti], tb = ((s_int_ptr)a.qtasks)[2 * ti + 1];
+    // (a global-address-space pointer: a flat load would count on both counters)
+    const float tv = ((const __attribute__((address_space(1))) float*)a.qdescs[tq].x)[(size_t)tb * 64 + lane];
 
     // 1. the lm_head activation, quantized into LDS (slots b >= nb hold a
-    // copy of block nb - 1 and are never read); this wavefront's tasks
+    // copy of block nb - 1 and are never read)
 #pragma unroll
     for (int k = 0; k < kPerWave; ++k) {
         const int b = q + kWaves * k;
         bfp8_quant_block_lds(hv[k], lane, &L.xsc[b], &L.xs[b * 32]);
     }
-    if (wid < ntasks) quantize_task(qdescs[tq], tb, tv, lane, L.rec[q]);
     __syncthreads();
 
     // 2. residue q's split words in registers: lane l holds word l & 7 of
@@ -625,17 +636,17 @@ extern "C" __global__ __launch_bounds__(256) void bfp8_gemv_head_kernel(
     const uint32_t xsv = lane < nb ? __float_as_uint(L.xsc[lane]) : 0u;
 
     // 3. the tiles
-    head_reduce(T, d, t, nb, q, lane, xr0, xr1, xsv, L);
-    for (int i = beg + 1; i < end; ++i) {
-        t = tiles[i].tile;
-        head_issue(T, d, t, nb, q, lane);
-        head_reduce(T, d, t, nb, q, lane, xr0, xr1, xsv, L);
+    head_reduce(T, a, t, nb, q, lane, xr0, xr1, xsv, L);
+    for (t += gridDim.x; t < a.ntiles; t += gridDim.x) {
+        head_issue(T, a, t, nb, q, lane);
+        head_reduce(T, a, t, nb, q, lane, xr0, xr1, xsv, L);
     }
-    // 4. tasks beyond one per wavefront (more tasks than wavefronts)
-    for (int j = wid + nw; j < ntasks; j += nw) {
-        const int jq = __builtin_amdgcn_readfirstlane(qtasks[j].x);
-        const int jb = __builtin_amdgcn_readfirstlane(qtasks[j].y);
-        const Bfp8QuantDesc& dj = qdescs[jq];
+    // 4. the quantization tasks: this wavefront's, then those beyond one per
+    // wavefront (more tasks than wavefronts)
+    if (wid < a.ntasks) quantize_task(a.qdescs[tq], tb, tv, lane, L.rec[q]);
+    for (int j = wid + nw; j < a.ntasks; j += nw) {
+        const int jq = ((s_int_ptr)a.qtasks)[2 * j], jb = ((s_int_ptr)a.qtasks)[2 * j + 1];
+        const Bfp8QuantDesc& dj = a.qdescs[jq];
         quantize_task(dj, jb, dj.x[(size_t)jb * 64 + lane], lane, L.rec[q]);
     }
 }
@@ -856,12 +867,9 @@ hipError_t bfp8_launch_gemv_grouped(const Bfp8GemvDesc* descs_dev, const Bfp8Til
     return hipGetLastError();
 }
 
-hipError_t bfp8_launch_gemv_head(const Bfp8GemvDesc* descs_dev, const Bfp8TileRef* tiles_dev, const int* wg_off_dev,
-                                 int nwg, int head_desc, const float* hx, const Bfp8QuantDesc* qdescs_dev,
-                                 const int* qtasks_dev, int ntasks, hipStream_t s) {
-    if (nwg <= 0) return hipSuccess;
-    hipLaunchKernelGGL(bfp8_gemv_head_kernel, dim3(nwg), dim3(256), 0, s, descs_dev, tiles_dev, wg_off_dev,
-                       head_desc, hx, qdescs_dev, reinterpret_cast<const int2*>(qtasks_dev), ntasks);
+hipError_t bfp8_launch_gemv_head(const Bfp8HeadArgs& a, int nwg, hipStream_t s) {
+    if (nwg <= 0 || a.ntiles < nwg) return nwg <= 0 ? hipSuccess : hipErrorInvalidValue;
+    hipLaunchKernelGGL(bfp8_gemv_head_kernel, dim3(nwg), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

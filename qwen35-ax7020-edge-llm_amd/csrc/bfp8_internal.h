@@ -111,9 +111,20 @@ hipError_t bfp8_launch_gemv_grouped(const Bfp8GemvDesc* descs_dev, const Bfp8Til
 // BFP8_HEAD_MAX_NB, K % 64 == 0) itself, and wavefront task j quantizes block
 // qtasks[2j+1] of qdescs_dev[qtasks[2j]] into that descriptor's records.
 #define BFP8_HEAD_MAX_NB 16
-hipError_t bfp8_launch_gemv_head(const Bfp8GemvDesc* descs_dev, const Bfp8TileRef* tiles_dev, const int* wg_off_dev,
-                                 int nwg, int head_desc, const float* hx, const Bfp8QuantDesc* qdescs_dev,
-                                 const int* qtasks_dev, int ntasks, hipStream_t s);
+// The fused lm_head launch: everything its weight loads need is an argument
+// (no table lookups ahead of them); workgroup w takes tiles w, w + nwg, ...
+struct Bfp8HeadArgs {
+    const Bfp8GemvDesc* descs;    // descs[head]: the outputs (y, partials, topk, pair_rows)
+    int head;
+    const uint8_t* mant;          // the lm_head's device planes and width
+    const uint8_t* exps;
+    int K, ntiles;
+    const float* hx;              // the lm_head's activation
+    const Bfp8QuantDesc* qdescs;  // the other activations, one 64-element block per task
+    const int* qtasks;            // (qdesc, block) pairs; at least one entry even when ntasks == 0
+    int ntasks;
+};
+hipError_t bfp8_launch_gemv_head(const Bfp8HeadArgs& a, int nwg, hipStream_t s);
 // Extra load, in blocks of the byte-balanced dealing, that a folded merge
 // puts on workgroup 0 of a grouped launch.
 #define BFP8_MERGE_COST_BLOCKS 16

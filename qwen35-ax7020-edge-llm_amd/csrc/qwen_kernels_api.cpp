@@ -1067,11 +1067,21 @@ int bfp8_plan_launch(void* plan, int stage, void* stream) {
     const Bfp8GemvDesc* descs = p->descs.as<Bfp8GemvDesc>();
     const bool fold = p->topk_desc >= 0 && p->rest.nwg > 0;
     if (stage == 0) {
-        if (p->fused_head)
-            HIP_OK(bfp8_launch_gemv_head(descs, p->head.tiles.as<Bfp8TileRef>(), p->head.wg_off.as<int>(),
-                                         p->head.nwg, p->topk_desc, p->items[p->topk_desc].x,
-                                         p->qdescs.as<Bfp8QuantDesc>(), p->qtasks.as<int>(), p->ntasks, s));
-        else
+        if (p->fused_head) {
+            const Bfp8GemvDesc& hd = p->hdesc[p->topk_desc];
+            Bfp8HeadArgs a{};
+            a.descs = descs;
+            a.head = p->topk_desc;
+            a.mant = hd.mant;
+            a.exps = hd.exps;
+            a.K = hd.K;
+            a.ntiles = p->head.ntiles;
+            a.hx = p->items[p->topk_desc].x;
+            a.qdescs = p->qdescs.as<Bfp8QuantDesc>();
+            a.qtasks = p->qtasks.as<int>();
+            a.ntasks = p->ntasks;
+            HIP_OK(bfp8_launch_gemv_head(a, p->head.nwg, s));
+        } else
             HIP_OK(bfp8_launch_gemv_grouped(descs, p->head.tiles.as<Bfp8TileRef>(), p->head.wg_off.as<int>(),
                                             p->head.nwg, -1, s));
     } else if (stage == 1) {
