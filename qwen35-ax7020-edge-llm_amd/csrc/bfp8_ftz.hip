@@ -495,6 +495,7 @@ struct HeadLds {
     float xsc[BFP8_HEAD_MAX_NB];
     uint32_t rec[kWaves][32];
     float red[256];
+    uint64_t keys[BFP8_TILE_ROWS];
 };
 
 // bfp8_quant_block_wave with the records written through global-address-space
@@ -580,15 +581,20 @@ __device__ __forceinline__ void head_reduce(HeadTile& T, const Bfp8HeadArgs& a, 
     const Bfp8GemvDesc& d = a.descs[a.head];
     L.red[q * 64 + lane] = fs;
     __syncthreads();
-    float y = 0.0f;
-    if (q == 0) {
-        // vadd_f32(low, high) then vpadd_f32: y = (fs0 + fs2) + (fs1 + fs3)
-        y = (L.red[lane] + L.red[128 + lane]) + (L.red[64 + lane] + L.red[192 + lane]);
-        const int row = t * BFP8_TILE_ROWS + lane;
+    // wavefront q, lane (r, qq): row 16q + r of the tile (each quad computes
+    // its row's y; vadd_f32(low, high) then vpadd_f32: (fs0 + fs2) + (fs1 + fs3))
+    const int tr = 16 * q + (lane >> 2);
+    const float y = (L.red[tr] + L.red[128 + tr]) + (L.red[64 + tr] + L.red[192 + tr]);
+    const int row = t * BFP8_TILE_ROWS + tr;
+    if ((lane & 3) == 0) {
         if (d.y && row < d.pair_rows) d.y[row] = y;
+        L.keys[tr] = tile_rank_key(y, row, row < d.pair_rows);
     }
-    if (d.topk > 0) topk_partial(d.partials, d.topk, d.pair_rows, t, y);
-    __syncthreads();  // L.red is reused by the next tile
+    if (d.topk > 0) {
+        __syncthreads();
+        tile_topk_rank(L.keys, d.partials, t, d.topk, q, lane);
+    }
+    __syncthreads();  // L.red and L.keys are reused by the next tile
 }
 
 // Loads go out in the order they are needed, and nothing but the arguments

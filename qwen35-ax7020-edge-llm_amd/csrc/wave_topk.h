@@ -28,6 +28,35 @@ __device__ __forceinline__ float key_score(uint64_t k) {
 }
 __device__ __forceinline__ int key_id(uint64_t k) { return (int)~(uint32_t)k; }
 
+// The same order for ranking a tile's rows: every row gets a distinct key,
+// rows without a candidate (invalid score, or past the rows in use) one below
+// every candidate (high word 0).  tile_partial_key maps those back to 0.
+__device__ __forceinline__ uint64_t tile_rank_key(float y, int row, bool in_use) {
+    const uint64_t k = in_use ? topk_key(y, row) : 0ull;
+    return k ? k : (uint64_t)(uint32_t)~(uint32_t)row;
+}
+__device__ __forceinline__ uint64_t tile_partial_key(uint64_t k) { return (k >> 32) ? k : 0ull; }
+
+// A 64-row tile's top-`topk` list (descending, "no candidate" 0s last) by
+// rank instead of a sort, on all four wavefronts of the workgroup: keys[]
+// holds the tile's 64 distinct rank keys (LDS, visible to the workgroup);
+// lane (r, qq) = (lane >> 2, lane & 3) of wavefront w counts the keys among
+// keys[16qq .. 16qq+15] above its row's key 16w + r, the quad adds the four
+// counts (DPP), and quarter 0 stores the key at its rank.  Distinct keys make
+// the ranks a permutation of 0..63, so slots 0..topk-1 are all written.
+__device__ __forceinline__ void tile_topk_rank(const uint64_t* keys, uint64_t* partials, int tile, int topk, int w,
+                                               int lane) {
+    const int r = lane >> 2, qq = lane & 3;
+    const uint64_t mine = keys[16 * w + r];
+    const uint64_t* quarter = keys + 16 * qq;
+    int cnt = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) cnt += quarter[i] > mine ? 1 : 0;
+    cnt += __builtin_amdgcn_update_dpp(0, cnt, 0xB1, 0xF, 0xF, false);  // + quad lane ^ 1
+    cnt += __builtin_amdgcn_update_dpp(0, cnt, 0x4E, 0xF, 0xF, false);  // + quad lane ^ 2
+    if (qq == 0 && cnt < topk) partials[(size_t)tile * topk + cnt] = tile_partial_key(mine);
+}
+
 // ---- wavefront exchange ----------------------------------------------------
 // Lane i receives lane i^j.  j = 1, 2: DPP quad permutes; j = 4, 8, 16:
 // ds_swizzle bit-mask mode (and 0x1f, xor j, within 32 lanes); j = 32, 63:
