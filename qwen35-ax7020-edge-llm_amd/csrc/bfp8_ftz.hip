@@ -76,7 +76,10 @@ struct MergeLds {
 };
 
 // Tree-reduces the W wavefronts' descending lists into wavefront 0's (the
-// partner's list is read reversed, i.e. ascending).
+// partner's list is read reversed, i.e. ascending).  A wavefront writes its
+// slot once, at the level where it drops out, and every slot is read at the
+// level it is written, so one barrier per level suffices; the caller puts a
+// barrier between two calls.
 template <int W>
 __device__ __forceinline__ uint64_t reduce_waves(uint64_t v, int w, int lane, MergeLds<W>& L) {
 #pragma unroll
@@ -84,7 +87,6 @@ __device__ __forceinline__ uint64_t reduce_waves(uint64_t v, int w, int lane, Me
         if ((w & (2 * step - 1)) == step) L.xch[w][lane] = v;
         __syncthreads();
         if ((w & (2 * step - 1)) == 0) v = wave_merge<true>(v, L.xch[w + step][63 - lane], lane);
-        __syncthreads();
     }
     return v;
 }
@@ -94,6 +96,32 @@ __device__ __forceinline__ uint64_t reduce_waves(uint64_t v, int w, int lane, Me
 // list whose head ranks h-th among all heads has at least h+i better keys:
 // only the lists of the kk best heads, and in them only i < kk - h, can reach
 // the top kk.
+// The result: ids / scores of the kk best keys (t: lane's key, lanes < kk),
+// their count, and the argmax (lm_head_argmax: lowest id among maxima above
+// -1e30, else 0; 04/qwen_kernels_opt.c:402-403, :483-490).  Wavefront 0.
+__device__ __forceinline__ void topk_write(const TopkArgs& d, uint64_t v, int lane) {
+    const int kk = d.topk;
+    const uint64_t t = lane < kk ? v : 0ull;
+    const int cnt = __popcll(__ballot(t != 0));
+    if (lane < kk) {
+        d.out_ids[lane] = t ? key_id(t) : -1;
+        d.out_scores[lane] = t ? key_score(t) : 0.0f;
+    }
+    if (lane == 0) {  // lane 0 holds the best key
+        *d.out_count = cnt;
+        *d.out_argmax = (t && key_score(t) > -1e30f) ? key_id(t) : 0;
+    }
+}
+
+__device__ __forceinline__ uint64_t wave_max_key(uint64_t v) {
+#pragma unroll
+    for (int j = 1; j < 64; j <<= 1) {
+        const uint64_t o = xor_lane(v, j);
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
 template <int W, int H>
 __device__ __forceinline__ void topk_merge(const TopkArgs& d, MergeLds<W>& L) {
     const int kk = d.topk;
@@ -101,6 +129,21 @@ __device__ __forceinline__ void topk_merge(const TopkArgs& d, MergeLds<W>& L) {
     const uint64_t* parts = d.partials;
     const int lane = threadIdx.x & 63;
     const int w = threadIdx.x >> 6;
+    if (kk == 1) {  // the best key is the largest list head: a max-reduction, no list merge
+        uint64_t m = 0;
+        for (int i = w * 64 + lane; i < ntiles; i += W * 64) {
+            const uint64_t h = __builtin_nontemporal_load(&parts[i]);
+            m = h > m ? h : m;
+        }
+        m = wave_max_key(m);
+        if (lane == 0) L.xch[0][w] = m;
+        __syncthreads();
+        if (w == 0) {
+            m = wave_max_key(lane < W ? L.xch[0][lane] : 0ull);
+            topk_write(d, m, lane);
+        }
+        return;
+    }
     // 1. the 64 best list heads
     uint64_t v = 0;
     for (int base = w * 64 * H; base < ntiles; base += W * 64 * H) {
@@ -144,20 +187,7 @@ __device__ __forceinline__ void topk_merge(const TopkArgs& d, MergeLds<W>& L) {
     else
         v = e[0];
     v = reduce_waves<W>(v, w, lane, L);
-    if (w == 0) {
-        const uint64_t t = lane < kk ? v : 0ull;
-        const int cnt = __popcll(__ballot(t != 0));
-        if (lane < kk) {
-            d.out_ids[lane] = t ? key_id(t) : -1;
-            d.out_scores[lane] = t ? key_score(t) : 0.0f;
-        }
-        if (lane == 0) {
-            *d.out_count = cnt;
-            // lm_head_argmax: lowest id among maxima above -1e30, else 0
-            // (04/qwen_kernels_opt.c:402-403, :483-490)
-            *d.out_argmax = (t && key_score(t) > -1e30f) ? key_id(t) : 0;
-        }
-    }
+    if (w == 0) topk_write(d, v, lane);
 }
 
 constexpr int kWaves = 4;        // wavefronts per GEMV workgroup

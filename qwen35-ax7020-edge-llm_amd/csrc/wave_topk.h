@@ -58,15 +58,21 @@ __device__ __forceinline__ void tile_topk_rank(const uint64_t* keys, uint64_t* p
 }
 
 // ---- wavefront exchange ----------------------------------------------------
-// Lane i receives lane i^j.  j = 1, 2: DPP quad permutes; j = 4, 8, 16:
-// ds_swizzle bit-mask mode (and 0x1f, xor j, within 32 lanes); j = 32, 63:
-// ds_bpermute.  Always called with j a constant after unrolling.
+// Lane i receives lane i^j.  j = 1, 2: DPP quad permutes; j = 4, 8: two DPP
+// moves each (quad_perm [3,2,1,0] gives i^3, row_half_mirror i^7, row_mirror
+// i^15 within a row of 16: i^3^7 = i^4, i^15^7 = i^8), no LDS round trip;
+// j = 16: ds_swizzle bit-mask mode (and 0x1f, xor 16, within 32 lanes);
+// j = 32, 63: ds_bpermute.  Always called with j a constant after unrolling.
+template <int kCtrl>
+__device__ __forceinline__ int dpp_move(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, kCtrl, 0xF, 0xF, false);
+}
 __device__ __forceinline__ uint32_t xor_lane32(uint32_t v, int j) {
     switch (j) {
-        case 1: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);
-        case 2: return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);
-        case 4: return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x1F | (4 << 10));
-        case 8: return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x1F | (8 << 10));
+        case 1: return (uint32_t)dpp_move<0xB1>((int)v);
+        case 2: return (uint32_t)dpp_move<0x4E>((int)v);
+        case 4: return (uint32_t)dpp_move<0x141>(dpp_move<0x1B>((int)v));
+        case 8: return (uint32_t)dpp_move<0x141>(dpp_move<0x140>((int)v));
         case 16: return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x1F | (16 << 10));
         default: return (uint32_t)__shfl_xor((int)v, j, 64);
     }

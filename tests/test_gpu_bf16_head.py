@@ -224,6 +224,13 @@ def test_tile_layout_and_tiled_lm_head(gpu, head_case):
         for src in np.argsort(-l2, kind="stable")[:8]:
             t2[(int(src) * 7 + 3) % vocab] = t2[src]
         cases.append((t2, h2, ol.bf16_logits(h2, t2, tail=0)))
+    # equal scores (every row the same, or three distinct rows): ties broken by
+    # the row alone, the selection's histogram bins refined down to the row bits
+    row = table[:1]
+    t_eq = np.ascontiguousarray(np.repeat(row, 5000, axis=0))
+    cases.append((t_eq, h, ol.bf16_logits(h, t_eq, tail=0)))
+    t3 = np.ascontiguousarray(table[np.random.default_rng(9).integers(0, 3, 9000)])
+    cases.append((t3, h, ol.bf16_logits(h, t3, tail=0)))
     hn = h.copy()
     hn[5] = np.inf
     cases.append((table, hn, ol.bf16_logits(hn, table, tail=0)))
@@ -246,7 +253,7 @@ def test_tile_layout_and_tiled_lm_head(gpu, head_case):
         torch.cuda.synchronize()
         assert np.array_equal(tiles.cpu().numpy().view(np.uint16), tile_layout(tb)), vocab
         assert same_f32(logits.cpu().numpy(), ref), vocab
-        for k in (1, 64):
+        for k in (1, 40, 64):
             qk.check(lib.bf16_dev_lm_head_tiles(ids.data_ptr(), sc.data_ptr(), cnt.data_ptr(), cnt.data_ptr() + 4,
                                                 None, hd.data_ptr(), tiles.data_ptr(), vocab, 1024, k, s))
             torch.cuda.synchronize()
