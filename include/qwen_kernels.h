@@ -367,8 +367,9 @@ void bfp8_synth_normal(float* out, int n, uint64_t seed);
 /* silu(a)*b with a, b ~ N(0,1), then a fraction of positions set to +-mag. */
 void bfp8_synth_swiglu(float* out, int n, uint64_t seed, double outlier_frac, float mag);
 
-/* Bandwidth probes for the roofline: a read-only sweep of `bytes` and a
- * device-to-device copy (used to calibrate hardware byte counters). */
+/* Bandwidth probes for the roofline: a read-only sweep of `bytes` (2 KiB runs
+ * per wavefront, interleaved, one in flight: the fastest read pattern measured)
+ * and a device-to-device copy (used to calibrate hardware byte counters). */
 int bfp8_dev_read_probe(const void* buf, size_t bytes, uint32_t* out, void* stream);
 int bfp8_dev_copy_probe(void* dst, const void* src, size_t bytes, void* stream);
 

@@ -207,20 +207,25 @@ extern "C" __global__ __launch_bounds__(256) void bfp8_synth_kernel(
 // non-temporal dwordx4 loads in flight per thread; the folded value is stored
 // only if it hits a magic constant, which keeps the loads live without any
 // atomic traffic.
-extern "C" __global__ __launch_bounds__(256) void bfp8_read_probe_kernel(
-    const u32x4* __restrict__ src, size_t n16, size_t chunk16, uint32_t* __restrict__ out) {
+// Read-bandwidth probe: wavefront v's step s reads the 2 KiB run at
+// (s * wavefronts + v) * 2 KiB (two 1 KiB loads, non-temporal), one step in
+// flight per wavefront, 4096 wavefronts.  Of the patterns measured (blocked
+// per workgroup with eight loads in flight per lane: 6.8-6.95 TB/s; runs of
+// 1-8 KiB, one to four steps in flight) this one reads fastest: 7.14-7.20 TB/s
+// over 1 GiB and 128 MiB.
+extern "C" __global__ __launch_bounds__(256) void bfp8_read_probe_kernel(const u32x4* __restrict__ src, size_t n16,
+                                                                         uint32_t* __restrict__ out) {
+    const size_t nw = (size_t)gridDim.x * 4;
+    const size_t wv = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
     u32x4 acc = u32x4(0u);
-    const size_t beg = (size_t)blockIdx.x * chunk16;
-    const size_t end = beg + chunk16 < n16 ? beg + chunk16 : n16;
-    size_t i = beg + threadIdx.x;
-    for (; i + 7 * 256 < end; i += 8 * 256) {
-        u32x4 v[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = __builtin_nontemporal_load(src + i + u * 256);
-#pragma unroll
-        for (int u = 0; u < 8; ++u) acc ^= v[u];
+    for (size_t st = 0;; ++st) {
+        const size_t i0 = (st * nw + wv) * 128 + lane, i1 = i0 + 64;
+        const u32x4 v0 = i0 < n16 ? __builtin_nontemporal_load(src + i0) : u32x4(0u);
+        const u32x4 v1 = i1 < n16 ? __builtin_nontemporal_load(src + i1) : u32x4(0u);
+        acc ^= v0 ^ v1;
+        if (!__builtin_amdgcn_ballot_w64(i0 < n16)) break;  // every lane past the end: the wavefront is done
     }
-    for (; i < end; i += 256) acc ^= __builtin_nontemporal_load(src + i);
     const uint32_t v = acc.x ^ acc.y ^ acc.z ^ acc.w;
     if (v == 0x9E3779B9u) out[0] = v;
 }
@@ -406,9 +411,7 @@ hipError_t bfp8_launch_sample(const Bfp8SampleArgs& a, hipStream_t s) {
 hipError_t bfp8_launch_read_probe(const void* buf, size_t bytes, uint32_t* out, hipStream_t s) {
     const size_t n16 = bytes / 16;
     if (n16 == 0) return hipSuccess;
-    const int grid = 4096;
-    const size_t chunk16 = (n16 + grid - 1) / grid;
-    hipLaunchKernelGGL(bfp8_read_probe_kernel, dim3(grid), dim3(256), 0, s, (const u32x4*)buf, n16, chunk16, out);
+    hipLaunchKernelGGL(bfp8_read_probe_kernel, dim3(1024), dim3(256), 0, s, (const u32x4*)buf, n16, out);
     return hipGetLastError();
 }
 
