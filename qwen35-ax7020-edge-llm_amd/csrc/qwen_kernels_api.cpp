@@ -839,7 +839,7 @@ struct Plan {
     std::vector<bfp8_plan_item> items;
     std::vector<int> odd_items;    // items needing the odd-row kernel
     std::vector<int> float_items;  // K > 4096 items (float path, own launches)
-    DevBuf descs, qdescs, xq, xscale, xsplit, partials;
+    DevBuf descs, qdescs, xscale, xsplit, partials;
     DevBuf qtasks;                 // fused head: (quantize descriptor, block) pairs
     Launch head, rest;             // lm_head tiles, then every other GEMV's
     int nq = 0, max_nb = 0, ntasks = 0;
@@ -896,7 +896,7 @@ int deal_tiles(Launch& L, const std::vector<int>& idx, const bfp8_plan_item* ite
 }
 
 void release_plan(Plan* p) {
-    p->descs.release(); p->qdescs.release(); p->xq.release(); p->xscale.release(); p->xsplit.release();
+    p->descs.release(); p->qdescs.release(); p->xscale.release(); p->xsplit.release();
     p->partials.release(); p->qtasks.release();
     p->head.tiles.release(); p->head.wg_off.release(); p->rest.tiles.release(); p->rest.wg_off.release();
 }
@@ -917,7 +917,7 @@ void* bfp8_plan_create(const bfp8_plan_item* items, int n) {
     Plan* p = new Plan();
     p->items.assign(items, items + n);
     int ntopk = 0;
-    size_t xs_words = 0, xsc_floats = 0, xq_elems = 0;
+    size_t xs_words = 0, xsc_floats = 0;
     for (int i = 0; i < n; ++i) {
         const bfp8_plan_item& it = items[i];
         if (it.M <= 0 || it.K < 64 || !it.x || !it.mant_gpu || !it.exps_gpu ||
@@ -933,7 +933,6 @@ void* bfp8_plan_create(const bfp8_plan_item* items, int n) {
         if (it.K <= 4096) {
             xs_words += (size_t)nb * 32;
             xsc_floats += nb;
-            xq_elems += (size_t)nb * 64;
             p->max_nb = std::max(p->max_nb, nb);
         }
     }
@@ -945,10 +944,9 @@ void* bfp8_plan_create(const bfp8_plan_item* items, int n) {
     int rc = 0;
     rc = rc ? rc : p->xsplit.reserve(xs_words * 4);
     rc = rc ? rc : p->xscale.reserve(xsc_floats * 4);
-    rc = rc ? rc : p->xq.reserve(xq_elems * 2);
     std::vector<Bfp8QuantDesc> hq;
     std::vector<int> hq_of_item(n, -1);
-    size_t ow = 0, of = 0, oq = 0;
+    size_t ow = 0, of = 0;
     for (int i = 0; i < n && !rc; ++i) {
         const bfp8_plan_item& it = items[i];
         Bfp8GemvDesc d{};
@@ -960,7 +958,7 @@ void* bfp8_plan_create(const bfp8_plan_item* items, int n) {
         const int nb = bfp8_nblocks(it.K);
         Bfp8QuantDesc q{};
         q.x = it.x;
-        q.xq = p->xq.as<int16_t>() + oq;
+        q.xq = nullptr;  // no plan kernel reads the int16 values (the tail rows read the split form)
         q.xscale = p->xscale.as<float>() + of;
         q.xsplit = p->xsplit.as<uint32_t>() + ow;
         q.K = it.K;
@@ -982,7 +980,6 @@ void* bfp8_plan_create(const bfp8_plan_item* items, int n) {
         p->hdesc.push_back(d);
         ow += (size_t)nb * 32;
         of += nb;
-        oq += (size_t)nb * 64;
     }
     // Two persistent launches: the lm_head's tiles, then every other GEMV's
     // (larger K first).  Workgroup 0 of the second launch merges the lm_head's
