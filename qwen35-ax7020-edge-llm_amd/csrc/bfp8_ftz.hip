@@ -758,6 +758,11 @@ __global__ __launch_bounds__(256) void bfp8_gemv_batch_kernel(float* __restrict_
     const int r = threadIdx.x & 63;
     const int t = blockIdx.x;
     const int nb = K >> 6;
+    // blockIdx.y: which B vectors of the call (a GEMV with fewer tiles than
+    // CUs spreads its vectors over several workgroups per tile)
+    Y += (size_t)blockIdx.y * B * M;
+    xsplit += (size_t)blockIdx.y * B * nb * 32;
+    xscale += (size_t)blockIdx.y * B * nb;
     const int nb4 = (nb + 3) >> 2;
     const uint8_t* mtile = mant + (size_t)t * nb * 4096u;
     const uint8_t* etile = exps + (size_t)t * nb4 * 256u;
@@ -919,23 +924,38 @@ hipError_t bfp8_launch_gemv_wide_grouped(const Bfp8GemvDesc* descs_dev, const Bf
 
 template <int B>
 static hipError_t launch_batch_t(float* Y, const uint32_t* xsplit, const float* xscale,
-                                 const uint8_t* mant, const uint8_t* exps, int M, int K,
+                                 const uint8_t* mant, const uint8_t* exps, int M, int K, int groups,
                                  hipStream_t s) {
-    hipLaunchKernelGGL(bfp8_gemv_batch_kernel<B>, dim3(bfp8_ntiles(M)), dim3(256), 0, s, Y, xsplit,
+    hipLaunchKernelGGL(bfp8_gemv_batch_kernel<B>, dim3(bfp8_ntiles(M), groups), dim3(256), 0, s, Y, xsplit,
                        xscale, mant, exps, M, K);
     return hipGetLastError();
+}
+
+static int cu_count() {
+    static const int n = [] {
+        int dev = 0, cus = 256;
+        hipDeviceProp_t p;
+        if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&p, dev) == hipSuccess) cus = p.multiProcessorCount;
+        return cus;
+    }();
+    return n;
 }
 
 hipError_t bfp8_launch_gemv_batch(float* Y, const uint32_t* xsplit, const float* xscale,
                                   const uint8_t* mant, const uint8_t* exps, int M, int K, int B,
                                   hipStream_t s) {
-    if (bfp8_ntiles(M) == 0) return hipSuccess;
-    switch (B) {
-        case 1: return launch_batch_t<1>(Y, xsplit, xscale, mant, exps, M, K, s);
-        case 2: return launch_batch_t<2>(Y, xsplit, xscale, mant, exps, M, K, s);
-        case 4: return launch_batch_t<4>(Y, xsplit, xscale, mant, exps, M, K, s);
-        case 8: return launch_batch_t<8>(Y, xsplit, xscale, mant, exps, M, K, s);
-        case 16: return launch_batch_t<16>(Y, xsplit, xscale, mant, exps, M, K, s);
-        default: return hipErrorInvalidValue;
+    const int nt = bfp8_ntiles(M);
+    if (nt == 0) return hipSuccess;
+    if (B != 1 && B != 2 && B != 4 && B != 8 && B != 16) return hipErrorInvalidValue;
+    // while the tiles leave CUs idle, split the vectors over more workgroups
+    // (each re-reads its tile's weights, from L2 / MALL for such small GEMVs)
+    int groups = 1;
+    while (groups * 2 <= B && nt * groups * 2 <= cu_count()) groups *= 2;
+    switch (B / groups) {
+        case 1: return launch_batch_t<1>(Y, xsplit, xscale, mant, exps, M, K, groups, s);
+        case 2: return launch_batch_t<2>(Y, xsplit, xscale, mant, exps, M, K, groups, s);
+        case 4: return launch_batch_t<4>(Y, xsplit, xscale, mant, exps, M, K, groups, s);
+        case 8: return launch_batch_t<8>(Y, xsplit, xscale, mant, exps, M, K, groups, s);
+        default: return launch_batch_t<16>(Y, xsplit, xscale, mant, exps, M, K, groups, s);
     }
 }
