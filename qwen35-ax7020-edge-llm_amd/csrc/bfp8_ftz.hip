@@ -753,7 +753,10 @@ __global__ __launch_bounds__(256) void bfp8_gemv_batch_kernel(float* __restrict_
                                                               const uint8_t* __restrict__ exps, int M,
                                                               int K) {
     __shared__ uint32_t xl[B * kBatchChunk * 32];
-    __shared__ float red[4 * 64 * B];
+    __shared__ float xsl[B * kBatchChunk];  // the chunk's block scales (LDS, like the split words: no scalar loads,
+                                            // whose out-of-order returns would make every LDS wait a full wait)
+    float* red = reinterpret_cast<float*>(xl);  // the cross-wave sums reuse the staging space (4 * 64 * B floats)
+    static_assert(kBatchChunk * 32 >= 4 * 64, "red fits in xl");
     const int q = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int r = threadIdx.x & 63;
     const int t = blockIdx.x;
@@ -777,16 +780,21 @@ __global__ __launch_bounds__(256) void bfp8_gemv_batch_kernel(float* __restrict_
     for (int b0 = 0; b0 < nb; b0 += kBatchChunk) {
         const int nbc = min(kBatchChunk, nb - b0);
         u32x4 w[kBatchChunk];
-        uint32_t ew[2] = {0u, 0u};
+        uint32_t ew[kBatchChunk / 4] = {};
 #pragma unroll
         for (int u = 0; u < kBatchChunk; ++u)
             if (u < nbc) w[u] = load_w(wrs, wv, (b0 + u) * 4096);
-        ew[0] = load_e(ers, r * 4, (b0 >> 2) * 256);
-        if (nbc > 4) ew[1] = load_e(ers, r * 4, (b0 >> 2) * 256 + 256);
+#pragma unroll
+        for (int m = 0; m < kBatchChunk / 4; ++m)
+            if (4 * m < nbc) ew[m] = load_e(ers, r * 4, ((b0 >> 2) + m) * 256);
         __syncthreads();  // previous chunk's LDS reads are done
         for (int i = threadIdx.x; i < B * nbc * 32; i += 256) {
             int v = i / (nbc * 32), o = i - v * nbc * 32;
             xl[v * kBatchChunk * 32 + o] = xsplit[(size_t)v * xwords + b0 * 32 + o];
+        }
+        for (int i = threadIdx.x; i < B * nbc; i += 256) {
+            const int v = i / nbc, u = i - v * nbc;
+            xsl[v * kBatchChunk + u] = xscale[(size_t)v * nb + b0 + u];
         }
         __syncthreads();
 #pragma unroll
@@ -794,26 +802,50 @@ __global__ __launch_bounds__(256) void bfp8_gemv_batch_kernel(float* __restrict_
             if (u >= nbc) break;
             const uint32_t e = (ew[u >> 2] >> (8 * (u & 3))) & 0xffu;
             const float sc = exp_scale_ftz(e);
+            // vectors in groups of four: the group's LDS reads go out together,
+            // then its four dot-product chains interleave
+            constexpr int kG = B < 4 ? B : 4;
 #pragma unroll
-            for (int v = 0; v < B; ++v) {
-                const uint32_t* xb = xl + (v * kBatchChunk + u) * 32 + q * 8;
-                const uint4 h = *reinterpret_cast<const uint4*>(xb);
-                const uint4 l = *reinterpret_cast<const uint4*>(xb + 4);
-                int acc = __builtin_amdgcn_sdot4((int)w[u].x, (int)h.x, 0, false);
-                acc = __builtin_amdgcn_sdot4((int)w[u].y, (int)h.y, acc, false);
-                acc = __builtin_amdgcn_sdot4((int)w[u].z, (int)h.z, acc, false);
-                acc = __builtin_amdgcn_sdot4((int)w[u].w, (int)h.w, acc, false);
-                acc = (int)((uint32_t)acc << 8);
-                acc = __builtin_amdgcn_sdot4((int)w[u].x, (int)l.x, acc, false);
-                acc = __builtin_amdgcn_sdot4((int)w[u].y, (int)l.y, acc, false);
-                acc = __builtin_amdgcn_sdot4((int)w[u].z, (int)l.z, acc, false);
-                acc = __builtin_amdgcn_sdot4((int)w[u].w, (int)l.w, acc, false);
-                float t1 = (float)acc * sc;
-                float t2 = t1 * xscale[(size_t)v * nb + b0 + u];
-                fs[v] = fs[v] + t2;
+            for (int v0 = 0; v0 < B; v0 += kG) {
+                uint4 h[kG], l[kG];
+                float xs[kG];
+#pragma unroll
+                for (int j = 0; j < kG; ++j) {
+                    const uint32_t* xb = xl + ((v0 + j) * kBatchChunk + u) * 32 + q * 8;
+                    h[j] = *reinterpret_cast<const uint4*>(xb);
+                    l[j] = *reinterpret_cast<const uint4*>(xb + 4);
+                    xs[j] = xsl[(v0 + j) * kBatchChunk + u];
+                }
+                int acc[kG];
+#pragma unroll
+                for (int j = 0; j < kG; ++j) acc[j] = __builtin_amdgcn_sdot4((int)w[u].x, (int)h[j].x, 0, false);
+#pragma unroll
+                for (int j = 0; j < kG; ++j) acc[j] = __builtin_amdgcn_sdot4((int)w[u].y, (int)h[j].y, acc[j], false);
+#pragma unroll
+                for (int j = 0; j < kG; ++j) acc[j] = __builtin_amdgcn_sdot4((int)w[u].z, (int)h[j].z, acc[j], false);
+#pragma unroll
+                for (int j = 0; j < kG; ++j) acc[j] = __builtin_amdgcn_sdot4((int)w[u].w, (int)h[j].w, acc[j], false);
+#pragma unroll
+                for (int j = 0; j < kG; ++j) {
+                    acc[j] = (int)((uint32_t)acc[j] << 8);
+                    acc[j] = __builtin_amdgcn_sdot4((int)w[u].x, (int)l[j].x, acc[j], false);
+                }
+#pragma unroll
+                for (int j = 0; j < kG; ++j) acc[j] = __builtin_amdgcn_sdot4((int)w[u].y, (int)l[j].y, acc[j], false);
+#pragma unroll
+                for (int j = 0; j < kG; ++j) acc[j] = __builtin_amdgcn_sdot4((int)w[u].z, (int)l[j].z, acc[j], false);
+#pragma unroll
+                for (int j = 0; j < kG; ++j) acc[j] = __builtin_amdgcn_sdot4((int)w[u].w, (int)l[j].w, acc[j], false);
+#pragma unroll
+                for (int j = 0; j < kG; ++j) {
+                    const float t1 = (float)acc[j] * sc;
+                    const float t2 = t1 * xs[j];
+                    fs[v0 + j] = fs[v0 + j] + t2;
+                }
             }
         }
     }
+    __syncthreads();  // every wavefront is done with the staged activations
 #pragma unroll
     for (int v = 0; v < B; ++v) red[(v * 4 + q) * 64 + r] = fs[v];
     __syncthreads();
