@@ -43,6 +43,9 @@ import time
 from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
+# the CPU baseline's OpenMP threads stay on neighbouring cores (read by
+# libgomp when the reference library first loads it)
+os.environ.setdefault("OMP_PROC_BIND", "close")
 PKG = ROOT / "qwen35-ax7020-edge-llm_amd"
 sys.path.insert(0, str(PKG))
 
@@ -101,10 +104,11 @@ def read_traffic(workload, kernel):
     return float(m.group(1)) if m else None
 
 
-def cpu_baseline(items, seconds=10.0):
+def cpu_baseline(items, seconds=10.0, single_seconds=6.0):
     """The reference's host bfp8_gemv (float path, 04/qwen_kernels_opt.c:311-325)
     built from its own sources (oracle/_ref), timed on this host over the same
-    synthetic GEMV list; falls back to the oracle's restatement of that path."""
+    synthetic GEMV list; falls back to the oracle's restatement of that path.
+    Timed with the OpenMP default thread count, then with one thread."""
     import numpy as np
 
     import qwen_kernels_gpu as qk
@@ -128,20 +132,41 @@ def cpu_baseline(items, seconds=10.0):
         x = qk.synth_normal(K, 8_000 + i)
         host.append((mant, exps, x, np.empty(M, dtype=np.float32), M, K))
     nbytes = metric_bytes(items)
-    t0 = time.perf_counter()
-    sweeps = 0
-    while True:
-        for mant, exps, x, y, M, K in host:
+
+    def timed(limit):
+        for mant, exps, x, y, M, K in host[:1]:  # first touch of the pages, untimed
             fn(y.ctypes.data, x.ctypes.data, mant.ctypes.data, exps.ctypes.data, M, K)
-        sweeps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count()
-    return {"value": round(nbytes * sweeps / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
-            "sample": f"{sweeps} passes over the same GEMV list ({len(items)} GEMVs, {nbytes / 1e6:.1f} MB per pass; "
-                      f"the lm_head as a plain GEMV, the reference having no fused BFP8 lm_head), host float path "
-                      f"with OpenMP over rows, {el:.1f} s"}
+        t0 = time.perf_counter()
+        sweeps = 0
+        while True:
+            for mant, exps, x, y, M, K in host:
+                fn(y.ctypes.data, x.ctypes.data, mant.ctypes.data, exps.ctypes.data, M, K)
+            sweeps += 1
+            el = time.perf_counter() - t0
+            if el >= limit:
+                return sweeps, el
+
+    gomp = None
+    if kind == "reference":
+        # libgomp.so.1 is the OpenMP runtime the reference library links:
+        # its thread count is the one the timed calls use
+        gomp = ctypes.CDLL("libgomp.so.1")
+        gomp.omp_set_num_threads.argtypes = [ctypes.c_int]
+        gomp.omp_get_max_threads.restype = ctypes.c_int
+    sweeps, el = timed(seconds)
+    threads = gomp.omp_get_max_threads() if gomp else 1
+    out = {"value": round(nbytes * sweeps / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
+           "sample": f"{sweeps} passes over the same GEMV list ({len(items)} GEMVs, {nbytes / 1e6:.1f} MB per pass; "
+                     f"the lm_head as a plain GEMV, the reference having no fused BFP8 lm_head), host float path "
+                     f"with OpenMP over rows (OMP_PROC_BIND={os.environ.get('OMP_PROC_BIND')}), {el:.1f} s"}
+    if gomp:
+        # the same library with one OpenMP thread
+        gomp.omp_set_num_threads(1)
+        s1, e1 = timed(single_seconds)
+        gomp.omp_set_num_threads(threads)
+        out["single_thread"] = {"value": round(nbytes * s1 / e1 / 1e9, 3), "unit": "GB/s", "cores": 1,
+                                "sample": f"{s1} passes over the same list, {e1:.1f} s"}
+    return out
 
 
 def main():
@@ -216,11 +241,34 @@ def main():
     value = mbytes / (ms_per_step * 1e-3) / 1e9
     print(f"[bench] timed {args.steps} steps: {ms_per_step * 1e3:.1f} us/step", file=sys.stderr, flush=True)
 
+    # each step alone between HIP events: median and min, cold (rotating
+    # weight copies, as above) and warm (one copy again and again, so a
+    # workload under the 256 MB last-level cache is served from it)
+    stream = torch.cuda.current_stream()
+
+    def per_step(pick):
+        evs = []
+        for i in range(args.steps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            plans[pick(i)].run()
+            b.record(stream)
+            evs.append((a, b))
+        torch.cuda.synchronize()
+        us = sorted(a.elapsed_time(b) * 1e3 for a, b in evs)
+        return {"us_median": round(us[len(us) // 2], 2), "us_min": round(us[0], 2),
+                "GBps_median": round(mbytes / (us[len(us) // 2] * 1e-6) / 1e9, 1)}
+
+    cold = per_step(lambda i: i % copies)
+    for i in range(2):
+        plans[0].run()
+    warm = per_step(lambda i: 0)
+    print(f"[bench] per step: cold {cold}, warm {warm}", file=sys.stderr, flush=True)
+
     # each GEMV launch alone, HIP events on the stream it is launched on:
     # stage 0 streams the lm_head's tiles, stage 1 every other GEMV's (its
     # workgroup 0 also merges the lm_head top-k; with no other GEMV, stage 1
     # is the stand-alone merge kernel)
-    stream = torch.cuda.current_stream()
     head = [it for it in items if it[5]]
     rest = [it for it in items if not it[5]]
     stages = []
@@ -295,6 +343,8 @@ def main():
                    "rotating_copies": copies, "parallelism": "single GPU"},
         "us_per_step": round(ms_per_step * 1e3, 2),
         "pct_of_peak": round(100 * value / PEAK_HBM_GBPS, 2),
+        "per_step_cold": cold,
+        "per_step_warm": warm,
         "kernel": {"name": dom["name"], "stage": dom["stage"], "avg_us": round(kernel_us, 2),
                    "algorithmic_bytes": dom["bytes"]},
         "launches_us": {f"stage{st['stage']}:{st['name']}": round(st["avg_us"], 2) for st in stages}
