@@ -115,7 +115,8 @@ struct Workspace {
     DevBuf buf;
     float *h, *h2;  // the hidden state ping-pongs between these (see RtRowsArgs::h_out)
     float *normed, *qkv, *z, *zsilu, *attn, *o, *gate, *up, *down;
-    int* lm;  // [ids 1, scores 1, count, argmax]
+    int* lm;        // [ids 1, scores 1, count, argmax]; directly after h2
+    bool start_h2;  // a token's embedding goes to h2 (see result_out)
 };
 
 struct Forward {
@@ -191,8 +192,10 @@ int ensure_workspace() {
         return r;
     };
     float** fl[] = {&w.h, &w.h2, &w.normed, &w.qkv, &w.z, &w.zsilu, &w.attn, &w.o, &w.gate, &w.up, &w.down};
-    for (int i = 0; i < 11; ++i) *fl[i] = reinterpret_cast<float*>(take((size_t)nf[i] * 4));
-    w.lm = reinterpret_cast<int*>(take(16));
+    for (int i = 0; i < 11; ++i) {
+        *fl[i] = reinterpret_cast<float*>(take((size_t)nf[i] * 4));
+        if (i == 1) w.lm = reinterpret_cast<int*>(take(16));  // h2 is a multiple of 256 B
+    }
     F.ws_ready = true;
     return BFP8_OK;
 }
@@ -470,6 +473,27 @@ int h_out(float* h, const float* dev) {
     HIP_OK(hipMemcpyAsync(h, dev, (size_t)kHidden * 4, hipMemcpyDeviceToHost, g.stream));
     HIP_OK(hipStreamSynchronize(g.stream));
     return BFP8_OK;
+}
+
+// A token's hidden state hd and lm_head result back to the host.  When hd is
+// h2 the two are adjacent and come back in one copy through pinned memory;
+// otherwise in two, and the next token starts in the other buffer: the layer
+// sequence fixes how often the state moves between h and h2, so it then ends
+// in h2.
+int result_out(float* h, const float* hd, int* out) {
+    Workspace& w = F.ws;
+    const size_t hb = (size_t)kHidden * 4;
+    if (hd == w.h2) {
+        if (int rc = g.rt_pin.reserve(hb + 16)) return rc;
+        HIP_OK(hipMemcpyAsync(g.rt_pin.p, w.h2, hb + 16, hipMemcpyDeviceToHost, g.stream));
+        HIP_OK(hipStreamSynchronize(g.stream));
+        memcpy(h, g.rt_pin.p, hb);
+        memcpy(out, static_cast<const char*>(g.rt_pin.p) + hb, 16);
+        return BFP8_OK;
+    }
+    w.start_h2 = !w.start_h2;
+    HIP_OK(hipMemcpyAsync(out, w.lm, 16, hipMemcpyDeviceToHost, g.stream));
+    return h_out(h, hd);
 }
 
 // Copies back the device states that resident calls left newer than the
@@ -785,7 +809,7 @@ int forward_token_c(int token_id, float* h, const LinearLayerPlan* linear_plans,
         RT_CHECK("forward_token_c", fwd_vec(embed_table, (size_t)kVocab * kHidden, &table));
     }
     Workspace& w = F.ws;
-    float* hd = w.h;  // the hidden state on the device
+    float* hd = w.start_h2 ? w.h2 : w.h;  // the hidden state on the device
     RT_CHECK("forward_token_c", states_in(layers));
     {
         Step s(QP_EMBED);
@@ -830,12 +854,8 @@ int forward_token_c(int token_id, float* h, const LinearLayerPlan* linear_plans,
         RT_CHECK("forward_token_c", s.done());
     }
     int out[4] = {0, 0, 0, 0};
-    if (hipMemcpyAsync(out, w.lm, sizeof out, hipMemcpyDeviceToHost, g.stream) != hipSuccess) {
-        set_error("lm_head readback failed");
-        fatal("forward_token_c");
-    }
     RT_CHECK("forward_token_c", states_out(layers));
-    RT_CHECK("forward_token_c", h_out(h, hd));
+    RT_CHECK("forward_token_c", result_out(h, hd, out));
     if (g_prof_on) g_prof_ms[QP_TOTAL] += now_ms() - t_total;
     return out[3];
 }
