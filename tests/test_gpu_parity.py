@@ -369,6 +369,32 @@ def test_lm_head_small_vocab_and_invalid_arguments(gpu, torch_mod):
     assert kk.lm_head_argmax(x, mant, exps, 99, 128) == -1
 
 
+def test_random_lm_heads_against_the_oracle(gpu, torch_mod):
+    """Eight seeded lm_heads: even vocabularies of 2-140,000 rows, hidden 64-1,024
+    (whole blocks), k in 1-64, half of them with mantissas in {-1, 0, 1} so that
+    equal scores are common: ids (ties broken by the lower id), scores bit-exact
+    and the argmax against the restatement."""
+    qk = gpu
+    kk = qk.Bfp8Kernels()
+    rng = np.random.default_rng(9091)
+    for i in range(8):
+        V = int(rng.integers(1, 70001)) * 2
+        H = int(rng.integers(1, 17)) * 64
+        k = int(rng.integers(1, 65))
+        seed = int(rng.integers(0, 2**31))
+        r = np.random.default_rng(seed)
+        lo, hi = (-1, 2) if i % 2 else (-128, 128)
+        mant = r.integers(lo, hi, size=(V, H), dtype=np.int8)
+        exps = r.integers(120, 131, size=(V, H // 64), dtype=np.uint8)
+        x = r.standard_normal(H).astype(F32)
+        say("random lm_head", V, H, k, seed)
+        y_ref, *_ = ol.gemv_neon(x, mant, exps)
+        ids, sc = kk.lm_head_topk(x, mant, exps, V, H, k)
+        ids_ref, sc_ref = ol.topk(y_ref, k)
+        assert np.array_equal(ids, ids_ref) and same_f32(sc, sc_ref), (V, H, k, seed)
+        assert kk.lm_head_argmax(x, mant, exps, V, H) == ol.argmax(y_ref), (V, H, seed)
+
+
 def test_small_plan_one_tile_per_workgroup(gpu, torch_mod):
     """A plan without an lm_head and with few row tiles runs its GEMVs one tile
     per 16-wavefront workgroup; an odd-M item adds the tail-row kernel and a
@@ -473,6 +499,54 @@ def test_plan_lm_head_merge_paths(gpu, torch_mod, shape):
 
 
 # ---- batch and sweep ---------------------------------------------------------------------------------
+def _random_cases(seed, n, kmax, k_whole):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        M = int(rng.choice([rng.integers(1, 40), rng.integers(40, 1500)]))
+        K = int(rng.integers(1, kmax // 64 + 1)) * 64 if (k_whole or i % 2 == 0) else int(rng.integers(1, kmax + 1))
+        out.append((M, K, int(rng.integers(0, 2**31))))
+    return out
+
+
+def _random_planes(M, K, seed):
+    rng = np.random.default_rng(seed)
+    mant = rng.integers(-128, 128, size=(M, K), dtype=np.int8)
+    exps = rng.integers(0, 256, size=(M, max(K // 64, 0)), dtype=np.uint8)
+    x = (rng.standard_normal(K) * np.float32(10.0) ** rng.integers(-4, 3)).astype(F32)
+    x[rng.random(K) < 0.02] = 0.0
+    return rng, mant, exps, x
+
+
+def test_random_shapes_against_the_oracle(gpu, torch_mod):
+    """24 seeded shapes: 1-1,499 rows (odd and even), K up to 4,096 whole
+    blocks or ragged, every exponent byte, mantissa -128 included, activations
+    spanning seven decades with zeros: y bit-exact against the NEON-order
+    restatement."""
+    qk = gpu
+    for M, K, seed in _random_cases(4242, 24, 4096, False):
+        _, mant, exps, x = _random_planes(M, K, seed)
+        say("random gemv", M, K, seed)
+        y = qk.Bfp8Kernels().gemv_bfp8(x, mant, exps, M, K)
+        y_ref, *_ = ol.gemv_neon(x, mant, exps)
+        assert same_f32(y, y_ref), (M, K, seed, mismatch(y, y_ref))
+
+
+def test_random_batches_against_the_oracle(gpu, torch_mod):
+    """Six seeded batched calls: 1-16 vectors, 1-1,499 rows, K whole blocks up
+    to 4,096; each vector bit-exact against the restatement."""
+    qk = gpu
+    for M, K, seed in _random_cases(777, 6, 4096, True):
+        rng, mant, exps, _ = _random_planes(M, K, seed)
+        B = int(rng.integers(1, 17))
+        X = np.stack([_random_planes(1, K, seed + 1 + b)[3] for b in range(B)])
+        say("random batch", B, M, K, seed)
+        Y = qk.Bfp8Kernels().gemv_batch(X, mant, exps, M, K)
+        for b in range(B):
+            y_ref, *_ = ol.gemv_neon(X[b], mant, exps)
+            assert same_f32(Y[b], y_ref), (B, M, K, seed, b, mismatch(Y[b], y_ref))
+
+
 @pytest.mark.parametrize("M", [3584, 65536])
 def test_batch16_matches_sixteen_single_calls(gpu, torch_mod, M):
     qk, torch = gpu, torch_mod
