@@ -547,6 +547,63 @@ def test_random_batches_against_the_oracle(gpu, torch_mod):
             assert same_f32(Y[b], y_ref), (B, M, K, seed, b, mismatch(Y[b], y_ref))
 
 
+def test_random_plans_against_the_oracle(gpu, torch_mod):
+    """Six seeded plans of 1-10 GEMVs (1-4,999 rows; K whole blocks up to 4,096
+    or ragged; some sharing an activation tensor), most with one fused lm_head
+    (even vocabularies up to 140,000, hidden 64-1,024, k in 1-64) at a random
+    place in the list: every y bit-exact, the top-k and argmax identical, on
+    two runs."""
+    qk, torch = gpu, torch_mod
+    rng = np.random.default_rng(31337)
+    for p in range(6):
+        items, refs = [], []
+        for j in range(int(rng.integers(1, 11))):
+            M = int(rng.integers(1, 5000))
+            K = int(rng.integers(1, 65)) * 64 if rng.random() < 0.8 else int(rng.integers(64, 4097))
+            seed = int(rng.integers(0, 2**31))
+            if refs and refs[-1][1] == K and rng.random() < 0.5:
+                xd, x = items[-1]["x"], refs[-1][3]  # the same activation tensor
+            else:
+                x = qk.synth_normal(K, seed + 1)
+                xd = torch.from_numpy(x).cuda()
+            items.append({"mat": qk.DeviceMatrix.synth(M, K, seed, 124, 130), "x": xd,
+                          "y": torch.empty(M, dtype=torch.float32, device="cuda")})
+            refs.append((M, K, seed, x))
+        head = None
+        if rng.random() < 0.7:
+            V, H, k = int(rng.integers(1, 70001)) * 2, int(rng.integers(1, 17)) * 64, int(rng.integers(1, 65))
+            seed = int(rng.integers(0, 2**31))
+            x = qk.synth_normal(H, seed + 1)
+            pos = int(rng.integers(0, len(items) + 1))
+            items.insert(pos, {"mat": qk.DeviceMatrix.synth(V, H, seed, 122, 128),
+                               "x": torch.from_numpy(x).cuda(), "topk": k})
+            head = (V, H, k, seed, x)
+        say("random plan", p, [(M, K) for M, K, *_ in refs], head[:3] if head else None)
+        plan = qk.SweepPlan(items)
+        for rep in range(2):
+            for it in items:
+                if "y" in it:
+                    it["y"].fill_(np.nan)
+            plan.run()
+            torch.cuda.synchronize()
+            ys = [it["y"].cpu().numpy() for it in items if "y" in it]
+            for y, (M, K, seed, x) in zip(ys, refs):
+                mant, exps = qk.synth_planes(M, K, seed, 124, 130)
+                y_ref = ol.gemv_neon(x, mant, exps)[0]
+                assert same_f32(y, y_ref), (p, rep, M, K, seed, mismatch(y, y_ref))
+            if head:
+                V, H, k, seed, x = head
+                mant, exps = qk.synth_planes(V, H, seed, 122, 128)
+                y_ref = ol.gemv_neon(x, mant, exps)[0]
+                ids_ref, sc_ref = ol.topk(y_ref, k)
+                ids, sc, cnt = plan.topk_out
+                n = int(cnt[0].item())
+                assert n == ids_ref.size and int(cnt[1].item()) == ol.argmax(y_ref), (p, rep, V, H, k)
+                assert np.array_equal(ids.cpu().numpy()[:n], ids_ref), (p, rep, V, H, k)
+                assert same_f32(sc.cpu().numpy()[:n], sc_ref), (p, rep, V, H, k)
+        plan.close()
+
+
 @pytest.mark.parametrize("M", [3584, 65536])
 def test_batch16_matches_sixteen_single_calls(gpu, torch_mod, M):
     qk, torch = gpu, torch_mod
