@@ -126,6 +126,33 @@ def test_ties_ragged_vocab_and_tail_rules(gpu):
             assert np.array_equal(ids, r_ids) and same_f32(sc, r_sc), (vocab, hidden, k)
 
 
+def test_random_tables_against_the_oracle(gpu):
+    """Eight seeded row-major tables: hidden 1-4,096 (any remainder mod 8),
+    vocabularies up to 40 M elements in all, k in 1-64, half of the tables
+    drawn from three values so that equal scores are common: argmax (tail
+    dropped) and top-k (tail added) identical, scores bit-exact."""
+    qk = gpu
+    lib = qk.load()
+    rng = np.random.default_rng(5150)
+    for i in range(8):
+        hidden = int(rng.integers(1, 4097))
+        vocab = int(rng.integers(1, 40_000_000 // hidden + 1))
+        k = int(rng.integers(1, 65))
+        seed = int(rng.integers(0, 2**31))
+        table, h = table_and_h(vocab, hidden, seed)
+        if i % 2:
+            r = np.random.default_rng(seed + 1)
+            vals = ol.f32_to_bf16_bits(np.array([-0.05, 0.0, 0.05], dtype=F32))
+            table = np.ascontiguousarray(vals[r.integers(0, 3, size=(vocab, hidden))])
+        say("bf16 random", vocab, hidden, k, seed)
+        l0 = ol.bf16_logits(h, table, tail=0)
+        l1 = ol.bf16_logits(h, table, tail=1)
+        assert lib.lm_head_argmax(h.ctypes.data, table.ctypes.data, vocab, hidden) == ol.argmax(l0), (vocab, hidden)
+        ids, sc = host_topk(qk, h, table, k)
+        r_ids, r_sc = ol.topk(l1, k)
+        assert np.array_equal(ids, r_ids) and same_f32(sc, r_sc), (vocab, hidden, k, seed)
+
+
 def test_nan_inf_hidden_state_and_invalid_arguments(gpu):
     qk = gpu
     lib = qk.load()
