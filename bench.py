@@ -184,7 +184,7 @@ def main():
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print("bench.py: this build runs on one GPU; the path shards by rows across GPUs "
+        print("bench.py runs on one GPU only; the path shards by rows across GPUs "
               "(each GPU a contiguous slice of row tiles, the lm_head top-k merged across them), but "
               "multi-GPU runs are not part of it", file=sys.stderr)
         sys.exit(2)

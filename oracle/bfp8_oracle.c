@@ -1,7 +1,7 @@
 /*
  * bfp8_oracle.c -- CPU restatement of the reference's W8A16 BFP8 GEMV path.
  *
- * TEST INFRASTRUCTURE ONLY.  This file is the checker, never the product:
+ * TEST INFRASTRUCTURE ONLY.  This file is the oracle, never the product:
  * only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
  * load the library built from it.  The HIP library never links or calls it.
  *
