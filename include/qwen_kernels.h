@@ -65,8 +65,8 @@ void bfp8_gemv(float* y, const float* x, const int8_t* mantissas, const uint8_t*
  * floats) dotted with h[hidden] in the board build's order (two float32x4
  * accumulators over 8-element chunks, flush-to-zero; hidden % 8 trailing
  * elements dropped), then the lowest id among the maximal scores above -1e30,
- * else 0.  Host pointers; a read-only table is kept on the device after the
- * first call. */
+ * else 0.  Any hidden.  Host pointers; a read-only table is kept on the
+ * device after the first call. */
 int lm_head_argmax(const float* h, const uint16_t* embed_table, int vocab_size, int hidden_dim);
 
 /* Replace the stage profiler, 04/qwen_kernels_opt.c:63-101 (same 15 slots,
@@ -149,11 +149,14 @@ int forward_token_c(int token_id, float* h, const LinearLayerPlan* linear_plans,
 
 /* ---- 2. new host-pointer symbols ------------------------------------------- */
 
-/* Fused BFP8 lm_head: logits = bfp8_gemv(h) over vocab rows (never
- * materialised), then the top k by (score desc, id asc) among logits above
+/* BFP8 lm_head: logits = bfp8_gemv(h) over vocab rows (04/qwen_kernels_opt.c:
+ * 207-326: an odd last row in the scalar order, the float path for
+ * hidden > 4096), then the top k by (score desc, id asc) among logits above
  * -FLT_MAX, exactly the selection of lm_head_topk (04/qwen_sampling.c:283-353).
- * Returns min(k, #candidates); 0 on invalid arguments (k < 1 or k > 64, odd
- * vocab, vocab > 262144, hidden not in [64, 4096]). */
+ * Even vocab, k <= 64 and hidden in [64, 4096] run fused (the logits are
+ * never materialised); other arguments go through the scores and a selection
+ * kernel.  Returns min(k, #candidates); 0 on invalid arguments (k < 1,
+ * vocab < 1 or above 2^28, hidden < 1). */
 int bfp8_lm_head_topk(const float* h, const int8_t* mantissas, const uint8_t* exps, int vocab,
                       int hidden, int k, int* out_ids, float* out_scores);
 
@@ -169,10 +172,24 @@ int bfp8_lm_head_argmax(const float* h, const int8_t* mantissas, const uint8_t* 
 void bfp8_gemv_batch(float* Y, const float* X, const int8_t* mantissas, const uint8_t* exps, int M,
                      int K, int B);
 
+/* Replaces the engine's numpy fallback QwenRealEngine.gemv_bfp8
+ * (04/qwen_real_engine.py:1230-1238, the path it takes when the operator
+ * library lacks bfp8_gemv): y[m] = sum_b (sum_k float(w) * x) * 2^(e-134) with
+ * unquantized x, float32 products and numpy's float32 summation order --
+ * pairwise != 0: numpy >= 1.9 (pairwise_sum: eight accumulators per 128
+ * elements, +0.0 start), pairwise == 0: numpy 1.8.2, the board's (left to
+ * right); 04/qwen_real_engine.py:323-329 names both.  Host pointers,
+ * synchronous; K a multiple of 64 (the engine's reshape requires it).
+ * Returns 0, or a BFP8_E* code (bfp8_last_error says why). */
+int bfp8_gemv_fallback(float* y, const float* x, const int8_t* mantissas, const uint8_t* exps, int M, int K,
+                       int pairwise);
+
 /* The implementations behind libqwen_sampling.so (include/qwen_sampling.h):
- * lm_head_topk over the bf16 table (04/qwen_sampling.c:283-353; k <= 64,
- * else 0 with bfp8_last_error set) and sample_from_topk
- * (04/qwen_sampling.c:384-529; n <= 4096 candidates, else -1). */
+ * lm_head_topk over the bf16 table (04/qwen_sampling.c:283-353; any k and
+ * hidden: k <= 64 fused into the scoring launch, larger k through a sort of
+ * every row's key) and sample_from_topk (04/qwen_sampling.c:384-529; any
+ * n up to 2^28 candidates).  GPU failures return 0 / -1 with bfp8_last_error
+ * set. */
 int qwen_lm_head_topk_bf16(const float* h, const uint16_t* embed_table, int vocab_size, int hidden_dim, int k,
                            int* out_ids, float* out_scores);
 int qwen_sample_from_topk(const int* ids, const float* scores, int n, float temperature, int top_k, float top_p,
@@ -259,23 +276,33 @@ int bfp8_dev_gemv(float* y, const uint32_t* xsplit, const float* xscale, const i
 int bfp8_dev_gemv_float(float* y, const float* x, const int8_t* mant_gpu, const uint8_t* exps_gpu,
                         int M, int K, void* stream);
 
+/* bfp8_gemv_fallback on device buffers (x: K floats, unquantized). */
+int bfp8_dev_gemv_fallback(float* y, const float* x, const int8_t* mant_gpu, const uint8_t* exps_gpu, int M, int K,
+                           int pairwise, void* stream);
+
 /* Batched GEMV: Y[B][M]; xsplit is B consecutive split vectors
  * (bfp8_dev_xsplit_bytes(K) each), xscale B x K/64.  B in 1..16. */
 int bfp8_dev_gemv_batch(float* Y, const uint32_t* xsplit, const float* xscale,
                         const int8_t* mant_gpu, const uint8_t* exps_gpu, int M, int K, int B,
                         void* stream);
 
-/* Fused lm_head on quantized activations: outputs on the device (ids[k],
- * scores[k], count, argmax).  Uses a library-owned device workspace. */
+/* The BFP8 lm_head on quantized activations (hidden <= 4096): outputs on the
+ * device (ids[min(k, vocab)], scores[min(k, vocab)], count, argmax), any
+ * vocab and k as bfp8_lm_head_topk.  Uses library-owned device scratch kept
+ * per stream: calls on one stream are ordered, calls on different streams
+ * use different scratch. */
 int bfp8_dev_lm_head_topk(int* out_ids, float* out_scores, int* out_count, int* out_argmax,
                           const uint32_t* xsplit, const float* xscale, const int8_t* mant_gpu,
                           const uint8_t* exps_gpu, int vocab, int hidden, int k, void* stream);
 
 /* bf16 tied-embedding lm_head on device buffers: scores of every row in the
  * board build's order (tail = 0: hidden % 8 trailing elements dropped, as
- * lm_head_argmax; tail = 1: added, as lm_head_topk), written to logits[vocab]
- * when logits is not NULL; with k in 1..64 also the fused top-k (ids[k],
- * scores[k], count, argmax by the lm_head_argmax rule).  k = 0 needs logits. */
+ * lm_head_argmax; tail = 1: added in IEEE arithmetic, as lm_head_topk),
+ * written to logits[vocab] when logits is not NULL; with k > 0 also the top
+ * k (ids[min(k, vocab)], scores, count, argmax by the lm_head_argmax rule;
+ * k <= 64 fused into the scoring launch).  k = 0 needs logits.  Any hidden
+ * (above 4096 h is read from global memory instead of an LDS copy).
+ * Scratch per stream, as bfp8_dev_lm_head_topk. */
 int bf16_dev_lm_head(int* out_ids, float* out_scores, int* out_count, int* out_argmax, float* logits,
                      const float* h, const uint16_t* embed_table, int vocab, int hidden, int k, int tail,
                      void* stream);
@@ -299,10 +326,12 @@ int bf16_dev_lm_head_tiles(int* out_ids, float* out_scores, int* out_count, int*
                            const float* h, const uint16_t* tiles, int vocab, int hidden, int k, void* stream);
 
 /* sample_from_topk (04/qwen_sampling.c:384-529) on the device: candidates
- * ids[]/scores[] (count from *count when count is not NULL, else n; n is the
- * capacity, at most 4096), xorshift32 state *rng_state updated in place
- * (NULL: greedy ids[0]), chosen id to *out_id.  work: 8*n bytes of device
- * scratch. */
+ * ids[]/scores[] (count from *count when count is not NULL, clamped to
+ * [0, n], else n; n is the capacity, at most 2^28; no candidate gives -1),
+ * xorshift32 state *rng_state updated in place (NULL: ids[0]), chosen id to
+ * *out_id.  work: 8*n bytes of device scratch.  One workgroup: the ordering
+ * and the exponentials in parallel, the double sums and the draw in the
+ * reference's order. */
 int bfp8_dev_sample_from_topk(int* out_id, const int* ids, const float* scores, const int* count, int n,
                               float temperature, int top_k, float top_p, uint32_t* rng_state, void* work,
                               void* stream);

@@ -31,6 +31,10 @@
  *                       order, flush-to-zero cases, float64 bound vs the
  *                       tb_gemv_core golden model
  *   orc_gemv_float      bit-exact vs the reference's own host build (oracle/_ref)
+ *   orc_gemv_fallback   pairwise: bit-exact vs numpy's own np.sum on the
+ *                       engine's expression (the numpy of this image, 2.2.6);
+ *                       sequential: vs np.cumsum's last element (add.accumulate
+ *                       adds left to right in every numpy)
  *   orc_argmax/orc_topk bit-exact vs the reference's own host build of
  *                       lm_head_argmax / lm_head_topk (oracle/_ref), and a
  *                       brute-force (score desc, id asc) sort
@@ -110,6 +114,60 @@ void orc_lane_sums(const int8_t* mant, const int16_t* xq, int M, int K, int32_t*
             for (int j = 0; j < 4; j++) lanes[((size_t)m * nb + b) * 4 + j] = s[j];
         }
     }
+}
+
+/* ---- the engine's numpy fallback, 04/qwen_real_engine.py:1230-1238 -------
+ *   scales = 2 ** (exps - 134)          float32, exact powers of two
+ *   dots   = np.sum(m * x, axis=-1)     per block, float32 products
+ *   y      = np.sum(dots * scales, axis=-1)
+ * in numpy's float32 summation order: pairwise (numpy >= 1.9: +0.0 plus
+ * pairwise_sum, which adds n < 8 elements one by one from -0.0, keeps eight
+ * accumulators up to 128 elements, splits larger n at n/2 rounded down to a
+ * multiple of 8) or sequential (numpy 1.8.2, the board's: a[0] + a[1] + ...).
+ * K % 64 == 0 (the engine's reshape requires it). */
+static float orc_np_pairwise(const float* a, int n) {
+    if (n < 8) {
+        float r = -0.0f;
+        for (int i = 0; i < n; i++) r += a[i];
+        return r;
+    }
+    if (n <= 128) {
+        float r[8];
+        int i;
+        for (int j = 0; j < 8; j++) r[j] = a[j];
+        for (i = 8; i < n - (n % 8); i += 8)
+            for (int j = 0; j < 8; j++) r[j] += a[i + j];
+        float res = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+        for (; i < n; i++) res += a[i];
+        return res;
+    }
+    int n2 = n / 2;
+    n2 -= n2 % 8;
+    return orc_np_pairwise(a, n2) + orc_np_pairwise(a + n2, n - n2);
+}
+
+static float orc_np_sum(const float* a, int n, int pairwise) {
+    if (pairwise) return 0.0f + orc_np_pairwise(a, n);
+    if (n == 0) return 0.0f;
+    float r = a[0];
+    for (int i = 1; i < n; i++) r += a[i];
+    return r;
+}
+
+void orc_gemv_fallback(float* y, const float* x, const int8_t* mant, const uint8_t* exps, int M, int K,
+                       int pairwise) {
+    int nb = K / 64;
+    float* terms = (float*)malloc(sizeof(float) * (size_t)(nb > 0 ? nb : 1));
+    float p[64];
+    for (int m = 0; m < M; m++) {
+        for (int b = 0; b < nb; b++) {
+            const int8_t* blk = mant + (size_t)m * K + (size_t)b * 64;
+            for (int k = 0; k < 64; k++) p[k] = (float)blk[k] * x[b * 64 + k];
+            terms[b] = orc_np_sum(p, 64, pairwise) * ldexpf(1.0f, (int)exps[(size_t)m * nb + b] - 134);
+        }
+        y[m] = orc_np_sum(terms, nb, pairwise);
+    }
+    free(terms);
 }
 
 /* ---- host float path, 04/qwen_kernels_opt.c:311-325 ----------------------

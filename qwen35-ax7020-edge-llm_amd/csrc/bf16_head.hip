@@ -12,7 +12,8 @@
 //                                 a[0..3] is accumulator a0, a[4..7] is a1)
 //   acc[j] = a[j] + a[4+j];  score = (acc[0] + acc[2]) + (acc[1] + acc[3])
 //   hidden % 8 trailing elements: dropped by lm_head_argmax, added one by one
-//   by lm_head_topk (its scalar tail; here in flush-to-zero arithmetic).
+//   by lm_head_topk (its scalar VFP tail: IEEE subnormals, product rounded
+//   then sum rounded, 04/qwen_sampling.c:201-204).
 //
 // Work mapping: a persistent workgroup of 4 wavefronts walks 64-row tiles;
 // wavefront w owns rows 16w..16w+15 of each tile.  A tile is streamed in
@@ -31,6 +32,7 @@
 #include <hip/hip_runtime.h>
 
 #include "bfp8_internal.h"
+#include "ieee_dev.h"
 #include "wave_topk.h"
 
 namespace {
@@ -113,8 +115,10 @@ __device__ __forceinline__ void wait_units(int later) {
 }  // namespace
 
 // Persistent: workgroup b takes tiles b, b + gridDim, ...; kTail adds the
-// hidden % 8 trailing elements (lm_head_topk's scalar tail).
-template <bool kTail>
+// hidden % 8 trailing elements (lm_head_topk's scalar tail).  kHGlobal: h is
+// read from global memory at every chunk instead of an LDS copy of its pairs
+// (hidden sizes whose copy would not fit beside the slice buffers).
+template <bool kTail, bool kHGlobal>
 __global__ __launch_bounds__(kThreads) void bf16_lm_head_kernel(Bf16HeadDesc d) {
     extern __shared__ __align__(16) uint8_t lds_raw[];
     float* score = reinterpret_cast<float*>(lds_raw + kScoreOff);
@@ -126,12 +130,14 @@ __global__ __launch_bounds__(kThreads) void bf16_lm_head_kernel(Bf16HeadDesc d) 
     const int lane = threadIdx.x & 63;
     const int r = lane >> 2, g = lane & 3;
     const int trow = kWaveRows * w + r;  // this lane's row within the tile
-    for (int i = threadIdx.x; i < 4 * nch; i += kThreads) {
-        const int gg = i / nch, c = i % nch;
-        u32x2 v;
-        v.x = __float_as_uint(d.h[8 * c + gg]);
-        v.y = __float_as_uint(d.h[8 * c + 4 + gg]);
-        hpair[gg * nch + c] = v;
+    if (!kHGlobal) {
+        for (int i = threadIdx.x; i < 4 * nch; i += kThreads) {
+            const int gg = i / nch, c = i % nch;
+            u32x2 v;
+            v.x = __float_as_uint(d.h[8 * c + gg]);
+            v.y = __float_as_uint(d.h[8 * c + 4 + gg]);
+            hpair[gg * nch + c] = v;
+        }
     }
     __syncthreads();
     if ((int)blockIdx.x >= ntiles) return;  // uniform per workgroup
@@ -159,7 +165,13 @@ __global__ __launch_bounds__(kThreads) void bf16_lm_head_kernel(Bf16HeadDesc d) 
         for (int ch = 0; ch < sc; ++ch) {
             const uint32_t lo = *reinterpret_cast<const uint32_t*>(rowp + ch * 16 + dw * 4);
             const uint32_t hi = *reinterpret_cast<const uint32_t*>(rowp + ch * 16 + 8 + dw * 4);
-            const u32x2 hp = hp_g[c0 + ch];
+            u32x2 hp;
+            if (kHGlobal) {
+                hp.x = __float_as_uint(d.h[8 * (c0 + ch) + g]);
+                hp.y = __float_as_uint(d.h[8 * (c0 + ch) + 4 + g]);
+            } else {
+                hp = hp_g[c0 + ch];
+            }
             a0 = a0 + __uint_as_float((lo << sh) & 0xFFFF0000u) * __uint_as_float(hp.x);
             a1 = a1 + __uint_as_float((hi << sh) & 0xFFFF0000u) * __uint_as_float(hp.y);
         }
@@ -173,7 +185,8 @@ __global__ __launch_bounds__(kThreads) void bf16_lm_head_kernel(Bf16HeadDesc d) 
                                    0, (int)__float_as_uint(x), 0xB1, 0xF, 0xF, false));  // (acc0+acc2)+(acc1+acc3)
             if (kTail && g == 0 && trow < rows) {
                 const uint16_t* wr = d.table + (size_t)(row0 + trow) * d.hidden;
-                for (int i = nch * 8; i < d.hidden; ++i) sc_row = sc_row + d.h[i] * __uint_as_float((uint32_t)wr[i] << 16);
+                for (int i = nch * 8; i < d.hidden; ++i)
+                    sc_row = ieee_add(sc_row, ieee_mul(d.h[i], __uint_as_float((uint32_t)wr[i] << 16)));
             }
             if (g == 0) {
                 score[trow] = sc_row;
@@ -360,14 +373,20 @@ __global__ __launch_bounds__(256) void bf16_tile_table_kernel(u32x4* __restrict_
 }
 
 // One resident workgroup per CU (the LDS copy takes most of a CU's LDS).
-static size_t head_lds_bytes(int hidden) { return (size_t)kPairOff + (size_t)4 * (hidden >> 3) * 8; }
+static size_t head_lds_bytes(int hidden) {
+    return (size_t)kPairOff + (hidden > kMaxHidden ? (size_t)0 : (size_t)4 * (hidden >> 3) * 8);
+}
 
 static int head_grid(const void* kernel) {
     const int most = (int)head_lds_bytes(kMaxHidden);
     static const bool attr_ok =
-        hipFuncSetAttribute(reinterpret_cast<const void*>(bf16_lm_head_kernel<false>),
+        hipFuncSetAttribute(reinterpret_cast<const void*>(bf16_lm_head_kernel<false, false>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, most) == hipSuccess &&
-        hipFuncSetAttribute(reinterpret_cast<const void*>(bf16_lm_head_kernel<true>),
+        hipFuncSetAttribute(reinterpret_cast<const void*>(bf16_lm_head_kernel<true, false>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, most) == hipSuccess &&
+        hipFuncSetAttribute(reinterpret_cast<const void*>(bf16_lm_head_kernel<false, true>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, most) == hipSuccess &&
+        hipFuncSetAttribute(reinterpret_cast<const void*>(bf16_lm_head_kernel<true, true>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, most) == hipSuccess;
     (void)kernel;
     if (!attr_ok) return 0;
@@ -380,7 +399,6 @@ static int head_grid(const void* kernel) {
 hipError_t bf16_launch_lm_head(const Bf16HeadDesc& d, hipStream_t s) {
     const int ntiles = (d.vocab + kRows - 1) / kRows;
     if (ntiles <= 0) return hipSuccess;
-    if (d.hidden > kMaxHidden) return hipErrorInvalidValue;
     static const int cap = head_grid(nullptr);
     if (cap <= 0) return hipErrorInvalidConfiguration;
     if (d.tiled) {  // one 64-row tile per workgroup
@@ -390,10 +408,15 @@ hipError_t bf16_launch_lm_head(const Bf16HeadDesc& d, hipStream_t s) {
     }
     const int grid = ntiles < cap ? ntiles : cap;
     const size_t lds = head_lds_bytes(d.hidden);
-    if (d.tail && (d.hidden & 7))
-        hipLaunchKernelGGL(bf16_lm_head_kernel<true>, dim3(grid), dim3(kThreads), lds, s, d);
+    const bool tail = d.tail && (d.hidden & 7), hg = d.hidden > kMaxHidden;
+    if (tail && hg)
+        hipLaunchKernelGGL((bf16_lm_head_kernel<true, true>), dim3(grid), dim3(kThreads), lds, s, d);
+    else if (tail)
+        hipLaunchKernelGGL((bf16_lm_head_kernel<true, false>), dim3(grid), dim3(kThreads), lds, s, d);
+    else if (hg)
+        hipLaunchKernelGGL((bf16_lm_head_kernel<false, true>), dim3(grid), dim3(kThreads), lds, s, d);
     else
-        hipLaunchKernelGGL(bf16_lm_head_kernel<false>, dim3(grid), dim3(kThreads), lds, s, d);
+        hipLaunchKernelGGL((bf16_lm_head_kernel<false, false>), dim3(grid), dim3(kThreads), lds, s, d);
     return hipGetLastError();
 }
 

@@ -121,6 +121,74 @@ extern "C" __global__ __launch_bounds__(64) void bfp8_gemv_float_kernel(
     }
 }
 
+// ---- the engine's numpy fallback, 04/qwen_real_engine.py:1230-1238 ------------
+// scales = 2^(e - 134) (float32, exact); products m * x rounded to float32;
+// dots = np.sum(products, axis=-1) per block; y = np.sum(dots * scales, axis=-1).
+// The summation order is numpy's (04/qwen_real_engine.py:323-329 names both):
+//   pairwise (numpy >= 1.9): +0.0 + pairwise_sum(a, n), where pairwise_sum of
+//     n < 8 elements adds them one by one from -0.0, of n <= 128 keeps eight
+//     accumulators r[j] += a[8i + j], combines them as
+//     ((r0 + r1) + (r2 + r3)) + ((r4 + r5) + (r6 + r7)) and adds the n % 8 rest
+//     one by one, and above 128 splits at n/2 rounded down to a multiple of 8;
+//   sequential (numpy 1.8.2, the board's): a[0] + a[1] + ... + a[n-1].
+// One wavefront per row; lanes take blocks, lane 0 sums the block terms.
+__device__ float np_pairwise(const float* a, int n) {
+    if (n < 8) {
+        float r = -0.0f;
+        for (int i = 0; i < n; ++i) r = __fadd_rn(r, a[i]);
+        return r;
+    }
+    if (n <= 128) {
+        float r[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) r[j] = a[j];
+        int i = 8;
+        for (; i < n - (n % 8); i += 8)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) r[j] = __fadd_rn(r[j], a[i + j]);
+        float res = __fadd_rn(__fadd_rn(__fadd_rn(r[0], r[1]), __fadd_rn(r[2], r[3])),
+                              __fadd_rn(__fadd_rn(r[4], r[5]), __fadd_rn(r[6], r[7])));
+        for (; i < n; ++i) res = __fadd_rn(res, a[i]);
+        return res;
+    }
+    int n2 = n / 2;
+    n2 -= n2 % 8;
+    return __fadd_rn(np_pairwise(a, n2), np_pairwise(a + n2, n - n2));
+}
+
+__device__ __forceinline__ float np_sum(const float* a, int n, bool pairwise) {
+    if (pairwise) return __fadd_rn(0.0f, np_pairwise(a, n));
+    if (n == 0) return 0.0f;
+    float r = a[0];
+    for (int i = 1; i < n; ++i) r = __fadd_rn(r, a[i]);
+    return r;
+}
+
+extern "C" __global__ __launch_bounds__(64) void bfp8_gemv_fallback_kernel(
+    float* __restrict__ y, const float* __restrict__ x, const uint8_t* __restrict__ mant,
+    const uint8_t* __restrict__ exps, int M, int K, int pairwise) {
+    extern __shared__ float terms[];
+    const int m = blockIdx.x;
+    const int nb = K >> 6;
+    for (int b = threadIdx.x; b < nb; b += 64) {
+        u32x4 c[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) c[q] = *chunk_ptr(mant, nb, m, b, q);
+        const float* xb = x + (size_t)b * 64;
+        float p[64];
+#pragma unroll
+        for (int k = 0; k < 64; ++k) {
+            const int i = k >> 2;  // element k: residue chunk k & 3, byte k >> 2
+            const uint32_t word = c[k & 3][i >> 2];
+            p[k] = __fmul_rn((float)(int)(int8_t)((word >> (8 * (i & 3))) & 0xffu), xb[k]);
+        }
+        const float dot = np_sum(p, 64, pairwise != 0);
+        terms[b] = __fmul_rn(dot, ldexpf(1.0f, (int)exp_byte(exps, nb, m, b) - 134));
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) y[m] = np_sum(terms, nb, pairwise != 0);
+}
+
 // ---- layout converter: reference SoA planes <-> GPU planes --------------------
 // One thread per (row tile lane, block): reads the 64 mantissas of a block
 // (row stride K, as the engine slices them) and writes the four residue
@@ -236,94 +304,6 @@ extern "C" __global__ __launch_bounds__(256) void bfp8_copy_probe_kernel(
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) dst[i] = src[i];
 }
 
-// ---- sampler (04/qwen_sampling.c:358-529) --------------------------------------------
-// One thread over the candidate list: xorshift32 draw, softmax weights summed
-// in double, top-k / top-p cut, as the reference.  expf is formed as the
-// float rounding of the double exponential (correctly rounded but for
-// results within about 2^-29 ulp of a rounding boundary).
-__device__ __forceinline__ float sample_expf(float x) { return (float)exp((double)x); }
-
-extern "C" __global__ __launch_bounds__(64) void bfp8_sample_kernel(Bfp8SampleArgs a) {
-    if (threadIdx.x != 0) return;
-    const int n = a.count ? *a.count : a.n;
-    if (n <= 0) {
-        *a.out = -1;
-        return;
-    }
-    int* id = a.work_ids;
-    float* sc = a.work_scores;
-    bool sorted = true;
-    for (int i = 0; i < n; ++i) {
-        id[i] = a.ids[i];
-        sc[i] = a.scores[i];
-        if (i > 0 && sc[i] > sc[i - 1]) sorted = false;
-    }
-    if (!a.rng) {
-        *a.out = id[0];
-        return;
-    }
-    if (!sorted) {  // (score desc, id asc)
-        for (int i = 1; i < n; ++i) {
-            const int ci = id[i];
-            const float cs = sc[i];
-            int j = i - 1;
-            while (j >= 0 && (sc[j] < cs || (!(sc[j] > cs) && id[j] > ci))) {
-                id[j + 1] = id[j];
-                sc[j + 1] = sc[j];
-                --j;
-            }
-            id[j + 1] = ci;
-            sc[j + 1] = cs;
-        }
-    }
-    int out = id[0];
-    if (a.temperature >= 1e-6f) {
-        const int m = (a.top_k > 0 && a.top_k < n) ? a.top_k : n;
-        float mx = sc[0];
-        for (int i = 1; i < m; ++i)
-            if (sc[i] > mx) mx = sc[i];
-        const float inv_t = 1.0f / a.temperature;
-        double all = 0.0;
-        for (int i = 0; i < m; ++i) all += (double)sample_expf((sc[i] - mx) * inv_t);
-        if (all > 0.0) {
-            float p = a.top_p;
-            if (!(p > 0.0f)) p = 0.0f;
-            if (p > 1.0f) p = 1.0f;
-            int keep = m;
-            double cum = 0.0;
-            for (int i = 0; i < m; ++i) {
-                cum += (double)sample_expf((sc[i] - mx) * inv_t) / all;
-                if (cum > (double)p) {
-                    keep = i + 1;
-                    break;
-                }
-            }
-            double kept = 0.0;
-            for (int i = 0; i < keep; ++i) kept += (double)sample_expf((sc[i] - mx) * inv_t);
-            if (kept > 0.0) {
-                uint32_t x = *a.rng;
-                if (x == 0u) x = 0x9E3779B9u;
-                x ^= x << 13;
-                x ^= x >> 17;
-                x ^= x << 5;
-                *a.rng = x;
-                const double r = (double)((float)(x >> 8) * (1.0f / 16777216.0f)) * kept;
-                int pick = keep - 1;
-                cum = 0.0;
-                for (int i = 0; i < keep; ++i) {
-                    cum += (double)sample_expf((sc[i] - mx) * inv_t);
-                    if (r < cum) {
-                        pick = i;
-                        break;
-                    }
-                }
-                out = id[pick];
-            }
-        }
-    }
-    *a.out = out;
-}
-
 // ---- launchers ----------------------------------------------------------------------
 static int grid_for(size_t work, int per_block) {
     size_t g = (work + per_block - 1) / per_block;
@@ -360,6 +340,16 @@ hipError_t bfp8_launch_gemv_float(float* y, const float* x, const uint8_t* mant,
     if (nb > 16384) return hipErrorInvalidValue;
     hipLaunchKernelGGL(bfp8_gemv_float_kernel, dim3(M), dim3(64), (size_t)(nb > 0 ? nb : 1) * 4, s, y, x,
                        mant, exps, M, K);
+    return hipGetLastError();
+}
+
+hipError_t bfp8_launch_gemv_fallback(float* y, const float* x, const uint8_t* mant, const uint8_t* exps, int M,
+                                     int K, int pairwise, hipStream_t s) {
+    if (M <= 0) return hipSuccess;
+    const int nb = bfp8_nblocks(K);
+    if (nb > 16384) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(bfp8_gemv_fallback_kernel, dim3(M), dim3(64), (size_t)(nb > 0 ? nb : 1) * 4, s, y, x, mant,
+                       exps, M, K, pairwise);
     return hipGetLastError();
 }
 
@@ -400,11 +390,6 @@ hipError_t bfp8_launch_synth_planes(int8_t* mant_soa, uint8_t* exps_soa, int M, 
     const size_t nm = (size_t)M * K, ne = (size_t)M * bfp8_nblocks(K);
     hipLaunchKernelGGL(bfp8_synth_kernel, dim3(grid_for(nm, 256 * 16)), dim3(256), 0, s, mant_soa, exps_soa, nm,
                        ne, seed, e_lo, e_hi);
-    return hipGetLastError();
-}
-
-hipError_t bfp8_launch_sample(const Bfp8SampleArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL(bfp8_sample_kernel, dim3(1), dim3(64), 0, s, a);
     return hipGetLastError();
 }
 

@@ -56,19 +56,18 @@ struct Bf16HeadDesc {
     int tiled;              // 1: table in the 64-row tile layout (bf16_launch_tile_table)
 };
 
-// The sampler over a sorted candidate list (bfp8_ieee.hip).
+// The sampler over a candidate list (select.hip).
 struct Bfp8SampleArgs {
     const int* ids;
     const float* scores;
-    const int* count;       // device candidate count, or null to use n
-    int n;
+    const int* count;       // device candidate count (clamped to [0, n]), or null to use n
+    int n;                  // capacity of ids / scores / work
     float temperature;
     int top_k;
     float top_p;
-    uint32_t* rng;          // xorshift32 state, updated in place (null: greedy)
+    uint32_t* rng;          // xorshift32 state, updated in place (null: ids[0])
     int* out;               // chosen id
-    int* work_ids;          // n-entry scratch
-    float* work_scores;
+    void* work;             // 8 * n bytes of scratch
 };
 
 // Grouped-launch work item: which descriptor and which row tile.
@@ -79,7 +78,7 @@ struct Bfp8TileRef {
 
 #define BFP8_TOPK_MAX 64
 #define BFP8_TOPK_MAX_TILES 4096
-#define BFP8_SAMPLE_MAX 4096  // candidates the sampler takes
+#define BFP8_SELECT_MAX (1 << 28)  // entries the sort-based selection and the sampler take
 #define BF16_HEAD_MAX_HIDDEN 4096  // hidden size of the bf16 lm_head (LDS copy of h)
 #define BFP8_STREAM_WG_PER_CU 4
 // Row tiles up to which a GEMV (or a plan's GEMVs) runs one tile per
@@ -145,14 +144,28 @@ bool bf16_tiled_ok(int hidden);
 size_t bf16_tiled_elems(int vocab, int hidden);
 hipError_t bf16_launch_tile_table(uint16_t* dst, const uint16_t* src, int vocab, int hidden, hipStream_t s);
 
-// ---- bfp8_ieee.hip -------------------------------------------------------
+// ---- select.hip ----------------------------------------------------------
+// Per-tile top-`topk` partials ([ntiles(n)][topk] keys) of logits[0, n), for
+// bfp8_launch_topk_merge (topk <= BFP8_TOPK_MAX).
+hipError_t bfp8_launch_select_partials(const float* logits, int n, int topk, uint64_t* partials, hipStream_t s);
+// The kk best of logits[0, n) by sorting all n keys (keys: n entries of
+// scratch): ids / scores [kk], count, argmax as the merge writes them.
+hipError_t bfp8_launch_select_sort(const float* logits, int n, int kk, uint64_t* keys, int* ids, float* scores,
+                                   int* count, int* argmax, hipStream_t s);
 hipError_t bfp8_launch_sample(const Bfp8SampleArgs& a, hipStream_t s);
+
+// ---- bfp8_ieee.hip -------------------------------------------------------
 hipError_t bfp8_launch_quantize(const Bfp8QuantDesc* descs_dev, int ndesc, int max_nb, hipStream_t s);
 hipError_t bfp8_launch_quantize1(const Bfp8QuantDesc& d, hipStream_t s);
 hipError_t bfp8_launch_tail_row(float* y, const uint32_t* xsplit, const float* xscale,
                                 const uint8_t* mant, const uint8_t* exps, int M, int K, hipStream_t s);
 hipError_t bfp8_launch_gemv_float(float* y, const float* x, const uint8_t* mant, const uint8_t* exps,
                                   int M, int K, hipStream_t s);
+// The engine's numpy fallback (04/qwen_real_engine.py:1230-1238): unquantized
+// x, float32 products, numpy's summation order (pairwise: numpy >= 1.9;
+// else sequential: numpy 1.8.2).  K % 64 == 0.
+hipError_t bfp8_launch_gemv_fallback(float* y, const float* x, const uint8_t* mant, const uint8_t* exps, int M,
+                                     int K, int pairwise, hipStream_t s);
 hipError_t bfp8_launch_pack(uint8_t* mant_gpu, uint8_t* exps_gpu, const int8_t* mant_soa,
                             const uint8_t* exps_soa, int M, int K, hipStream_t s);
 // Row r's mantissas at mant_src + r*mant_stride, its exponents at

@@ -81,6 +81,7 @@ struct DevBuf {
 struct Bf16Table {
     DevBuf buf;
     int tiled = 0;
+    uint64_t fp = 0;  // content fingerprint at conversion (content_fingerprint)
 };
 
 struct PinnedBuf {
@@ -100,9 +101,26 @@ struct PinnedBuf {
 
 struct CachedWeights {
     DevBuf mant, exps;
+    uint64_t fp = 0;  // content fingerprint of both planes at conversion
 };
 
+// A cheap fingerprint of host memory [p, p+n): the first and last 64 bytes
+// and 32 evenly spaced 8-byte words, hashed with the length.  A cached device
+// copy is checked against it on every hit, so a buffer that was unmapped and
+// replaced at the same address (a model reload) or rewritten is converted
+// again instead of being served stale; changes that touch none of the sampled
+// bytes still need bfp8_cache_clear().
+uint64_t content_fingerprint(const void* p, size_t n);
+
 using WeightKey = std::tuple<const void*, const void*, int, int>;
+
+// Device scratch of the lm_head selections, one set per HIP stream: work on
+// one stream is ordered, so calls on different streams never share partials.
+struct StreamScratch {
+    DevBuf partials;  // per-tile top-k lists
+    DevBuf logits;    // scores of every row (general selection path)
+    DevBuf keys;      // sort keys (k > BFP8_TOPK_MAX)
+};
 
 struct State {
     std::mutex mu;
@@ -112,7 +130,8 @@ struct State {
     PinnedBuf h_in, h_out;
     DevBuf x, xq, xscale, xsplit, y;            // activation / output workspace
     DevBuf soa_m, soa_e, gpu_m, gpu_e;          // per-call weight upload
-    DevBuf tk_partials, tk_out;                 // fused lm_head workspace
+    DevBuf tk_out;                              // lm_head outputs of the host-pointer calls
+    std::map<hipStream_t, StreamScratch> scratch;  // lm_head selection scratch per stream
     DevBuf bf16_ws;                             // per-call bf16 table upload
     DevBuf smp_in, smp_work, smp_out;           // sampler inputs / scratch / outputs
     PinnedBuf smp_h;
@@ -121,6 +140,9 @@ struct State {
     std::map<WeightKey, CachedWeights> cache;
     std::map<WeightKey, Bf16Table> bf16_cache;  // read-only bf16 embedding tables
     size_t cache_bytes = 0;
+    // ranges found writable by a /proc/self/maps scan: not scanned again
+    // (such weights are uploaded per call either way)
+    std::map<std::pair<const void*, size_t>, bool> writable;
 };
 
 extern State g;
@@ -131,6 +153,11 @@ int ensure_init_locked();
 inline hipStream_t pick_stream(void* s) { return static_cast<hipStream_t>(s); }
 // Is every page of [p, p+n) mapped without write permission?
 bool range_readonly(const void* p, size_t n);
+// range_readonly, remembering a "writable" answer per (p, n) until
+// bfp8_cache_clear(); g.mu held.
+bool range_readonly_cached(const void* p, size_t n);
+// The cached device copy of a bf16 table, if any (fingerprint checked).
+bool bf16_table_lookup(const uint16_t* table, int vocab, int hidden, const uint16_t** out, int* tiled);
 
 struct DevWeights {
     const uint8_t* mant;
@@ -156,6 +183,14 @@ int bf16_lm_head_dev(int* ids, float* scores, int* count, int* argmax, float* lo
                      const uint16_t* table, int tiled, int vocab, int hidden, int k, int tail, hipStream_t s);
 Bfp8GemvDesc plain_desc(float* y, const uint32_t* xsplit, const float* xscale, const uint8_t* m,
                         const uint8_t* e, int M, int K, int32_t* lanes);
+// The lm_head selection scratch of stream s; g.mu held.
+StreamScratch& scratch_for(hipStream_t s);
+// The kk best rows of logits[0, n) by (score desc, id asc) among scores above
+// -FLT_MAX into device outputs ids / scores [kk], count, argmax (the
+// lm_head_argmax rule), on stream s: per-tile partials and the merge kernel
+// for kk <= BFP8_TOPK_MAX, else a sort of all n keys.  g.mu held.
+int select_topk_dev(const float* logits, int n, int kk, int* ids, float* scores, int* count, int* argmax,
+                    hipStream_t s);
 
 // One grouped launch: its tile table, either dealt over a persistent grid
 // (wg_off per workgroup) or one tile per 16-wavefront workgroup (wide).

@@ -105,6 +105,33 @@ bool range_readonly(const void* p, size_t n) {
     return ok;
 }
 
+bool range_readonly_cached(const void* p, size_t n) {
+    const auto key = std::make_pair(p, n);
+    if (g.writable.count(key)) return false;
+    const bool ro = range_readonly(p, n);
+    if (!ro) g.writable.emplace(key, true);
+    return ro;
+}
+
+uint64_t content_fingerprint(const void* p, size_t n) {
+    const unsigned char* b = static_cast<const unsigned char*>(p);
+    uint64_t h = 0xcbf29ce484222325ull ^ (uint64_t)n;
+    auto mix = [&h](const unsigned char* q, size_t len) {
+        for (size_t i = 0; i < len; ++i) h = (h ^ q[i]) * 0x100000001b3ull;
+    };
+    if (!b || n == 0) return h;
+    const size_t edge = std::min<size_t>(n, 64);
+    mix(b, edge);
+    mix(b + (n - edge), edge);
+    if (n >= 8)
+        for (size_t i = 0; i < 32; ++i) mix(b + (i * (n - 8)) / 31, 8);
+    return h;
+}
+
+static uint64_t planes_fingerprint(const int8_t* mant, size_t mbytes, const uint8_t* exps, size_t ebytes) {
+    return content_fingerprint(mant, mbytes) * 31 + content_fingerprint(exps, ebytes);
+}
+
 // Device GPU-layout planes for host reference planes.
 int weights_cached(const int8_t* mant, const uint8_t* exps, int M, int K, bool force, DevWeights* out) {
     const int nb = bfp8_nblocks(K);
@@ -112,9 +139,17 @@ int weights_cached(const int8_t* mant, const uint8_t* exps, int M, int K, bool f
     const WeightKey key{mant, exps, M, K};
     auto it = g.cache.find(key);
     if (it != g.cache.end()) {
-        out->mant = it->second.mant.as<uint8_t>();
-        out->exps = it->second.exps.as<uint8_t>();
-        return BFP8_OK;
+        if (it->second.fp == planes_fingerprint(mant, mbytes, exps, ebytes)) {
+            out->mant = it->second.mant.as<uint8_t>();
+            out->exps = it->second.exps.as<uint8_t>();
+            return BFP8_OK;
+        }
+        // the memory behind the cached address changed: convert again
+        HIP_OK(hipStreamSynchronize(g.stream));
+        g.cache_bytes -= it->second.mant.n + it->second.exps.n;
+        it->second.mant.release();
+        it->second.exps.release();
+        g.cache.erase(it);
     }
     int rc;
     if ((rc = g.soa_m.reserve(mbytes)) || (rc = g.soa_e.reserve(ebytes))) return rc;
@@ -122,7 +157,7 @@ int weights_cached(const int8_t* mant, const uint8_t* exps, int M, int K, bool f
     HIP_OK(hipMemcpyAsync(g.soa_e.p, exps, ebytes, hipMemcpyHostToDevice, g.stream));
     const size_t gm = bfp8_gpu_mant_bytes(M, K), ge = bfp8_gpu_exps_bytes(M, K);
     const bool cacheable = g.cache_bytes + gm + ge <= kCacheLimit &&
-                           (force || (range_readonly(mant, mbytes) && range_readonly(exps, ebytes)));
+                           (force || (range_readonly_cached(mant, mbytes) && range_readonly_cached(exps, ebytes)));
     if (force && !cacheable) {
         set_error("device weight cache full (%zu bytes)", g.cache_bytes);
         return BFP8_EINVAL;
@@ -140,6 +175,7 @@ int weights_cached(const int8_t* mant, const uint8_t* exps, int M, int K, bool f
     out->mant = dm->as<uint8_t>();
     out->exps = de->as<uint8_t>();
     if (cacheable) {
+        cw.fp = planes_fingerprint(mant, mbytes, exps, ebytes);
         g.cache_bytes += cw.mant.n + cw.exps.n;
         g.cache.emplace(key, cw);
     }
@@ -156,18 +192,29 @@ int upload_x(const float* x, size_t nfloat);
 // read-only memory (the engine's mmap) or when forced, else uploaded per call.
 // A cached table whose width the tile kernel takes is converted once, on the
 // device, into the tile layout (the row-major upload goes through bf16_ws).
+bool bf16_table_lookup(const uint16_t* table, int vocab, int hidden, const uint16_t** out, int* tiled) {
+    const size_t bytes = (size_t)vocab * (size_t)hidden * 2;
+    auto it = g.bf16_cache.find(WeightKey{table, nullptr, vocab, hidden});
+    if (it == g.bf16_cache.end()) return false;
+    if (it->second.fp != content_fingerprint(table, bytes)) {  // replaced or rewritten: convert again
+        (void)hipStreamSynchronize(g.stream);
+        g.cache_bytes -= it->second.buf.n;
+        it->second.buf.release();
+        g.bf16_cache.erase(it);
+        return false;
+    }
+    *out = it->second.buf.as<uint16_t>();
+    *tiled = it->second.tiled;
+    return true;
+}
+
 int bf16_table_cached(const uint16_t* table, int vocab, int hidden, bool force, const uint16_t** out, int* tiled) {
     const size_t bytes = (size_t)vocab * (size_t)hidden * 2;
     const WeightKey key{table, nullptr, vocab, hidden};
-    auto it = g.bf16_cache.find(key);
-    if (it != g.bf16_cache.end()) {
-        *out = it->second.buf.as<uint16_t>();
-        *tiled = it->second.tiled;
-        return BFP8_OK;
-    }
+    if (bf16_table_lookup(table, vocab, hidden, out, tiled)) return BFP8_OK;
     const bool tile = bf16_tiled_ok(hidden);
     const size_t kept = tile ? bf16_tiled_elems(vocab, hidden) * 2 : bytes;
-    const bool cacheable = g.cache_bytes + kept <= kCacheLimit && (force || range_readonly(table, bytes));
+    const bool cacheable = g.cache_bytes + kept <= kCacheLimit && (force || range_readonly_cached(table, bytes));
     int rc;
     if (!cacheable) {
         if ((rc = g.bf16_ws.reserve(bytes))) return rc;
@@ -191,6 +238,7 @@ int bf16_table_cached(const uint16_t* table, int vocab, int hidden, bool force, 
     }
     *out = fresh.buf.as<uint16_t>();
     *tiled = fresh.tiled;
+    fresh.fp = content_fingerprint(table, bytes);
     g.cache_bytes += fresh.buf.n;
     g.bf16_cache.emplace(key, fresh);
     return BFP8_OK;
@@ -200,22 +248,73 @@ int bf16_table_for(const uint16_t* table, int vocab, int hidden, const uint16_t*
     return bf16_table_cached(table, vocab, hidden, false, out, tiled);
 }
 
-// bf16 lm_head scores (+ fused top-k) on device buffers.
+StreamScratch& scratch_for(hipStream_t s) { return g.scratch[s]; }
+
+// Selection with the caller's scratch: partials (bfp8_ntiles(n) * kk keys)
+// when kk <= BFP8_TOPK_MAX, else keys (n keys).  Allocates nothing.
+int select_topk_raw(const float* logits, int n, int kk, int* ids, float* scores, int* count, int* argmax,
+                    uint64_t* partials, uint64_t* keys, hipStream_t s) {
+    if (kk <= BFP8_TOPK_MAX) {
+        HIP_OK(bfp8_launch_select_partials(logits, n, kk, partials, s));
+        Bfp8GemvDesc md{};
+        md.M = n;
+        md.topk = kk;
+        md.partials = partials;
+        md.out_ids = ids;
+        md.out_scores = scores;
+        md.out_count = count;
+        md.out_argmax = argmax;
+        HIP_OK(bfp8_launch_topk_merge(md, s));
+        return BFP8_OK;
+    }
+    HIP_OK(bfp8_launch_select_sort(logits, n, kk, keys, ids, scores, count, argmax, s));
+    return BFP8_OK;
+}
+
+int select_topk_bufs(const float* logits, int n, int kk, int* ids, float* scores, int* count, int* argmax,
+                     DevBuf& partials, DevBuf& keys, hipStream_t s) {
+    int rc;
+    if (kk <= BFP8_TOPK_MAX) {
+        if ((rc = partials.reserve((size_t)bfp8_ntiles(n) * kk * 8))) return rc;
+    } else if ((rc = keys.reserve((size_t)n * 8))) {
+        return rc;
+    }
+    return select_topk_raw(logits, n, kk, ids, scores, count, argmax, partials.as<uint64_t>(), keys.as<uint64_t>(), s);
+}
+
+int select_topk_dev(const float* logits, int n, int kk, int* ids, float* scores, int* count, int* argmax,
+                    hipStream_t s) {
+    StreamScratch& ss = scratch_for(s);
+    return select_topk_bufs(logits, n, kk, ids, scores, count, argmax, ss.partials, ss.keys, s);
+}
+
+// bf16 lm_head scores (+ top-k) on device buffers: k <= BFP8_TOPK_MAX fused
+// into the scoring launch (per-tile lists, then the merge), larger k through
+// the scores and a sort.
 int bf16_lm_head_dev(int* ids, float* scores, int* count, int* argmax, float* logits, const float* h,
                      const uint16_t* table, int tiled, int vocab, int hidden, int k, int tail, hipStream_t s) {
     const int kk = k > 0 ? std::min(k, vocab) : 0;
+    StreamScratch& ss = scratch_for(s);
     int rc;
-    if (kk > 0 && (rc = g.tk_partials.reserve((size_t)bfp8_ntiles(vocab) * kk * 8))) return rc;
     Bf16HeadDesc d{};
     d.table = table;
     d.h = h;
     d.logits = logits;
-    d.partials = kk > 0 ? g.tk_partials.as<uint64_t>() : nullptr;
     d.vocab = vocab;
     d.hidden = hidden;
-    d.topk = kk;
     d.tail = tail;
     d.tiled = tiled;
+    if (kk > BFP8_TOPK_MAX) {
+        if (!logits) {
+            if ((rc = ss.logits.reserve((size_t)vocab * 4))) return rc;
+            d.logits = ss.logits.as<float>();
+        }
+        HIP_OK(bf16_launch_lm_head(d, s));
+        return select_topk_dev(d.logits, vocab, kk, ids, scores, count, argmax, s);
+    }
+    if (kk > 0 && (rc = ss.partials.reserve((size_t)bfp8_ntiles(vocab) * kk * 8))) return rc;
+    d.partials = kk > 0 ? ss.partials.as<uint64_t>() : nullptr;
+    d.topk = kk;
     HIP_OK(bf16_launch_lm_head(d, s));
     if (kk > 0) {
         Bfp8GemvDesc md{};
@@ -240,21 +339,21 @@ int host_bf16_lm_head(const float* h, const uint16_t* table, int vocab, int hidd
     int tiled = 0;
     if ((rc = bf16_table_for(table, vocab, hidden, &tdev, &tiled)) || (rc = upload_x(h, (size_t)hidden))) return rc;
     const int kk = std::min(k, vocab);
-    if ((rc = g.tk_out.reserve((size_t)(2 * BFP8_TOPK_MAX + 2) * 4)) || (rc = g.h_out.reserve((size_t)(2 * BFP8_TOPK_MAX + 2) * 4)))
-        return rc;
+    const size_t outb = (size_t)(2 * kk + 2) * 4;
+    if ((rc = g.tk_out.reserve(outb)) || (rc = g.h_out.reserve(outb))) return rc;
     int* d_ids = g.tk_out.as<int>();
-    float* d_sc = reinterpret_cast<float*>(d_ids + BFP8_TOPK_MAX);
-    int* d_cnt = d_ids + 2 * BFP8_TOPK_MAX;
+    float* d_sc = reinterpret_cast<float*>(d_ids + kk);
+    int* d_cnt = d_ids + 2 * kk;
     if ((rc = bf16_lm_head_dev(d_ids, d_sc, d_cnt, d_cnt + 1, nullptr, g.x.as<float>(), tdev, tiled, vocab, hidden,
                                kk, tail, g.stream)))
         return rc;
-    HIP_OK(hipMemcpyAsync(g.h_out.p, g.tk_out.p, (size_t)(2 * BFP8_TOPK_MAX + 2) * 4, hipMemcpyDeviceToHost, g.stream));
+    HIP_OK(hipMemcpyAsync(g.h_out.p, g.tk_out.p, outb, hipMemcpyDeviceToHost, g.stream));
     HIP_OK(hipStreamSynchronize(g.stream));
     const int* hi = static_cast<const int*>(g.h_out.p);
-    const int n = hi[2 * BFP8_TOPK_MAX];
-    if (am) *am = hi[2 * BFP8_TOPK_MAX + 1];
+    const int n = hi[2 * kk];
+    if (am) *am = hi[2 * kk + 1];
     if (out_ids && n > 0) memcpy(out_ids, hi, (size_t)n * 4);
-    if (out_scores && n > 0) memcpy(out_scores, hi + BFP8_TOPK_MAX, (size_t)n * 4);
+    if (out_scores && n > 0) memcpy(out_scores, hi + kk, (size_t)n * 4);
     return n;
 }
 
@@ -332,6 +431,31 @@ int rows_gemv_float(float* y, const float* x, const uint8_t* m, const uint8_t* e
     return BFP8_OK;
 }
 
+// y_dev[M] = bfp8_gemv(x) for x already in g.x (K floats), on g.stream: the
+// quantized path for K <= 4096 (whole blocks; an odd last row in the scalar
+// order), the float path above; no whole block gives zeros.
+int gemv_from_x(float* y_dev, const DevWeights& w, int M, int K) {
+    const int nb = bfp8_nblocks(K);
+    int rc;
+    if (nb == 0) {
+        HIP_OK(hipMemsetAsync(y_dev, 0, (size_t)M * 4, g.stream));
+    } else if (K <= 4096 && bfp8_ntiles(M) <= BFP8_WIDE_MAX_TILES) {
+        // one launch: the 16-row kernel quantizes x itself
+        if ((rc = g.xscale.reserve((size_t)nb * 4)) || (rc = g.xsplit.reserve(bfp8_xsplit_bytes(K)))) return rc;
+        if ((rc = rows_gemv_float(y_dev, g.x.as<float>(), w.mant, w.exps, M, K, g.xsplit.as<uint32_t>(),
+                                  g.xscale.as<float>(), g.stream)))
+            return rc;
+    } else if (K <= 4096) {
+        if ((rc = quantize_ws(K, 1))) return rc;
+        if ((rc = gemv_q(y_dev, g.xsplit.as<uint32_t>(), g.xscale.as<float>(), w.mant, w.exps, M, K, nullptr,
+                         g.stream)))
+            return rc;
+    } else {
+        HIP_OK(bfp8_launch_gemv_float(y_dev, g.x.as<float>(), w.mant, w.exps, M, K, g.stream));
+    }
+    return BFP8_OK;
+}
+
 int host_gemv(float* y, const float* x, const int8_t* mant, const uint8_t* exps, int M, int K) {
     const int nb = bfp8_nblocks(K);
     if (nb == 0) {  // no whole block: the reference's accumulators stay 0
@@ -341,42 +465,47 @@ int host_gemv(float* y, const float* x, const int8_t* mant, const uint8_t* exps,
     int rc;
     DevWeights w;
     if ((rc = weights_for(mant, exps, M, K, &w))) return rc;
-    if ((rc = upload_x(x, (size_t)nb * 64))) return rc;
+    if ((rc = upload_x(x, (size_t)(K <= 4096 ? nb * 64 : K)))) return rc;
     if ((rc = g.y.reserve((size_t)M * 4)) || (rc = g.h_out.reserve((size_t)M * 4))) return rc;
-    if (K <= 4096 && bfp8_ntiles(M) <= BFP8_WIDE_MAX_TILES) {
-        // one launch: the 16-row kernel quantizes x itself
-        if ((rc = g.xscale.reserve((size_t)nb * 4)) || (rc = g.xsplit.reserve(bfp8_xsplit_bytes(K)))) return rc;
-        if ((rc = rows_gemv_float(g.y.as<float>(), g.x.as<float>(), w.mant, w.exps, M, K, g.xsplit.as<uint32_t>(),
-                                  g.xscale.as<float>(), g.stream)))
-            return rc;
-    } else if (K <= 4096) {
-        if ((rc = quantize_ws(K, 1))) return rc;
-        if ((rc = gemv_q(g.y.as<float>(), g.xsplit.as<uint32_t>(), g.xscale.as<float>(), w.mant, w.exps,
-                         M, K, nullptr, g.stream)))
-            return rc;
-    } else {
-        HIP_OK(bfp8_launch_gemv_float(g.y.as<float>(), g.x.as<float>(), w.mant, w.exps, M, K, g.stream));
-    }
+    if ((rc = gemv_from_x(g.y.as<float>(), w, M, K))) return rc;
     HIP_OK(hipMemcpyAsync(g.h_out.p, g.y.p, (size_t)M * 4, hipMemcpyDeviceToHost, g.stream));
     HIP_OK(hipStreamSynchronize(g.stream));
     memcpy(y, g.h_out.p, (size_t)M * 4);
     return BFP8_OK;
 }
 
-bool lm_head_args_ok(int vocab, int hidden, int k) {
+// The fused BFP8 lm_head launch takes: even vocab (every row in a pair),
+// k <= BFP8_TOPK_MAX, a quantized activation (hidden 64 .. 4096).  Other
+// arguments take the general path: the plain GEMV (odd last row included,
+// the float path above 4096) into a scores buffer, then the selection.
+bool lm_head_fused_ok(int vocab, int hidden, int kk) {
     return vocab > 0 && !(vocab & 1) && bfp8_ntiles(vocab) <= BFP8_TOPK_MAX_TILES && hidden >= 64 &&
-           hidden <= 4096 && k >= 1 && k <= BFP8_TOPK_MAX;
+           hidden <= 4096 && kk >= 1 && kk <= BFP8_TOPK_MAX;
+}
+
+bool lm_head_args_ok(int vocab, int hidden, int k) {
+    return vocab > 0 && vocab <= BFP8_SELECT_MAX && hidden > 0 && k >= 1;
 }
 
 int lm_head_dev(int* ids, float* scores, int* count, int* argmax, const uint32_t* xsplit,
                 const float* xscale, const uint8_t* m, const uint8_t* e, int vocab, int hidden, int k,
                 hipStream_t s) {
     const int kk = std::min(k, vocab);
+    StreamScratch& ss = scratch_for(s);
     int rc;
-    if ((rc = g.tk_partials.reserve((size_t)bfp8_ntiles(vocab) * kk * 8))) return rc;
+    if (!lm_head_fused_ok(vocab, hidden, kk)) {  // general path (hidden <= 4096: a quantized activation)
+        if ((rc = ss.logits.reserve((size_t)vocab * 4))) return rc;
+        float* lg = ss.logits.as<float>();
+        if (bfp8_nblocks(hidden) == 0)
+            HIP_OK(hipMemsetAsync(lg, 0, (size_t)vocab * 4, s));
+        else if ((rc = gemv_q(lg, xsplit, xscale, m, e, vocab, hidden, nullptr, s)))
+            return rc;
+        return select_topk_dev(lg, vocab, kk, ids, scores, count, argmax, s);
+    }
+    if ((rc = ss.partials.reserve((size_t)bfp8_ntiles(vocab) * kk * 8))) return rc;
     Bfp8GemvDesc d = plain_desc(nullptr, xsplit, xscale, m, e, vocab, hidden, nullptr);
     d.topk = kk;
-    d.partials = g.tk_partials.as<uint64_t>();
+    d.partials = ss.partials.as<uint64_t>();
     d.out_ids = ids;
     d.out_scores = scores;
     d.out_count = count;
@@ -391,17 +520,26 @@ int host_lm_head(const float* h, const int8_t* mant, const uint8_t* exps, int vo
     DevWeights w;
     if ((rc = weights_for(mant, exps, vocab, hidden, &w))) return rc;
     const int nb = bfp8_nblocks(hidden);
-    if ((rc = upload_x(h, (size_t)nb * 64)) || (rc = quantize_ws(hidden, 1))) return rc;
     const int kk = std::min(k, vocab);
-    if ((rc = g.tk_out.reserve((size_t)(2 * kk + 2) * 4)) || (rc = g.h_out.reserve((size_t)(2 * kk + 2) * 4)))
-        return rc;
+    const size_t outb = (size_t)(2 * kk + 2) * 4;
+    if ((rc = g.tk_out.reserve(outb)) || (rc = g.h_out.reserve(outb))) return rc;
     int* d_ids = g.tk_out.as<int>();
     float* d_scores = reinterpret_cast<float*>(d_ids + kk);
     int* d_cnt = d_ids + 2 * kk;
-    if ((rc = lm_head_dev(d_ids, d_scores, d_cnt, d_cnt + 1, g.xsplit.as<uint32_t>(), g.xscale.as<float>(),
-                          w.mant, w.exps, vocab, hidden, kk, g.stream)))
-        return rc;
-    HIP_OK(hipMemcpyAsync(g.h_out.p, g.tk_out.p, (size_t)(2 * kk + 2) * 4, hipMemcpyDeviceToHost, g.stream));
+    if ((rc = upload_x(h, (size_t)(hidden <= 4096 ? nb * 64 : hidden)))) return rc;
+    if (lm_head_fused_ok(vocab, hidden, kk)) {
+        if ((rc = quantize_ws(hidden, 1))) return rc;
+        if ((rc = lm_head_dev(d_ids, d_scores, d_cnt, d_cnt + 1, g.xsplit.as<uint32_t>(), g.xscale.as<float>(),
+                              w.mant, w.exps, vocab, hidden, kk, g.stream)))
+            return rc;
+    } else {  // the plain GEMV's scores, then the selection
+        StreamScratch& ss = scratch_for(g.stream);
+        if ((rc = ss.logits.reserve((size_t)vocab * 4))) return rc;
+        if ((rc = gemv_from_x(ss.logits.as<float>(), w, vocab, hidden))) return rc;
+        if ((rc = select_topk_dev(ss.logits.as<float>(), vocab, kk, d_ids, d_scores, d_cnt, d_cnt + 1, g.stream)))
+            return rc;
+    }
+    HIP_OK(hipMemcpyAsync(g.h_out.p, g.tk_out.p, outb, hipMemcpyDeviceToHost, g.stream));
     HIP_OK(hipStreamSynchronize(g.stream));
     const int* hi = static_cast<const int*>(g.h_out.p);
     const int cnt = hi[2 * kk];
@@ -505,6 +643,31 @@ void bfp8_gemv_batch(float* Y, const float* X, const int8_t* mantissas, const ui
     memcpy(Y, g.h_out.p, (size_t)B * M * 4);
 }
 
+int bfp8_gemv_fallback(float* y, const float* x, const int8_t* mantissas, const uint8_t* exps, int M, int K,
+                       int pairwise) {
+    if (M < 0 || K < 0 || (K & 63) || bfp8_nblocks(K) > 16384 || (M > 0 && (!y || (K > 0 && (!x || !mantissas || !exps))))) {
+        set_error("bfp8_gemv_fallback: invalid arguments (K must be a multiple of 64)");
+        return BFP8_EINVAL;
+    }
+    if (M == 0) return BFP8_OK;
+    std::lock_guard<std::mutex> lk(g.mu);
+    int rc;
+    if ((rc = ensure_init_locked())) return rc;
+    if (K == 0) {  // np.sum over no block: +0.0
+        memset(y, 0, (size_t)M * 4);
+        return BFP8_OK;
+    }
+    DevWeights w;
+    if ((rc = weights_for(mantissas, exps, M, K, &w)) || (rc = upload_x(x, (size_t)K))) return rc;
+    if ((rc = g.y.reserve((size_t)M * 4)) || (rc = g.h_out.reserve((size_t)M * 4))) return rc;
+    HIP_OK(bfp8_launch_gemv_fallback(g.y.as<float>(), g.x.as<float>(), w.mant, w.exps, M, K, pairwise ? 1 : 0,
+                                     g.stream));
+    HIP_OK(hipMemcpyAsync(g.h_out.p, g.y.p, (size_t)M * 4, hipMemcpyDeviceToHost, g.stream));
+    HIP_OK(hipStreamSynchronize(g.stream));
+    memcpy(y, g.h_out.p, (size_t)M * 4);
+    return BFP8_OK;
+}
+
 int bfp8_lm_head_topk(const float* h, const int8_t* mantissas, const uint8_t* exps, int vocab, int hidden,
                       int k, int* out_ids, float* out_scores) {
     if (!h || !mantissas || !exps || !out_ids || !out_scores || !lm_head_args_ok(vocab, hidden, k)) return 0;
@@ -525,10 +688,6 @@ int bfp8_lm_head_argmax(const float* h, const int8_t* mantissas, const uint8_t* 
 
 int lm_head_argmax(const float* h, const uint16_t* embed_table, int vocab_size, int hidden_dim) {
     if (!h || !embed_table || vocab_size <= 0 || hidden_dim <= 0) return 0;
-    if (hidden_dim > BF16_HEAD_MAX_HIDDEN) {
-        set_error("lm_head_argmax: hidden_dim %d above %d", hidden_dim, BF16_HEAD_MAX_HIDDEN);
-        fatal("lm_head_argmax");
-    }
     std::lock_guard<std::mutex> lk(g.mu);
     int am = 0;
     if (ensure_init_locked() != BFP8_OK ||
@@ -540,9 +699,8 @@ int lm_head_argmax(const float* h, const uint16_t* embed_table, int vocab_size, 
 int qwen_lm_head_topk_bf16(const float* h, const uint16_t* embed_table, int vocab_size, int hidden_dim, int k,
                            int* out_ids, float* out_scores) {
     if (!h || !embed_table || !out_ids || !out_scores || vocab_size <= 0 || hidden_dim <= 0 || k <= 0) return 0;
-    if (std::min(k, vocab_size) > BFP8_TOPK_MAX || hidden_dim > BF16_HEAD_MAX_HIDDEN) {
-        set_error("lm_head_topk: k = %d or hidden_dim = %d above the limits %d, %d", k, hidden_dim, BFP8_TOPK_MAX,
-                  BF16_HEAD_MAX_HIDDEN);
+    if (vocab_size > BFP8_SELECT_MAX) {
+        set_error("lm_head_topk: vocab_size %d above %d", vocab_size, BFP8_SELECT_MAX);
         return 0;
     }
     std::lock_guard<std::mutex> lk(g.mu);
@@ -555,8 +713,8 @@ int qwen_sample_from_topk(const int* ids, const float* scores, int n, float temp
                           unsigned int* rng_state) {
     if (!ids || !scores || n <= 0) return -1;
     if (!rng_state) return ids[0];
-    if (n > BFP8_SAMPLE_MAX) {
-        set_error("sample_from_topk: n = %d above %d candidates", n, BFP8_SAMPLE_MAX);
+    if (n > BFP8_SELECT_MAX) {
+        set_error("sample_from_topk: n = %d above %d candidates", n, BFP8_SELECT_MAX);
         return -1;
     }
     std::lock_guard<std::mutex> lk(g.mu);
@@ -564,7 +722,7 @@ int qwen_sample_from_topk(const int* ids, const float* scores, int n, float temp
     int rc;
     if ((rc = g.smp_in.reserve((size_t)n * 8 + 4)) || (rc = g.smp_work.reserve((size_t)n * 8)) ||
         (rc = g.smp_out.reserve(8)) || (rc = g.smp_h.reserve((size_t)n * 8 + 8)))
-        fatal("sample_from_topk");
+        return -1;
     char* hb = static_cast<char*>(g.smp_h.p);
     memcpy(hb, ids, (size_t)n * 4);
     memcpy(hb + (size_t)n * 4, scores, (size_t)n * 4);
@@ -578,14 +736,15 @@ int qwen_sample_from_topk(const int* ids, const float* scores, int n, float temp
     a.top_k = top_k;
     a.top_p = top_p;
     a.out = g.smp_out.as<int>();
-    a.work_ids = g.smp_work.as<int>();
-    a.work_scores = reinterpret_cast<float*>(g.smp_work.as<char>() + (size_t)n * 4);
+    a.work = g.smp_work.p;
     if (hipMemcpyAsync(g.smp_in.p, hb, (size_t)n * 8 + 4, hipMemcpyHostToDevice, g.stream) != hipSuccess ||
         bfp8_launch_sample(a, g.stream) != hipSuccess ||
         hipMemcpyAsync(hb, g.smp_out.p, 4, hipMemcpyDeviceToHost, g.stream) != hipSuccess ||
         hipMemcpyAsync(hb + 4, a.rng, 4, hipMemcpyDeviceToHost, g.stream) != hipSuccess ||
-        hipStreamSynchronize(g.stream) != hipSuccess)
-        fatal("sample_from_topk");
+        hipStreamSynchronize(g.stream) != hipSuccess) {
+        set_error("sample_from_topk: the sampler launch failed on the GPU");
+        return -1;
+    }
     int out;
     memcpy(&out, hb, 4);
     memcpy(rng_state, hb + 4, 4);
@@ -612,6 +771,7 @@ void bfp8_cache_clear(void) {
     }
     g.cache.clear();
     g.cache_bytes = 0;
+    g.writable.clear();
 }
 
 void qwen_prof_enable(int on) { g_prof_on = on; }
@@ -692,6 +852,17 @@ int bfp8_dev_gemv_float(float* y, const float* x, const int8_t* mant_gpu, const 
     return BFP8_OK;
 }
 
+int bfp8_dev_gemv_fallback(float* y, const float* x, const int8_t* mant_gpu, const uint8_t* exps_gpu, int M, int K,
+                           int pairwise, void* stream) {
+    if (M < 0 || K < 0 || (K & 63) || bfp8_nblocks(K) > 16384 || (M > 0 && (!y || (K > 0 && (!x || !mant_gpu || !exps_gpu)))))
+        return BFP8_EINVAL;
+    if (M == 0) return BFP8_OK;
+    DEV_PROLOGUE();
+    HIP_OK(bfp8_launch_gemv_fallback(y, x, (const uint8_t*)mant_gpu, exps_gpu, M, K, pairwise ? 1 : 0,
+                                     pick_stream(stream)));
+    return BFP8_OK;
+}
+
 int bfp8_dev_gemv_batch(float* Y, const uint32_t* xsplit, const float* xscale, const int8_t* mant_gpu,
                         const uint8_t* exps_gpu, int M, int K, int B, void* stream) {
     if (M < 0 || K < 64 || K > 4096 || B < 1 || B > 16) return BFP8_EINVAL;
@@ -717,7 +888,8 @@ int bfp8_dev_gemv_batch(float* Y, const uint32_t* xsplit, const float* xscale, c
 int bfp8_dev_lm_head_topk(int* out_ids, float* out_scores, int* out_count, int* out_argmax,
                           const uint32_t* xsplit, const float* xscale, const int8_t* mant_gpu,
                           const uint8_t* exps_gpu, int vocab, int hidden, int k, void* stream) {
-    if (!lm_head_args_ok(vocab, hidden, k) || !out_ids || !out_scores || !out_count || !out_argmax)
+    if (!lm_head_args_ok(vocab, hidden, k) || hidden > 4096 || !out_ids || !out_scores || !out_count ||
+        !out_argmax || (bfp8_nblocks(hidden) > 0 && (!xsplit || !xscale || !mant_gpu || !exps_gpu)))
         return BFP8_EINVAL;
     std::lock_guard<std::mutex> lk(g.mu);
     if (ensure_init_locked() != BFP8_OK) return BFP8_EHIP;
@@ -769,8 +941,7 @@ int bfp8_dev_copy_probe(void* dst, const void* src, size_t bytes, void* stream) 
 int bf16_dev_lm_head(int* out_ids, float* out_scores, int* out_count, int* out_argmax, float* logits,
                      const float* h, const uint16_t* table, int vocab, int hidden, int k, int tail, void* stream) {
     DEV_PROLOGUE();
-    if (!h || !table || vocab <= 0 || hidden <= 0 || hidden > BF16_HEAD_MAX_HIDDEN || k < 0 ||
-        std::min(k, vocab) > BFP8_TOPK_MAX ||
+    if (!h || !table || vocab <= 0 || vocab > BFP8_SELECT_MAX || hidden <= 0 || k < 0 ||
         (k > 0 && (!out_ids || !out_scores || !out_count || !out_argmax)) || (k == 0 && !logits)) {
         set_error("bf16_dev_lm_head: invalid arguments");
         return BFP8_EINVAL;
@@ -797,7 +968,7 @@ int bf16_dev_tile_table(uint16_t* tiles, const uint16_t* table, int vocab, int h
 int bf16_dev_lm_head_tiles(int* out_ids, float* out_scores, int* out_count, int* out_argmax, float* logits,
                            const float* h, const uint16_t* tiles, int vocab, int hidden, int k, void* stream) {
     DEV_PROLOGUE();
-    if (!h || !tiles || vocab <= 0 || !bf16_tiled_ok(hidden) || k < 0 || std::min(k, vocab) > BFP8_TOPK_MAX ||
+    if (!h || !tiles || vocab <= 0 || vocab > BFP8_SELECT_MAX || !bf16_tiled_ok(hidden) || k < 0 ||
         (k > 0 && (!out_ids || !out_scores || !out_count || !out_argmax)) || (k == 0 && !logits)) {
         set_error("bf16_dev_lm_head_tiles: invalid arguments");
         return BFP8_EINVAL;
@@ -810,7 +981,7 @@ int bfp8_dev_sample_from_topk(int* out_id, const int* ids, const float* scores, 
                               float temperature, int top_k, float top_p, uint32_t* rng_state, void* work,
                               void* stream) {
     DEV_PROLOGUE();
-    if (!out_id || !ids || !scores || n <= 0 || n > BFP8_SAMPLE_MAX || !work) {
+    if (!out_id || !ids || !scores || n <= 0 || n > BFP8_SELECT_MAX || !work) {
         set_error("bfp8_dev_sample_from_topk: invalid arguments");
         return BFP8_EINVAL;
     }
@@ -824,8 +995,7 @@ int bfp8_dev_sample_from_topk(int* out_id, const int* ids, const float* scores, 
     a.top_p = top_p;
     a.rng = rng_state;
     a.out = out_id;
-    a.work_ids = static_cast<int*>(work);
-    a.work_scores = reinterpret_cast<float*>(static_cast<char*>(work) + (size_t)n * 4);
+    a.work = work;
     HIP_OK(bfp8_launch_sample(a, pick_stream(stream)));
     return BFP8_OK;
 }
@@ -846,6 +1016,11 @@ struct Plan {
     bool fused_head = false;       // the lm_head launch quantizes every activation
     bool rows_float = false;       // the 16-row launch quantizes its (shared) activation
     int topk_desc = -1;            // the lm_head item, if any
+    // an lm_head item outside the fused launch's range (odd vocab, k > 64,
+    // K > 4096) runs as a plain GEMV into `logits`, selected at the end
+    int gen_head = -1;
+    bfp8_plan_item gen_out{};      // its outputs and k
+    DevBuf logits, gen_partials, gen_keys;
     std::vector<Bfp8GemvDesc> hdesc;
 };
 
@@ -898,6 +1073,7 @@ int deal_tiles(Launch& L, const std::vector<int>& idx, const bfp8_plan_item* ite
 void release_plan(Plan* p) {
     p->descs.release(); p->qdescs.release(); p->xscale.release(); p->xsplit.release();
     p->partials.release(); p->qtasks.release();
+    p->logits.release(); p->gen_partials.release(); p->gen_keys.release();
     p->head.tiles.release(); p->head.wg_off.release(); p->rest.tiles.release(); p->rest.wg_off.release();
 }
 
@@ -918,17 +1094,32 @@ void* bfp8_plan_create(const bfp8_plan_item* items, int n) {
     p->items.assign(items, items + n);
     int ntopk = 0;
     size_t xs_words = 0, xsc_floats = 0;
+    int rc = 0;
     for (int i = 0; i < n; ++i) {
         const bfp8_plan_item& it = items[i];
         if (it.M <= 0 || it.K < 64 || !it.x || !it.mant_gpu || !it.exps_gpu ||
             (it.topk > 0 && (!lm_head_args_ok(it.M, it.K, it.topk) || !it.out_ids || !it.out_scores ||
                              !it.out_count || !it.out_argmax)) ||
-            (it.topk <= 0 && !it.y) || (it.topk > 0 && it.K > 4096)) {
+            (it.topk <= 0 && !it.y)) {
             set_error("bfp8_plan_create: invalid item %d", i);
             delete p;
             return nullptr;
         }
         ntopk += it.topk > 0;
+        if (it.topk > 0 && !lm_head_fused_ok(it.M, it.K, std::min(it.topk, it.M))) {
+            // the general path: a plain GEMV item into the plan's scores buffer
+            const int kk = std::min(it.topk, it.M);
+            p->gen_head = i;
+            p->gen_out = it;
+            p->gen_out.topk = kk;
+            rc = rc ? rc : p->logits.reserve((size_t)it.M * 4);
+            if (kk <= BFP8_TOPK_MAX)
+                rc = rc ? rc : p->gen_partials.reserve((size_t)bfp8_ntiles(it.M) * kk * 8);
+            else
+                rc = rc ? rc : p->gen_keys.reserve((size_t)it.M * 8);
+            p->items[i].topk = 0;
+            p->items[i].y = p->logits.as<float>();
+        }
         const int nb = bfp8_nblocks(it.K);
         if (it.K <= 4096) {
             xs_words += (size_t)nb * 32;
@@ -936,12 +1127,13 @@ void* bfp8_plan_create(const bfp8_plan_item* items, int n) {
             p->max_nb = std::max(p->max_nb, nb);
         }
     }
-    if (ntopk > 1) {
-        set_error("bfp8_plan_create: at most one lm_head item");
+    if (ntopk > 1 || rc) {
+        set_error(rc ? "bfp8_plan_create: allocation failed" : "bfp8_plan_create: at most one lm_head item");
+        release_plan(p);
         delete p;
         return nullptr;
     }
-    int rc = 0;
+    items = p->items.data();  // the general lm_head, if any, is a plain item from here on
     rc = rc ? rc : p->xsplit.reserve(xs_words * 4);
     rc = rc ? rc : p->xscale.reserve(xsc_floats * 4);
     std::vector<Bfp8QuantDesc> hq;
@@ -966,7 +1158,6 @@ void* bfp8_plan_create(const bfp8_plan_item* items, int n) {
         hq.push_back(q);
         d = plain_desc(it.y, q.xsplit, q.xscale, (const uint8_t*)it.mant_gpu, it.exps_gpu, it.M, it.K, nullptr);
         if (it.topk > 0) {
-            if (it.M & 1) rc = BFP8_EINVAL;
             d.topk = std::min(it.topk, it.M);
             rc = rc ? rc : p->partials.reserve((size_t)bfp8_ntiles(it.M) * d.topk * 8);
             d.partials = p->partials.as<uint64_t>();
@@ -1117,6 +1308,11 @@ int bfp8_plan_launch(void* plan, int stage, void* stream) {
             const bfp8_plan_item& it = p->items[i];
             HIP_OK(bfp8_launch_gemv_float(it.y, it.x, (const uint8_t*)it.mant_gpu, it.exps_gpu, it.M, it.K, s));
         }
+        if (p->gen_head >= 0) {
+            const bfp8_plan_item& o = p->gen_out;
+            return select_topk_bufs(p->logits.as<float>(), o.M, o.topk, o.out_ids, o.out_scores, o.out_count,
+                                    o.out_argmax, p->gen_partials, p->gen_keys, s);
+        }
     }
     return BFP8_OK;
 }
@@ -1135,7 +1331,10 @@ const char* bfp8_plan_kernel_name(void* plan, int stage) {
     }
     if (stage == 2) {
         if (!p->odd_items.empty()) return "bfp8_tail_row_kernel";
-        return p->float_items.empty() ? "" : "bfp8_gemv_float_kernel";
+        if (!p->float_items.empty()) return "bfp8_gemv_float_kernel";
+        if (p->gen_head >= 0)
+            return p->gen_out.topk <= BFP8_TOPK_MAX ? "bfp8_select_partials_kernel" : "bfp8_select_sort_kernel";
+        return "";
     }
     return "";
 }

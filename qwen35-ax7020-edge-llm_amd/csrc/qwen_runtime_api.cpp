@@ -156,7 +156,7 @@ int fwd_vec(const T* p, size_t n, const T** out) {
 // GPU-layout planes: the shared read-only cache, else a forward-owned copy.
 int fwd_planes(const int8_t* mant, const uint8_t* exps, int M, int K, DevWeights* out) {
     const size_t mb = (size_t)M * K, eb = (size_t)M * bfp8_nblocks(K);
-    if (range_readonly(mant, mb) && range_readonly(exps, eb)) return weights_for(mant, exps, M, K, out);
+    if (range_readonly_cached(mant, mb) && range_readonly_cached(exps, eb)) return weights_for(mant, exps, M, K, out);
     const ParamKey key{mant, mb};
     auto it = F.planes.find(key);
     if (it == F.planes.end()) {
@@ -803,7 +803,9 @@ int forward_token_c(int token_id, float* h, const LinearLayerPlan* linear_plans,
     const size_t tbytes = (size_t)kVocab * kHidden * 2;
     RT_CHECK("forward_token_c", fwd_vec(final_norm_w, kHidden, &fnorm));
     int tiled = 0;  // the cached table's layout
-    if (range_readonly(embed_table, tbytes)) {
+    if (bf16_table_lookup(embed_table, kVocab, kHidden, &table, &tiled)) {
+        // cached on an earlier token: no /proc/self/maps scan
+    } else if (range_readonly_cached(embed_table, tbytes)) {
         RT_CHECK("forward_token_c", bf16_table_for(embed_table, kVocab, kHidden, &table, &tiled));
     } else {
         RT_CHECK("forward_token_c", fwd_vec(embed_table, (size_t)kVocab * kHidden, &table));

@@ -14,12 +14,17 @@ namespace {
 // ---- top-k keys ------------------------------------------------------------
 // Order (score desc, id asc) as one unsigned 64-bit key, larger = better.
 // Candidates are the scores the reference would ever offer: > -FLT_MAX, not
-// NaN (04/qwen_sampling.c:243-248 with thr = -FLT_MAX).  -0 equals +0 there,
-// so it is keyed as +0.  0 is "no candidate".
+// NaN (04/qwen_sampling.c:243-248 with thr = -FLT_MAX, compared in IEEE
+// arithmetic).  -0 equals +0 there, so it is keyed as +0; a subnormal score
+// keeps its value.  The tests are on the bits: a float compare inside a
+// flush-to-zero unit would read a subnormal score as zero.  0 is "no
+// candidate".
 __device__ __forceinline__ uint64_t topk_key(float y, int row) {
-    if (!(y > -FLT_MAX)) return 0;
-    uint32_t b = __float_as_uint(y == 0.0f ? 0.0f : y);
-    uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    uint32_t b = __float_as_uint(y);
+    const uint32_t a = b & 0x7fffffffu;
+    if (a > 0x7f800000u || b == 0xff800000u || b == 0xff7fffffu) return 0;  // NaN, -inf, -FLT_MAX
+    if (a == 0u) b = 0u;
+    const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
     return ((uint64_t)o << 32) | (uint32_t)~(uint32_t)row;
 }
 __device__ __forceinline__ float key_score(uint64_t k) {

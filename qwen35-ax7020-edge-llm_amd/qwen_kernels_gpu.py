@@ -99,6 +99,10 @@ def bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.bfp8_lm_head_argmax.restype = i
     lib.bfp8_gemv_batch.argtypes = [vp, vp, vp, vp, i, i, i]
     lib.bfp8_gemv_batch.restype = None
+    lib.bfp8_gemv_fallback.argtypes = [vp, vp, vp, vp, i, i, i]
+    lib.bfp8_gemv_fallback.restype = i
+    lib.bfp8_dev_gemv_fallback.argtypes = [vp, vp, vp, vp, i, i, i, vp]
+    lib.bfp8_dev_gemv_fallback.restype = i
     # the bf16 tied-embedding lm_head (04/qwen_real_engine.py:691-696) and sampler
     lib.lm_head_argmax.argtypes = [vp, vp, i, i]
     lib.lm_head_argmax.restype = i
@@ -280,6 +284,15 @@ class Bfp8Kernels:
         if y is None:
             y = np.empty(M, dtype=np.float32)
         self.lib.bfp8_gemv(_ptr(y), _ptr(x), _ptr(mantissas), _ptr(exps), M, K)
+        return y
+
+    def gemv_fallback(self, x: np.ndarray, mantissas: np.ndarray, exps: np.ndarray, M: int, K: int,
+                      pairwise: bool = True) -> np.ndarray:
+        """The engine's numpy fallback (04/qwen_real_engine.py:1230-1238) on the GPU."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.empty(M, dtype=np.float32)
+        check(self.lib.bfp8_gemv_fallback(_ptr(y), _ptr(x), _ptr(mantissas), _ptr(exps), M, K, int(pairwise)),
+              "bfp8_gemv_fallback")
         return y
 
     def gemv_batch(self, X: np.ndarray, mantissas: np.ndarray, exps: np.ndarray, M: int, K: int) -> np.ndarray:

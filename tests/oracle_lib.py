@@ -33,6 +33,7 @@ def oracle() -> ctypes.CDLL:
         lib.orc_quant_x.argtypes = [vp, i, vp, vp]
         lib.orc_lane_sums.argtypes = [vp, vp, i, i, vp]
         lib.orc_gemv_float.argtypes = [vp, vp, vp, vp, i, i]
+        lib.orc_gemv_fallback.argtypes = [vp, vp, vp, vp, i, i, i]
         lib.orc_gemv_neon.argtypes = [vp, vp, vp, vp, i, i, vp, vp, vp]
         lib.orc_argmax.argtypes = [vp, i]
         lib.orc_argmax.restype = i
@@ -93,6 +94,17 @@ def gemv_float(x, mant, exps):
     y = np.zeros(M, dtype=np.float32)
     oracle().orc_gemv_float(_p(y), _p(np.ascontiguousarray(x, dtype=np.float32)), _p(mant),
                             _p(np.ascontiguousarray(exps)), M, K)
+    return y
+
+
+def gemv_fallback(x, mant, exps, pairwise=True):
+    """The engine's numpy fallback (04/qwen_real_engine.py:1230-1238) in numpy's
+    summation order: pairwise (numpy >= 1.9) or sequential (numpy 1.8.2)."""
+    mant = np.ascontiguousarray(mant, dtype=np.int8)
+    M, K = mant.shape
+    y = np.zeros(M, dtype=np.float32)
+    oracle().orc_gemv_fallback(_p(y), _p(np.ascontiguousarray(x, dtype=np.float32)), _p(mant),
+                               _p(np.ascontiguousarray(exps, dtype=np.uint8)), M, K, int(bool(pairwise)))
     return y
 
 

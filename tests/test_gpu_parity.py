@@ -363,10 +363,18 @@ def test_lm_head_small_vocab_and_invalid_arguments(gpu, torch_mod):
     assert np.array_equal(ids, ids_ref) and same_f32(sc, sc_ref)
     ids, _ = kk.lm_head_topk(x, mant, exps, 30, 128, 64)  # k > vocab -> min(k, vocab)
     assert np.array_equal(ids, ol.topk(y_ref[:30], 64)[0])
-    assert kk.lm_head_topk(x, mant, exps, 99, 128, 40)[0].size == 0  # odd vocab rejected
-    assert kk.lm_head_topk(x, mant, exps, 100, 128, 65)[0].size == 0
+    # an odd vocabulary: the last row in the scalar order of the odd-M tail
+    y99, *_ = ol.gemv_neon(x, mant[:99], exps[:99])
+    ids, sc = kk.lm_head_topk(x, mant, exps, 99, 128, 40)
+    ids_ref, sc_ref = ol.topk(y99, 40)
+    assert np.array_equal(ids, ids_ref) and same_f32(sc, sc_ref)
+    assert kk.lm_head_argmax(x, mant, exps, 99, 128) == ol.argmax(y99)
+    ids, sc = kk.lm_head_topk(x, mant, exps, 100, 128, 65)  # k above the fused launch's 64
+    ids_ref, sc_ref = ol.topk(y_ref, 65)
+    assert ids.size == 65 and np.array_equal(ids, ids_ref) and same_f32(sc, sc_ref)
     assert kk.lm_head_topk(x, mant, exps, 100, 128, 0)[0].size == 0
-    assert kk.lm_head_argmax(x, mant, exps, 99, 128) == -1
+    assert kk.lm_head_topk(x, mant, exps, 0, 128, 5)[0].size == 0
+    assert kk.lm_head_argmax(x, mant, exps, 0, 128) == -1
 
 
 def test_random_lm_heads_against_the_oracle(gpu, torch_mod):

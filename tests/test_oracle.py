@@ -110,6 +110,117 @@ def test_quant_error_bound():
     assert err.max() <= 0.5 + 1e-3  # half an int16 step (plus the rounding of q)
 
 
+# The two soft spots of the restatement, pinned by hand-worked blocks where a
+# plausible other form of the reference's lines gives another answer.
+QUANT_ORDER_AMAX = np.array([1065491860], dtype=np.uint32).view(F32)[0]  # 1.0165277
+QUANT_ORDER_X = np.array([1043759005], dtype=np.uint32).view(F32)[0]     # 0.17822118
+
+
+def test_quant_multiplies_by_the_rounded_reciprocal():
+    """04/qwen_kernels_opt.c:196-199: q = 16384.0f / amax is rounded to float
+    first, then xq = lrintf(x * q).  For this block x * q rounds to
+    2871.52.. -> 2872, whereas (x * 16384) / amax in float and the exact
+    x * 16384 / amax both give 2873."""
+    x = np.zeros(64, dtype=F32)
+    x[0], x[1] = QUANT_ORDER_AMAX, QUANT_ORDER_X
+    xq, xs = ol.quant_x(x)
+    q = F32(F32(16384.0) / QUANT_ORDER_AMAX)
+    assert xq[0] == 16384 and xq[1] == 2872 and np.rint(F32(QUANT_ORDER_X * q)) == 2872
+    assert np.rint(F32(F32(QUANT_ORDER_X * F32(16384.0)) / QUANT_ORDER_AMAX)) == 2873
+    assert round(float(QUANT_ORDER_X) * 16384 / float(QUANT_ORDER_AMAX)) == 2873
+
+
+def epilogue_case():
+    """Two blocks of one residue lane: block 0 gives S = 2^24 (xscale 1,
+    EXP_SCALE 1), block 1 gives S = 3 with xscale = float(1/3) rounded up
+    (amax = 16384 * xscale, whose quantizer q is exactly 3, so x = 1 gives
+    xq = 3).  Returns (mant, exps, x) for two identical rows."""
+    xs1 = F32(1.0) / F32(3.0)
+    assert np.float64(xs1) > 1.0 / 3.0
+    K = 128
+    x = np.zeros(K, dtype=F32)
+    w = np.zeros(K, dtype=np.int8)
+    pos = np.arange(0, 64, 4)[:9]          # residue-0 positions of block 0
+    x[pos] = 16384.0
+    w[pos] = [127] * 8 + [8]               # 16384 * 1024 = 2^24
+    x[64 + 1] = F32(16384.0) * xs1         # block 1's amax (residue 1, weight 0)
+    x[64 + 0] = 1.0                        # xq = rint(1 * 3) = 3, weight 1
+    w[64 + 0] = 1
+    mant = np.stack([w, w])
+    exps = np.full((2, 2), 134, dtype=np.uint8)
+    return mant, exps, x, xs1
+
+
+def test_gemv_epilogue_rounds_the_product_before_the_add():
+    """04/qwen_kernels_opt.c:265-268: fs = fs + (float(S) * EXP_SCALE) * xscale
+    with vmlaq_n_f32, which on Cortex-A9 rounds the product and then the sum.
+    Block 1's product 3 * xscale = 1 + 2^-25.3 rounds to 1, and 2^24 + 1 ties to
+    even: y = 2^24.  A fused multiply-add would see 2^24 + 1.00000003 and give
+    2^24 + 2."""
+    mant, exps, x, xs1 = epilogue_case()
+    y, xq, xs, lanes = ol.gemv_neon(x, mant, exps)
+    assert xs[0] == 1.0 and xs[1] == xs1 and xq[64] == 3
+    assert lanes[0, 0, 0] == 2 ** 24 and lanes[0, 1, 0] == 3 and not lanes[0, :, 1:].any()
+    assert F32(F32(3.0) * xs1) == 1.0
+    assert list(y) == [2.0 ** 24, 2.0 ** 24]
+    fused = F32(np.float64(2.0 ** 24) + 3.0 * np.float64(xs1))  # exact in double, one rounding
+    assert fused == 2.0 ** 24 + 2
+
+
+# ---- the engine's numpy fallback (04/qwen_real_engine.py:1230-1238) ----------------------
+def _numpy_fallback(x, mant, exps, order):
+    """The engine's lines on numpy itself: np.sum (pairwise in numpy >= 1.9) or
+    the last element of np.cumsum (left to right, as numpy 1.8.2 sums)."""
+    M, K = mant.shape
+    nb = K // 64
+    scales = (2.0 ** (exps.astype(np.float32) - 134.0)).reshape(M, nb)
+    assert scales.dtype == np.float32
+    m_blocks = mant.reshape(M, nb, 64).astype(np.float32)
+    x_blocks = x.reshape(nb, 64)
+    if order == "pairwise":
+        dots = np.sum(m_blocks * x_blocks, axis=-1)
+        return np.sum(dots * scales, axis=-1)
+    dots = np.cumsum(m_blocks * x_blocks, axis=-1)[..., -1]
+    return np.cumsum(dots * scales, axis=-1)[..., -1]
+
+
+@pytest.mark.parametrize("K", [64, 448, 512, 1024, 3584, 8256, 65 * 128])
+@pytest.mark.parametrize("order", ["pairwise", "sequential"])
+def test_fallback_matches_numpy_summation(K, order):
+    """Activations over many decades, so that every summation order rounds
+    differently: the restatement equals numpy's own result bit for bit (the
+    numpy of this image, 2.2.6), and the two orders differ from each other."""
+    rng = np.random.default_rng(K)
+    M = 24
+    mant = rng.integers(-128, 128, size=(M, K), dtype=np.int8)
+    exps = rng.integers(118, 136, size=(M, K // 64), dtype=np.uint8)
+    x = (rng.standard_normal(K) * 10.0 ** rng.uniform(-6, 6, K)).astype(F32)
+    want = _numpy_fallback(x, mant, exps, order)
+    got = ol.gemv_fallback(x, mant, exps, pairwise=(order == "pairwise"))
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    other = ol.gemv_fallback(x, mant, exps, pairwise=(order != "pairwise"))
+    assert not np.array_equal(other, got)
+
+
+def test_fallback_zero_and_subnormal_terms():
+    """All-zero rows sum to +0.0 in the pairwise order (numpy adds the
+    pairwise sum to +0.0); exponent bytes below 7 give subnormal scales,
+    which numpy keeps (IEEE)."""
+    M, K = 3, 128
+    mant = np.zeros((M, K), dtype=np.int8)
+    mant[1, :64] = 1
+    mant[2, 64:] = -1
+    exps = np.array([[0, 0], [1, 0], [2, 3]], dtype=np.uint8)
+    x = np.full(K, -0.0, dtype=F32)
+    x[:64] = 1.0
+    x[64:] = 3.0
+    for order in ("pairwise", "sequential"):
+        want = _numpy_fallback(x, mant, exps, order)
+        got = ol.gemv_fallback(x, mant, exps, pairwise=(order == "pairwise"))
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert 0 < ol.gemv_fallback(x, mant, exps)[1] < np.finfo(F32).tiny
+
+
 # ---- Advanced SIMD float model (ARM ARM FPRound with FPSCR.FZ = 1) ----------------------
 def test_neon_flush_to_zero_rules():
     tiny = F32(2.0 ** -130)  # subnormal operand reads as zero
