@@ -295,6 +295,20 @@ int bfp8_dev_lm_head_topk(int* out_ids, float* out_scores, int* out_count, int* 
                           const uint32_t* xsplit, const float* xscale, const int8_t* mant_gpu,
                           const uint8_t* exps_gpu, int vocab, int hidden, int k, void* stream);
 
+/* No counterpart in the reference: bfp8_dev_lm_head_topk for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Same arguments and results; it
+ * allocates nothing: its partial lists, scores and sort keys live in one
+ * fixed device array of the library (5 MiB per GPU, held until the process
+ * ends; its address is looked up by init_kernels or the first call on a
+ * device).  Limits: vocab <= 262144, hidden in [64, 4096]; larger sizes
+ * return BFP8_EINVAL with bfp8_last_error set.  Every call on one GPU shares
+ * that array: calls that overlap on one GPU (other streams, other threads)
+ * race and must be ordered by the caller. */
+int bfp8_dev_lm_head_topk_noalloc(int* out_ids, float* out_scores, int* out_count, int* out_argmax,
+                                  const uint32_t* xsplit, const float* xscale, const int8_t* mant_gpu,
+                                  const uint8_t* exps_gpu, int vocab, int hidden, int k, void* stream);
+
 /* bf16 tied-embedding lm_head on device buffers: scores of every row in the
  * board build's order (tail = 0: hidden % 8 trailing elements dropped, as
  * lm_head_argmax; tail = 1: added in IEEE arithmetic, as lm_head_topk),

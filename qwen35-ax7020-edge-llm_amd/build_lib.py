@@ -6,6 +6,7 @@ Translation units:
   csrc/bfp8_ftz.hip          GEMV kernels, f32 flush-to-zero (Advanced SIMD semantics)
   csrc/bfp8_ieee.hip         quantizer / scalar-order kernels, IEEE subnormals
   csrc/select.hip            general top-k selection (tile lists, sort) and the sampler, IEEE
+  csrc/noalloc.hip           the fixed device scratch of the no-alloc lm_head entry point
   csrc/bf16_head.hip         bf16 tied-embedding lm_head, f32 flush-to-zero
   csrc/runtime_ftz.hip       decode runtime kernels (norms, conv, GDN, swiglu), f32 flush-to-zero
   csrc/fused_gemv.hip        the forward's GEMVs with their activation prologue, f32 flush-to-zero
@@ -46,6 +47,7 @@ UNITS = {
     "fused_gemv.hip": ["-fgpu-flush-denormals-to-zero"],
     "bfp8_ieee.hip": [],
     "select.hip": [],
+    "noalloc.hip": [],
     "qwen_kernels_api.cpp": [],
     "qwen_runtime_api.cpp": [],
     "qwen_weights.cpp": [],

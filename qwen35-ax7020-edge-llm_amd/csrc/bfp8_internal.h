@@ -144,6 +144,17 @@ bool bf16_tiled_ok(int hidden);
 size_t bf16_tiled_elems(int vocab, int hidden);
 hipError_t bf16_launch_tile_table(uint16_t* dst, const uint16_t* src, int vocab, int hidden, hipStream_t s);
 
+// ---- noalloc.hip ---------------------------------------------------------
+// The fixed device scratch of bfp8_dev_lm_head_topk_noalloc: vocabularies up
+// to BFP8_NOALLOC_MAX_VOCAB rows.
+#define BFP8_NOALLOC_MAX_VOCAB 262144
+#define BFP8_NOALLOC_PARTIALS_BYTES ((size_t)(BFP8_NOALLOC_MAX_VOCAB / 64) * BFP8_TOPK_MAX * 8)
+#define BFP8_NOALLOC_LOGITS_BYTES ((size_t)BFP8_NOALLOC_MAX_VOCAB * 4)
+#define BFP8_NOALLOC_KEYS_BYTES ((size_t)BFP8_NOALLOC_MAX_VOCAB * 8)
+// Device address of the scratch on the current device (looked up once per
+// device with hipGetSymbolAddress, then cached).
+hipError_t bfp8_noalloc_setup(void** out);
+
 // ---- select.hip ----------------------------------------------------------
 // Per-tile top-`topk` partials ([ntiles(n)][topk] keys) of logits[0, n), for
 // bfp8_launch_topk_merge (topk <= BFP8_TOPK_MAX).

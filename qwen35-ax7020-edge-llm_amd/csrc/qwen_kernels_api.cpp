@@ -568,6 +568,13 @@ extern "C" {
 void init_kernels(void) {
     std::lock_guard<std::mutex> lk(g.mu);
     if (ensure_init_locked() != BFP8_OK) fatal("init_kernels");
+    // the no-alloc lm_head's device scratch: its address on this device
+    void* scratch = nullptr;
+    const hipError_t e = bfp8_noalloc_setup(&scratch);
+    if (e != hipSuccess) {
+        set_error("hipGetSymbolAddress of the no-alloc scratch: %s", hipGetErrorString(e));
+        fatal("init_kernels");
+    }
 }
 
 void bfp8_gemv(float* y, const float* x, const int8_t* mantissas, const uint8_t* exps, int M, int K) {
@@ -895,6 +902,44 @@ int bfp8_dev_lm_head_topk(int* out_ids, float* out_scores, int* out_count, int* 
     if (ensure_init_locked() != BFP8_OK) return BFP8_EHIP;
     return lm_head_dev(out_ids, out_scores, out_count, out_argmax, xsplit, xscale, (const uint8_t*)mant_gpu,
                        exps_gpu, vocab, hidden, k, pick_stream(stream));
+}
+
+int bfp8_dev_lm_head_topk_noalloc(int* out_ids, float* out_scores, int* out_count, int* out_argmax,
+                                  const uint32_t* xsplit, const float* xscale, const int8_t* mant_gpu,
+                                  const uint8_t* exps_gpu, int vocab, int hidden, int k, void* stream) {
+    if (vocab <= 0 || hidden < 64 || hidden > 4096 || k < 1 || !out_ids || !out_scores || !out_count ||
+        !out_argmax || !xsplit || !xscale || !mant_gpu || !exps_gpu) {
+        set_error("bfp8_dev_lm_head_topk_noalloc: invalid arguments");
+        return BFP8_EINVAL;
+    }
+    if (vocab > BFP8_NOALLOC_MAX_VOCAB) {
+        set_error("bfp8_dev_lm_head_topk_noalloc: vocab %d above the scratch's %d rows", vocab,
+                  BFP8_NOALLOC_MAX_VOCAB);
+        return BFP8_EINVAL;
+    }
+    std::lock_guard<std::mutex> lk(g.mu);
+    void* base = nullptr;
+    HIP_OK(bfp8_noalloc_setup(&base));
+    uint64_t* partials = static_cast<uint64_t*>(base);
+    float* logits = reinterpret_cast<float*>(static_cast<char*>(base) + BFP8_NOALLOC_PARTIALS_BYTES);
+    uint64_t* keys = reinterpret_cast<uint64_t*>(static_cast<char*>(base) + BFP8_NOALLOC_PARTIALS_BYTES +
+                                                 BFP8_NOALLOC_LOGITS_BYTES);
+    hipStream_t s = pick_stream(stream);
+    const uint8_t* m = (const uint8_t*)mant_gpu;
+    const int kk = std::min(k, vocab);
+    if (lm_head_fused_ok(vocab, hidden, kk)) {
+        Bfp8GemvDesc d = plain_desc(nullptr, xsplit, xscale, m, exps_gpu, vocab, hidden, nullptr);
+        d.topk = kk;
+        d.partials = partials;
+        d.out_ids = out_ids;
+        d.out_scores = out_scores;
+        d.out_count = out_count;
+        d.out_argmax = out_argmax;
+        HIP_OK(bfp8_launch_gemv(d, s));
+        return BFP8_OK;
+    }
+    int rc = gemv_q(logits, xsplit, xscale, m, exps_gpu, vocab, hidden, nullptr, s);
+    return rc ? rc : select_topk_raw(logits, vocab, kk, out_ids, out_scores, out_count, out_argmax, partials, keys, s);
 }
 
 int bfp8_dev_synth_planes(int8_t* mant_soa, uint8_t* exps_soa, int M, int K, uint64_t seed, int e_lo, int e_hi,

@@ -160,6 +160,7 @@ def bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.bfp8_dev_gemv_float.argtypes = [vp, vp, vp, vp, i, i, vp]
     lib.bfp8_dev_gemv_batch.argtypes = [vp, vp, vp, vp, vp, i, i, i, vp]
     lib.bfp8_dev_lm_head_topk.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, i, i, i, vp]
+    lib.bfp8_dev_lm_head_topk_noalloc.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, i, i, i, vp]
     lib.bfp8_dev_synth_planes.argtypes = [vp, vp, i, i, c_uint64, i, i, vp]
     lib.bfp8_dev_read_probe.argtypes = [vp, c_size_t, vp, vp]
     lib.bfp8_dev_copy_probe.argtypes = [vp, vp, c_size_t, vp]
@@ -170,7 +171,7 @@ def bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.bf16_dev_lm_head_tiles.argtypes = [vp, vp, vp, vp, vp, vp, vp, i, i, i, vp]
     lib.bfp8_dev_sample_from_topk.argtypes = [vp, vp, vp, vp, i, c_float, i, c_float, vp, vp, vp]
     for name in ("bf16_dev_lm_head", "bf16_dev_tile_table", "bf16_dev_lm_head_tiles", "bfp8_dev_sample_from_topk", "bfp8_dev_pack", "bfp8_dev_unpack", "bfp8_dev_quantize", "bfp8_dev_gemv",
-                 "bfp8_dev_gemv_float", "bfp8_dev_gemv_batch", "bfp8_dev_lm_head_topk",
+                 "bfp8_dev_gemv_float", "bfp8_dev_gemv_batch", "bfp8_dev_lm_head_topk", "bfp8_dev_lm_head_topk_noalloc",
                  "bfp8_dev_synth_planes", "bfp8_dev_read_probe", "bfp8_dev_copy_probe"):
         getattr(lib, name).restype = i
     lib.bfp8_plan_create.argtypes = [POINTER(bfp8_plan_item), i]
