@@ -10,6 +10,7 @@ Translation units:
   csrc/bf16_head.hip         bf16 tied-embedding lm_head, f32 flush-to-zero
   csrc/runtime_ftz.hip       decode runtime kernels (norms, conv, GDN, swiglu), f32 flush-to-zero
   csrc/fused_gemv.hip        the forward's GEMVs with their activation prologue, f32 flush-to-zero
+  csrc/sweep.hip             a whole sweep plan in one launch (LDS-quantized activations, in-launch top-k)
   csrc/qwen_kernels_api.cpp  C ABI host code (include/qwen_kernels.h)
   csrc/qwen_runtime_api.cpp  C ABI of the runtime kernels and the forward loop
   csrc/qwen_weights.cpp      manifest-driven weight-image loader
@@ -45,6 +46,7 @@ UNITS = {
     "bf16_head.hip": ["-fgpu-flush-denormals-to-zero"],
     "runtime_ftz.hip": ["-fgpu-flush-denormals-to-zero"],
     "fused_gemv.hip": ["-fgpu-flush-denormals-to-zero"],
+    "sweep.hip": ["-fgpu-flush-denormals-to-zero"],
     "bfp8_ieee.hip": [],
     "select.hip": [],
     "noalloc.hip": [],

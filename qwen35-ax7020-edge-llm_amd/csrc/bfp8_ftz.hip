@@ -30,6 +30,7 @@
 #include "gemv_dev.h"
 #include "quant_block.h"
 #include "runtime_internal.h"
+#include "topk_merge.h"
 #include "wave_topk.h"
 
 namespace {
@@ -47,147 +48,14 @@ __device__ __forceinline__ float epilogue(float fs, int S, uint32_t e, float xs)
     return fs + t2;
 }
 
-// ---- top-k final merge ---------------------------------------------------------
+// ---- top-k final merge (topk_merge.h) --------------------------------------------
 // The per-tile partials ([ntiles][topk] sorted keys) are written by one
 // streaming launch and merged by a later launch on the same stream: the
 // kernel boundary makes them visible, so no cross-workgroup fence or atomic
 // is needed.  The merge runs as its own 16-wavefront kernel, or folded into
 // workgroup 0 of the next grouped launch (4 wavefronts).
-
-// What the merge needs of a descriptor, by value so that non-inlined code
-// never takes the address of a kernel argument.
-struct TopkArgs {
-    const uint64_t* partials;
-    int* out_ids;
-    float* out_scores;
-    int* out_count;
-    int* out_argmax;
-    int topk, ntiles;
-};
-
 __device__ __forceinline__ TopkArgs topk_args(const Bfp8GemvDesc& d) {
     return TopkArgs{d.partials, d.out_ids, d.out_scores, d.out_count, d.out_argmax, d.topk, bfp8_ntiles(d.M)};
-}
-
-template <int W>
-struct MergeLds {
-    uint64_t xch[W][64];
-    int list[BFP8_TOPK_MAX];
-};
-
-// Tree-reduces the W wavefronts' descending lists into wavefront 0's (the
-// partner's list is read reversed, i.e. ascending).  A wavefront writes its
-// slot once, at the level where it drops out, and every slot is read at the
-// level it is written, so one barrier per level suffices; the caller puts a
-// barrier between two calls.
-template <int W>
-__device__ __forceinline__ uint64_t reduce_waves(uint64_t v, int w, int lane, MergeLds<W>& L) {
-#pragma unroll
-    for (int step = 1; step < W; step <<= 1) {
-        if ((w & (2 * step - 1)) == step) L.xch[w][lane] = v;
-        __syncthreads();
-        if ((w & (2 * step - 1)) == 0) v = wave_merge<true>(v, L.xch[w + step][63 - lane], lane);
-    }
-    return v;
-}
-
-// Final merge by one workgroup of W wavefronts, H list heads per lane per
-// pass.  Keys are unique (they carry the row), so an entry at position i of a
-// list whose head ranks h-th among all heads has at least h+i better keys:
-// only the lists of the kk best heads, and in them only i < kk - h, can reach
-// the top kk.
-// The result: ids / scores of the kk best keys (t: lane's key, lanes < kk),
-// their count, and the argmax (lm_head_argmax: lowest id among maxima above
-// -1e30, else 0; 04/qwen_kernels_opt.c:402-403, :483-490).  Wavefront 0.
-__device__ __forceinline__ void topk_write(const TopkArgs& d, uint64_t v, int lane) {
-    const int kk = d.topk;
-    const uint64_t t = lane < kk ? v : 0ull;
-    const int cnt = __popcll(__ballot(t != 0));
-    if (lane < kk) {
-        d.out_ids[lane] = t ? key_id(t) : -1;
-        d.out_scores[lane] = t ? key_score(t) : 0.0f;
-    }
-    if (lane == 0) {  // lane 0 holds the best key
-        *d.out_count = cnt;
-        *d.out_argmax = (t && key_score(t) > -1e30f) ? key_id(t) : 0;
-    }
-}
-
-__device__ __forceinline__ uint64_t wave_max_key(uint64_t v) {
-#pragma unroll
-    for (int j = 1; j < 64; j <<= 1) {
-        const uint64_t o = xor_lane(v, j);
-        v = o > v ? o : v;
-    }
-    return v;
-}
-
-template <int W, int H>
-__device__ __forceinline__ void topk_merge(const TopkArgs& d, MergeLds<W>& L) {
-    const int kk = d.topk;
-    const int ntiles = d.ntiles;
-    const uint64_t* parts = d.partials;
-    const int lane = threadIdx.x & 63;
-    const int w = threadIdx.x >> 6;
-    if (kk == 1) {  // the best key is the largest list head: a max-reduction, no list merge
-        uint64_t m = 0;
-        for (int i = w * 64 + lane; i < ntiles; i += W * 64) {
-            const uint64_t h = __builtin_nontemporal_load(&parts[i]);
-            m = h > m ? h : m;
-        }
-        m = wave_max_key(m);
-        if (lane == 0) L.xch[0][w] = m;
-        __syncthreads();
-        if (w == 0) {
-            m = wave_max_key(lane < W ? L.xch[0][lane] : 0ull);
-            topk_write(d, m, lane);
-        }
-        return;
-    }
-    // 1. the 64 best list heads
-    uint64_t v = 0;
-    for (int base = w * 64 * H; base < ntiles; base += W * 64 * H) {
-        uint64_t h[H];
-        bool desc[H];
-#pragma unroll
-        for (int u = 0; u < H; ++u) {
-            const int i = base + u * 64 + lane;
-            h[u] = i < ntiles ? __builtin_nontemporal_load(&parts[(size_t)i * kk]) : 0ull;
-            desc[u] = (H > 1) && (u % 2 == 0);  // the last tree level must come out ascending
-        }
-        wave_sort<H>(h, desc, lane);
-#pragma unroll
-        for (int s = 1; s < H; s <<= 1) {
-#pragma unroll
-            for (int i = 0; i < H; i += 2 * s) {
-                if ((i / (2 * s)) % 2 == 0 && 2 * s < H)
-                    h[i] = wave_merge<true>(h[i], h[i + s], lane);
-                else
-                    h[i] = wave_merge<false>(h[i], h[i + s], lane);
-            }
-        }
-        v = wave_merge<true>(v, h[0], lane);
-    }
-    v = reduce_waves<W>(v, w, lane, L);
-    if (w == 0 && lane < kk) L.list[lane] = v ? key_id(v) / BFP8_TILE_ROWS : -1;
-    __syncthreads();
-    // 2. wavefront w merges lists h = w, w + W, ... (list h cut after kk - h
-    // entries); odd slots are loaded reversed (ascending) for the tree.
-    constexpr int kSlots = BFP8_TOPK_MAX / W;
-    uint64_t e[kSlots];
-#pragma unroll
-    for (int sl = 0; sl < kSlots; ++sl) {
-        const int hh = w + sl * W;
-        const int list = hh < kk ? L.list[hh] : -1;
-        const int idx = (sl & 1) ? 63 - lane : lane;
-        e[sl] = (list >= 0 && idx < kk - hh) ? __builtin_nontemporal_load(&parts[(size_t)list * kk + idx]) : 0ull;
-    }
-    if (kSlots > 1)
-        v = wave_merge_tree<kSlots>(e, lane);
-    else
-        v = e[0];
-    v = reduce_waves<W>(v, w, lane, L);
-    if (w == 0) topk_write(d, v, lane);
 }
 
 constexpr int kWaves = 4;        // wavefronts per GEMV workgroup
@@ -195,7 +63,7 @@ constexpr int kMergeWaves = 16;  // wavefronts of the stand-alone merge kernel
 
 // Folded merge for workgroup 0 of a grouped launch.
 __device__ __noinline__ void topk_merge_folded(TopkArgs d, MergeLds<kWaves>& L) {
-    topk_merge<kWaves, 4>(d, L);
+    topk_merge<kWaves, 4>(d, PlainKeys{}, L);
     __syncthreads();  // L is reused by the streaming code
 }
 
@@ -739,7 +607,7 @@ extern "C" __global__ __launch_bounds__(kWideWaves * 64) void bfp8_gemv_wide_gro
 // Stand-alone final top-k merge (one workgroup of 16 wavefronts).
 extern "C" __global__ __launch_bounds__(kMergeWaves * 64) void bfp8_topk_merge_kernel(Bfp8GemvDesc d) {
     __shared__ MergeLds<kMergeWaves> L;
-    topk_merge<kMergeWaves, 1>(topk_args(d), L);
+    topk_merge<kMergeWaves, 1>(topk_args(d), PlainKeys{}, L);
 }
 
 // Batched GEMV: B activation vectors against one weight matrix, weights read

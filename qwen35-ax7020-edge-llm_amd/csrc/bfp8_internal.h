@@ -129,6 +129,44 @@ hipError_t bfp8_launch_gemv_head(const Bfp8HeadArgs& a, int nwg, hipStream_t s);
 #define BFP8_MERGE_COST_BLOCKS 16
 // Number of workgroups the persistent GEMV kernels keep resident.
 int bfp8_stream_grid();
+
+// ---- sweep.hip: a whole plan in one persistent launch -----------------------
+// Workgroup w takes its lm_head tiles (w, w + grid, ... of descs[head], whose
+// planes and width are arguments) then tiles[wg_off[w] .. wg_off[w+1]).  Its
+// activation slots are acts[act_off[w] .. act_off[w+1]) (slot 0: the
+// lm_head's when it has lm_head tiles), each quantized into LDS at word
+// offset xoff (a multiple of 4; nb*32 split words then nb scale words).
+struct Bfp8SweepTile {
+    int desc, tile;
+    int xoff;  // LDS word offset of the tile's activation slot
+    int slot;  // index of that slot in the workgroup's list
+};
+struct Bfp8SweepAct {
+    const float* x;
+    int K;
+    int xoff;
+};
+struct Bfp8SweepArgs {
+    const Bfp8GemvDesc* descs;
+    const Bfp8SweepTile* tiles;
+    const int* wg_off;
+    const Bfp8SweepAct* acts;
+    const int* act_off;
+    const uint8_t* head_mant;  // descs[head]'s planes and width (head >= 0)
+    const uint8_t* head_exps;
+    int head_K, head_ntiles;
+    int head;                  // -1: no lm_head
+    int merger;                // the workgroup that merges the lm_head's top-k
+    uint32_t epoch;            // 1 .. 2^14 - 1, different from the previous launch's
+};
+#define BFP8_SWEEP_LDS_WORDS 8192  // activation slots per workgroup (32 KiB)
+// Extra load, in blocks, that the in-launch top-k merge puts on the merging
+// workgroup of a single launch.
+#define BFP8_SWEEP_MERGE_COST_BLOCKS 64
+// Words of one activation slot of K elements (split words + scales, padded).
+static inline int bfp8_sweep_slot_words(int K) { return ((K >> 6) * 33 + 3) & ~3; }
+int bfp8_sweep_grid();
+hipError_t bfp8_launch_sweep(const Bfp8SweepArgs& a, int nwg, int lds_words, hipStream_t s);
 hipError_t bfp8_launch_gemv_batch(float* Y, const uint32_t* xsplit, const float* xscale,
                                   const uint8_t* mant, const uint8_t* exps, int M, int K, int B,
                                   hipStream_t s);

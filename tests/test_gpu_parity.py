@@ -465,7 +465,7 @@ def test_plan_rows_kernel_paths(gpu, torch_mod, case):
 
 
 @pytest.mark.parametrize("shape", ["alone", "with_small_gemv", "ragged_2049_tiles"])
-def test_plan_lm_head_merge_paths(gpu, torch_mod, shape):
+def test_plan_lm_head_merge_paths(gpu, torch_mod, shape, plan_mode):
     """A plan's lm_head merge runs as the stand-alone merge kernel (lm_head
     alone) or folded into workgroup 0 of the second launch (other GEMVs
     present, here a 2-tile one); a 2049-tile ragged vocabulary takes several
@@ -474,7 +474,7 @@ def test_plan_lm_head_merge_paths(gpu, torch_mod, shape):
     qk, torch = gpu, torch_mod
     V, H, k = {"alone": (16384, 1024, 64), "with_small_gemv": (65536, 1024, 40),
                "ragged_2049_tiles": (131074, 1024, 40)}[shape]
-    say("plan lm_head", shape, V, H, k)
+    say("plan lm_head", shape, V, H, k, plan_mode)
     lm = qk.DeviceMatrix.synth(V, H, 777, 122, 128)
     xl = qk.synth_normal(H, 778)
     items = [{"mat": lm, "x": torch.from_numpy(xl).cuda(), "topk": k}]
@@ -555,7 +555,7 @@ def test_random_batches_against_the_oracle(gpu, torch_mod):
             assert same_f32(Y[b], y_ref), (B, M, K, seed, b, mismatch(Y[b], y_ref))
 
 
-def test_random_plans_against_the_oracle(gpu, torch_mod):
+def test_random_plans_against_the_oracle(gpu, torch_mod, plan_mode):
     """Six seeded plans of 1-10 GEMVs (1-4,999 rows; K whole blocks up to 4,096
     or ragged; some sharing an activation tensor), most with one fused lm_head
     (even vocabularies up to 140,000, hidden 64-1,024, k in 1-64) at a random
@@ -586,7 +586,7 @@ def test_random_plans_against_the_oracle(gpu, torch_mod):
             items.insert(pos, {"mat": qk.DeviceMatrix.synth(V, H, seed, 122, 128),
                                "x": torch.from_numpy(x).cuda(), "topk": k})
             head = (V, H, k, seed, x)
-        say("random plan", p, [(M, K) for M, K, *_ in refs], head[:3] if head else None)
+        say("random plan", plan_mode, p, [(M, K) for M, K, *_ in refs], head[:3] if head else None)
         plan = qk.SweepPlan(items)
         for rep in range(2):
             for it in items:
@@ -636,9 +636,25 @@ def test_batch_odd_sizes(gpu, torch_mod):
         assert same_f32(Y[b], ol.gemv_neon(X[b], mant, exps)[0]), b
 
 
-def test_sweep_plan_24_layers_and_lm_head(gpu, torch_mod):
+@pytest.fixture(params=["two_launches", "single_launch"])
+def plan_mode(request):
+    """Plans created under this fixture take the default two launches, or the
+    opt-in single launch (BFP8_PLAN_SINGLE_LAUNCH=1 when the plan is created)."""
+    import os
+
+    old = os.environ.get("BFP8_PLAN_SINGLE_LAUNCH")
+    os.environ["BFP8_PLAN_SINGLE_LAUNCH"] = "1" if request.param == "single_launch" else "0"
+    yield request.param
+    if old is None:
+        del os.environ["BFP8_PLAN_SINGLE_LAUNCH"]
+    else:
+        os.environ["BFP8_PLAN_SINGLE_LAUNCH"] = old
+
+
+def test_sweep_plan_24_layers_and_lm_head(gpu, torch_mod, plan_mode):
     """The full synthetic decode sweep in one plan: 24 x {gate, up, down, in, out}
-    plus the fused lm_head, every output bit-exact, twice in a row."""
+    plus the fused lm_head, every output bit-exact, twice in a row, in both
+    launch modes."""
     qk, torch = gpu, torch_mod
     shapes = [(3584, 1024), (3584, 1024), (1024, 3584), (6144, 1024), (1024, 2048)]
     items, refs = [], []
@@ -655,8 +671,9 @@ def test_sweep_plan_24_layers_and_lm_head(gpu, torch_mod):
     xl = qk.synth_normal(1024, 99_998)
     items.insert(0, {"mat": lm, "x": torch.from_numpy(xl).cuda(), "topk": 40})
     plan = qk.SweepPlan(items)
+    assert (plan.kernel_name(0) == "bfp8_sweep_kernel") == (plan_mode == "single_launch")
     for rep in range(2):
-        say("sweep plan run", rep)
+        say("sweep plan run", plan_mode, rep)
         for it in items[1:]:
             it["y"].fill_(np.nan)
         plan.run()
