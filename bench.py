@@ -50,7 +50,7 @@ PKG = ROOT / "qwen35-ax7020-edge-llm_amd"
 sys.path.insert(0, str(PKG))
 
 PEAK_HBM_GBPS = 8000.0
-PEAK_VALU_INT_TOPS = 157.3  # v_dot4_i32_i8, two passes per int16 activation (see bench_batch16)
+PEAK_VALU_INT_TOPS = 157.3  # v_dot4_i32_i8 with two passes per int16 activation (see bench_batch16)
 LAYER = [("gate", 3584, 1024), ("up", 3584, 1024), ("down", 1024, 3584), ("in_proj", 6144, 1024),
          ("out_proj", 1024, 2048)]
 N_LAYERS = 24
@@ -104,11 +104,14 @@ def read_traffic(workload, kernel):
     return float(m.group(1)) if m else None
 
 
-def cpu_baseline(items, seconds=10.0, single_seconds=6.0):
+def cpu_baseline(items, seconds=10.0, single_seconds=6.0, batch=1, nbytes=None):
     """The reference's host bfp8_gemv (float path, 04/qwen_kernels_opt.c:311-325)
     built from its own sources (oracle/_ref), timed on this host over the same
     synthetic GEMV list; falls back to the oracle's restatement of that path.
-    Timed with the OpenMP default thread count, then with one thread."""
+    Timed with the OpenMP default thread count, then with one thread.  With
+    batch > 1 each GEMV is called once per activation vector (the reference
+    has no batched GEMV) and a pass counts `nbytes` (default: the list's
+    metric bytes)."""
     import numpy as np
 
     import qwen_kernels_gpu as qk
@@ -129,9 +132,11 @@ def cpu_baseline(items, seconds=10.0, single_seconds=6.0):
     host = []
     for i, (tag, M, K, lo, hi, tk) in enumerate(items):
         mant, exps = qk.synth_planes(M, K, 7_000 + i, lo, hi)
-        x = qk.synth_normal(K, 8_000 + i)
-        host.append((mant, exps, x, np.empty(M, dtype=np.float32), M, K))
-    nbytes = metric_bytes(items)
+        for b in range(batch):
+            x = qk.synth_normal(K, 8_000 + 100 * i + b)
+            host.append((mant, exps, x, np.empty(M, dtype=np.float32), M, K))
+    if nbytes is None:
+        nbytes = metric_bytes(items)
 
     def timed(limit):
         for mant, exps, x, y, M, K in host[:1]:  # first touch of the pages, untimed
@@ -156,16 +161,19 @@ def cpu_baseline(items, seconds=10.0, single_seconds=6.0):
     sweeps, el = timed(seconds)
     threads = gomp.omp_get_max_threads() if gomp else 1
     out = {"value": round(nbytes * sweeps / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
-           "sample": f"{sweeps} passes over the same GEMV list ({len(items)} GEMVs, {nbytes / 1e6:.1f} MB per pass; "
-                     f"the lm_head as a plain GEMV, the reference having no fused BFP8 lm_head), host float path "
-                     f"with OpenMP over rows (OMP_PROC_BIND={os.environ.get('OMP_PROC_BIND')}), {el:.1f} s"}
+           "sample": (f"{sweeps} passes over the same GEMV list ({len(items)} GEMVs, {nbytes / 1e6:.1f} MB per pass; "
+                      f"the lm_head as a plain GEMV, the reference having no fused BFP8 lm_head)" if batch == 1 else
+                      f"{sweeps} batches of {batch} bfp8_gemv calls on one {items[0][1]}x{items[0][2]} matrix "
+                      f"({nbytes / 1e6:.2f} MB per batch counted as for the GPU: weights once + f32 x in + f32 y out)")
+                     + f", host float path with OpenMP over rows (OMP_PROC_BIND={os.environ.get('OMP_PROC_BIND')}), "
+                       f"{el:.1f} s"}
     if gomp:
         # the same library with one OpenMP thread
         gomp.omp_set_num_threads(1)
         s1, e1 = timed(single_seconds)
         gomp.omp_set_num_threads(threads)
         out["single_thread"] = {"value": round(nbytes * s1 / e1 / 1e9, 3), "unit": "GB/s", "cores": 1,
-                                "sample": f"{s1} passes over the same list, {e1:.1f} s"}
+                                "sample": f"{s1} {'batches' if batch > 1 else 'passes over the same list'}, {e1:.1f} s"}
     return out
 
 
@@ -181,6 +189,8 @@ def main():
     ap.add_argument("--bf16-layout", choices=["tiles", "rows"], default="tiles",
                     help="lm_head_bf16: the library's cached tile layout or a row-major device table")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--batch-shape", choices=["all", "3584x1024", "65536x1024"], default="all",
+                    help="batch16: the matrix shapes to run")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -373,16 +383,21 @@ def main():
 
 def bench_batch16(args, qk, torch, np):
     """C4: B = 16 activation vectors against one weight matrix, weights read
-    once per batch, at 3584 x 1024 and at 65536 x 1024.  Past ~10 vectors the
-    batch is bound by the VALU, not HBM: the roofline is the int-op rate.
-    Peak: v_dot4_i32_i8 on 256 CUs x 64 lanes x 8 int-ops x 2.4 GHz =
-    314.6 TOP/s; an int16 activation takes two dot4 passes (its high and low
-    bytes), so 157.3 TOP/s of algorithmic int-ops (2 per weight per vector)."""
+    once per batch, at 3584 x 1024 and at 65536 x 1024, on the matrix-core
+    batch kernel (int8 MFMA for the exact residue sums, the float epilogue on
+    the VALU).  roofline: HBM, with the kernel's algorithmic bytes (weights +
+    int16 activations + f32 block scales + f32 outputs) over its time between
+    HIP events.  int_tops / valu_frac: algorithmic int-ops (2 per weight per
+    vector) against 157.3 TOP/s, the rate of v_dot4_i32_i8 on 256 CUs x 64
+    lanes x 8 int-ops x 2.4 GHz with two passes per int16 activation -- the
+    roof of a dot-product (non-MFMA) batch kernel."""
     B = 16
     lib = qk.load()
     s = torch.cuda.current_stream()
     shapes = []
     for M, K, e_lo, e_hi in ((3584, 1024, 124, 130), (65536, 1024, 122, 128)):
+        if args.batch_shape not in ("all", f"{M}x{K}"):
+            continue
         per_copy = wbytes(M, K)
         copies = max(1, int(np.ceil(args.rotate_gb * 1e9 / per_copy)))
         mats = [qk.DeviceMatrix.synth(M, K, 900 + c, e_lo, e_hi) for c in range(copies)]
@@ -393,30 +408,54 @@ def bench_batch16(args, qk, torch, np):
             qk.check(lib.bfp8_dev_quantize(None, xsc.data_ptr() + b * (K // 64) * 4, xsp.data_ptr() + b * (K // 64) * 128,
                                            X[b].data_ptr(), K, s.cuda_stream))
         Y = torch.empty((B, M), dtype=torch.float32, device="cuda")
+        # the launches' arguments resolved beforehand: a loop of bare ctypes
+        # calls keeps ahead of the GPU, so the events time the kernels
+        fn = lib.bfp8_dev_gemv_batch
+        call = [(Y.data_ptr(), xsp.data_ptr(), xsc.data_ptr(), m.mant.data_ptr(), m.exps.data_ptr(), M, K, B,
+                 s.cuda_stream) for m in mats]
         for i in range(args.warmup):
-            qk.gemv_batch(mats[i % copies], xsp, xsc, B, Y)
+            qk.check(fn(*call[i % copies]), "gemv_batch")
         torch.cuda.synchronize()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        rcs = []
         a.record(s)
         for i in range(args.steps):
-            qk.gemv_batch(mats[i % copies], xsp, xsc, B, Y)
+            rcs.append(fn(*call[i % copies]))
         b.record(s)
         torch.cuda.synchronize()
+        if any(rcs):
+            raise RuntimeError(f"bfp8_dev_gemv_batch failed: {set(rcs)}")
         us = a.elapsed_time(b) * 1e3 / args.steps
         gbs = (per_copy + B * 4 * K + B * 4 * M) / (us * 1e-6) / 1e9
         tops = 2.0 * M * K * B / (us * 1e-6) / 1e12
+        kbytes = per_copy + B * (2 * K + 4 * (K // 64)) + B * 4 * M
+        kgbs = kbytes / (us * 1e-6) / 1e9
         shapes.append({"M": M, "K": K, "B": B, "us": round(us, 3), "GBps": round(gbs, 2), "int_tops": round(tops, 3),
-                       "rotating_copies": copies,
-                       "roofline": {"bound": "valu", "achieved": round(tops, 3), "peak": PEAK_VALU_INT_TOPS,
-                                    "unit": "TOP/s", "frac": round(tops / PEAK_VALU_INT_TOPS, 4)}})
+                       "valu_frac": round(tops / PEAK_VALU_INT_TOPS, 4), "rotating_copies": copies,
+                       "roofline": {"bound": "hbm", "achieved": round(kgbs, 2), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                                    "frac": round(kgbs / PEAK_HBM_GBPS, 4), "algorithmic_bytes": kbytes,
+                                    "traffic": read_traffic("batch16", f"bfp8_gemv_batch_mfma_kernel@{M}x{K}")}})
         del mats, X, Y
+    # a copy of known size: the PMC counters' calibration kernel
+    src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+    cpy = torch.empty_like(src)
+    qk.check(lib.bfp8_dev_copy_probe(cpy.data_ptr(), src.data_ptr(), cpy.numel(), s.cuda_stream))
+    torch.cuda.synchronize()
+    del src, cpy
     first = shapes[0]
-    print(json.dumps({"metric": "BFP8 GEMV B=16 achieved GB/s and int Tops/s", "value": first["GBps"],
-                      "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-                      "us_per_step": first["us"], "int_tops": first["int_tops"], "higher_is_better": True,
-                      "dtype": "int8xint16->int32, f32 epilogue", "data": "synthetic",
-                      "config": {"workload": "batch16", "M": first["M"], "K": first["K"], "B": B},
-                      "roofline": first["roofline"], "shapes": shapes}))
+    out = {"metric": "BFP8 GEMV B=16 achieved GB/s and int Tops/s", "value": first["GBps"],
+           "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "us_per_step": first["us"], "int_tops": first["int_tops"], "valu_frac": first["valu_frac"],
+           "higher_is_better": True,
+           "dtype": "int8xint16->int32, f32 epilogue", "data": "synthetic",
+           "config": {"workload": "batch16", "M": first["M"], "K": first["K"], "B": B},
+           "roofline": first["roofline"], "shapes": shapes}
+    if not args.no_cpu:
+        print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
+        M, K = first["M"], first["K"]
+        out["cpu_baseline"] = cpu_baseline([("batch16", M, K, 124, 130, 0)], batch=B,
+                                           nbytes=wbytes(M, K) + B * 4 * K + B * 4 * M)
+    print(json.dumps(out), flush=True)
 
 
 def bench_lm_head_bf16(args, qk, torch, np):

@@ -1,0 +1,265 @@
+// batch_mfma.hip -- the batched BFP8 GEMV (8..16 activation vectors against
+// one weight matrix, weights read once) on the matrix cores, f32 flush-to-zero
+// like the reference's Advanced SIMD epilogue.
+//
+// The reference has no batched GEMV: a batch is B calls of bfp8_gemv
+// (04/qwen_kernels_opt.c:207-278), each keeping four int32 residue lanes per
+// row and block (elements k = q mod 4), S_q = sum of mantissa * xq, and a
+// float epilogue per block  fs_q += (float(S_q) * 2^(e-134)) * xscale,
+// y = (fs_0 + fs_2) + (fs_1 + fs_3).
+//
+// Integer part on v_mfma_i32_32x32x16_i8, whose K of 16 is exactly the 16
+// elements of one residue of one block.  With xq = 256*xh + xl (xh, xl int8,
+// bfp8_layout.h) one MFMA computes, for 32 weight rows and residue q,
+//   D[(v, p)][row] = sum over the residue's 16 elements of x_p[v] * m[row]
+// for the 16 vectors v and both parts p (h, l) as its 32 rows: the A operand
+// is the batch's split activations, the B operand the weight plane's
+// residue-q slice.  A lane of D holds column `row` and rows 8(i/4) + 4(l/32)
+// + i%4 (i < 16), so its registers i and i + 8 are the h and l sums of the same
+// vector: S_q = 256 * D[i] + D[i + 8] exactly, in the lane, for 8 vectors.
+// Integer sums are exact in any order.
+//
+// Float part, per (row, vector, block, residue), in the reference's order:
+// float(S_q) * es * xs with es = 2^(e-134) a power of two.  float(S_q) * es is
+// exact whenever it is a normal float (e in 8..236: |S_q| <= 2^25), so the two
+// products round once, on S_q * es * xs.  When c = es * xs is itself a normal
+// float it is exact too, and float(S_q) * c rounds the same real number: one
+// product instead of two.  Each block checks that c is normal for every
+// vector of the batch (a range of e computed from the batch's block scales)
+// and takes the two products otherwise; e < 8 (es = 0) and zero, infinite or
+// NaN scales give the same result either way.
+//
+// Work split: a workgroup per 64-row tile; wavefront (s, g) takes the tile's
+// 32-row half s and the residues of group g (kRes residues per wavefront: 2 or,
+// for GEMVs with few tiles, 1, so that more wavefronts run), keeping fs_q of
+// its residues; the wavefronts of a half combine their fs_q into y at the end
+// through LDS.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "bfp8_internal.h"
+#include "bfp8_layout.h"
+#include "gemv_dev.h"
+
+namespace {
+
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kMfVec = 16;    // vectors (the MFMA's rows are vector x part)
+constexpr int kMfChunk = 16;  // blocks of split activations staged in LDS at a time
+constexpr int kMfGroup = 2;   // blocks per weight-load group
+
+struct MfLds {
+    // A operands: [block][residue][k half][part][vector], 8 bytes each: the
+    // 64 lanes of one (block, residue) read 512 contiguous bytes
+    uint64_t xa[kMfChunk][4][64];
+    float xs[kMfChunk][kMfVec];      // [block][vector] block scales
+    int lo[kMfChunk], hi[kMfChunk];  // per block: e range of the one-product epilogue
+};
+// the end's exchange: 3 residue groups x 2 halves x 8 values x 64 lanes at most
+static_assert(sizeof(MfLds::xa) >= 3 * 2 * 8 * 64 * sizeof(float), "the fs exchange fits in the staging area");
+
+// Stages blocks c0 .. c0+nbc-1 of the B split activations and scales (vectors
+// >= B and blocks >= nbc as zeros), then each block's exponent range
+// [lo, hi] inside which es * xs is a normal float for every normal scale xs of
+// the batch: biased exponent of es * xs = e - 134 + E(xs), normal for
+// 1..254, and e <= 236 keeps float(S) * es finite.
+__device__ void mf_stage(MfLds& L, const uint32_t* __restrict__ xsplit, const float* __restrict__ xscale, int nb,
+                         int B, int c0, int nbc) {
+    // 16 bytes of xsplit = one part of one residue (both k halves): item
+    // ((u * 4 + q) * 2 + p) * 16 + v, vectors fastest, so the LDS stores of
+    // consecutive threads are consecutive
+    for (int i = threadIdx.x; i < kMfChunk * 4 * 2 * kMfVec; i += blockDim.x) {
+        const int v = i % kMfVec, p = (i / kMfVec) % 2, q = (i / (2 * kMfVec)) % 4, u = i / (8 * kMfVec);
+        u32x4 val = {0u, 0u, 0u, 0u};
+        if (v < B && u < nbc)
+            val = *reinterpret_cast<const u32x4*>(xsplit + ((size_t)v * nb + c0 + u) * BFP8_XSPLIT_WORDS_PER_BLOCK +
+                                                  q * 8 + p * 4);
+        L.xa[u][q][p * 16 + v] = ((uint64_t)val.y << 32) | val.x;       // k half 0: bytes 0..7
+        L.xa[u][q][32 + p * 16 + v] = ((uint64_t)val.w << 32) | val.z;  // k half 1: bytes 8..15
+    }
+    for (int i = threadIdx.x; i < kMfChunk * kMfVec; i += blockDim.x) {
+        const int v = i % kMfVec, u = i / kMfVec;
+        const float xs = (v < B && u < nbc) ? xscale[(size_t)v * nb + c0 + u] : 0.0f;
+        L.xs[u][v] = xs;
+        const int E = (int)((__float_as_uint(xs) >> 23) & 0xffu);
+        const bool normal = E >= 1 && E <= 254;
+        int emin = normal ? E : 255, emax = normal ? E : 0;
+#pragma unroll
+        for (int m = 1; m < kMfVec; m <<= 1) {  // over the 16 lanes of block u
+            emin = min(emin, __shfl_xor(emin, m, 64));
+            emax = max(emax, __shfl_xor(emax, m, 64));
+        }
+        if (v == 0) {
+            L.lo[u] = 135 - emin;
+            L.hi[u] = min(236, 388 - emax);
+        }
+    }
+    __syncthreads();
+}
+
+template <int kRes>
+struct MfState {
+    float fs[kRes][8];  // [residue of the group][i]: vector 8(i/4) + 4*kh + i%4, the lane's row
+};
+
+struct MfLoads {
+    uint64_t w[kMfGroup][2];  // [block][residue of the group] (the second unused for kRes = 1)
+    uint32_t e;
+};
+
+// One block: an MFMA per residue of the group and the epilogue.
+template <int kRes>
+__device__ __forceinline__ void mf_block(MfState<kRes>& st, const MfLds& L, const uint64_t (&w)[2], uint32_t e,
+                                         int u, int q0, int lane) {
+    i32x16 d[kRes];
+    const i32x16 zero = {};
+#pragma unroll
+    for (int r = 0; r < kRes; ++r)
+        d[r] = __builtin_amdgcn_mfma_i32_32x32x16_i8((long)L.xa[u][q0 + r][lane], (long)w[r], zero, 0, 0, 0);
+    const int kh = lane >> 5;
+    const f32x4 xa = *reinterpret_cast<const f32x4*>(&L.xs[u][4 * kh]);
+    const f32x4 xb = *reinterpret_cast<const f32x4*>(&L.xs[u][8 + 4 * kh]);
+    const float xs[8] = {xa[0], xa[1], xa[2], xa[3], xb[0], xb[1], xb[2], xb[3]};
+    const float es = exp_scale_ftz(e);
+    const int lo = L.lo[u], hi = L.hi[u];
+    const bool one_product = (e < 8u) | ((uint32_t)((int)e - lo) <= (uint32_t)(hi - lo));
+    if (__builtin_amdgcn_ballot_w64(!one_product) == 0) {
+        float c[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) c[i] = es * xs[i];
+#pragma unroll
+        for (int r = 0; r < kRes; ++r)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int S = (int)((uint32_t)d[r][i] << 8) + d[r][i + 8];
+                st.fs[r][i] = st.fs[r][i] + (float)S * c[i];
+            }
+    } else {
+#pragma unroll
+        for (int r = 0; r < kRes; ++r)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int S = (int)((uint32_t)d[r][i] << 8) + d[r][i + 8];
+                const float t1 = (float)S * es;
+                st.fs[r][i] = st.fs[r][i] + t1 * xs[i];
+            }
+    }
+}
+
+// Weights of group gi (blocks kMfGroup*gi ..) for the lane's row, k half and
+// the group's residues, and the row's exponent dword holding them (4 blocks
+// per dword).  The whole offset goes in the per-lane offset, which the buffer
+// range check covers: groups past the tile read zeros without touching memory.
+static_assert(4 % kMfGroup == 0, "a group's exponents share one dword");
+template <int kRes>
+__device__ __forceinline__ void mf_issue(MfLoads& ld, __amdgpu_buffer_rsrc_t wrs, __amdgpu_buffer_rsrc_t ers, int wv,
+                                         int ev, int gi) {
+#pragma unroll
+    for (int uu = 0; uu < kMfGroup; ++uu)
+#pragma unroll
+        for (int r = 0; r < kRes; ++r) {
+            const u32x2 v = __builtin_bit_cast(
+                u32x2, __builtin_amdgcn_raw_buffer_load_b64(wrs, wv + (gi * kMfGroup + uu) * 4096 + r * 1024, 0,
+                                                            kNonTemporal));
+            ld.w[uu][r] = ((uint64_t)v.y << 32) | v.x;
+        }
+    ld.e = load_e(ers, ev + (gi * kMfGroup / 4) * 256, 0);
+}
+
+template <int kRes>
+__device__ __forceinline__ void mf_group(MfState<kRes>& st, MfLds& L, const MfLoads& ld, int gi, int nb,
+                                         const uint32_t* __restrict__ xsplit, const float* __restrict__ xscale, int B,
+                                         int q0, int lane) {
+    const int b0 = gi * kMfGroup;
+    if (b0 % kMfChunk == 0) {
+        __syncthreads();  // every wavefront is done with the previous chunk
+        mf_stage(L, xsplit, xscale, nb, B, b0, min(kMfChunk, nb - b0));
+    }
+#pragma unroll
+    for (int uu = 0; uu < kMfGroup; ++uu) {
+        if (b0 + uu >= nb) break;
+        mf_block<kRes>(st, L, ld.w[uu], (ld.e >> (8 * ((b0 + uu) & 3))) & 0xffu, (b0 + uu) % kMfChunk, q0, lane);
+    }
+}
+
+template <int kRes>
+__global__ __launch_bounds__(64 * 2 * (4 / kRes)) void bfp8_gemv_batch_mfma_kernel(
+    float* __restrict__ Y, const uint32_t* __restrict__ xsplit, const float* __restrict__ xscale,
+    const uint8_t* __restrict__ mant, const uint8_t* __restrict__ exps, int M, int K, int B) {
+    __shared__ MfLds L;
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int s = w & 1, grp = w >> 1;  // 32-row half, residue group
+    const int q0 = grp * kRes;
+    const int col = lane & 31, kh = lane >> 5;
+    const int t = blockIdx.x;
+    const int nb = K >> 6, nb4 = (nb + 3) >> 2;
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(mant + (size_t)t * nb * 4096u, (uint32_t)nb * 4096u);
+    const __amdgpu_buffer_rsrc_t ers = make_rsrc(exps + (size_t)t * nb4 * 256u, (uint32_t)nb4 * 256u);
+    const int wv = q0 * 1024 + (32 * s + col) * 16 + kh * 8;
+    const int ev = (32 * s + col) * 4;
+    MfState<kRes> st;
+#pragma unroll
+    for (int r = 0; r < kRes; ++r)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) st.fs[r][i] = 0.0f;
+    const int ng = (nb + kMfGroup - 1) / kMfGroup;
+    MfLoads A, Bq;
+    mf_issue<kRes>(A, wrs, ers, wv, ev, 0);
+    for (int gi = 0; gi < ng; gi += 2) {
+        // two load sets in alternating roles: the next group is always in flight
+        mf_issue<kRes>(Bq, wrs, ers, wv, ev, gi + 1);
+        mf_group<kRes>(st, L, A, gi, nb, xsplit, xscale, B, q0, lane);
+        mf_issue<kRes>(A, wrs, ers, wv, ev, gi + 2);
+        if (gi + 1 < ng) mf_group<kRes>(st, L, Bq, gi + 1, nb, xsplit, xscale, B, q0, lane);
+    }
+    float (&fs)[kRes][8] = st.fs;
+
+    // y = (fs_0 + fs_2) + (fs_1 + fs_3): the other residue groups of the half
+    // hand their sums to group 0 through the (no longer needed) staging area
+    __syncthreads();
+    float* xch = reinterpret_cast<float*>(&L.xa[0][0][0]);  // [group - 1][half][residue][i][lane]
+    if (grp > 0) {
+#pragma unroll
+        for (int r = 0; r < kRes; ++r)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) xch[((((grp - 1) * 2 + s) * kRes + r) * 8 + i) * 64 + lane] = fs[r][i];
+    }
+    __syncthreads();
+    if (grp == 0) {
+        const int row = t * 64 + 32 * s + col;
+        const int pair_rows = M & ~1;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            float f[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int gq = q / kRes, rq = q % kRes;
+                f[q] = gq == 0 ? fs[rq][i] : xch[((((gq - 1) * 2 + s) * kRes + rq) * 8 + i) * 64 + lane];
+            }
+            const int v = 8 * (i / 4) + 4 * kh + (i % 4);
+            const float y = (f[0] + f[2]) + (f[1] + f[3]);
+            if (v < B && row < pair_rows) Y[(size_t)v * M + row] = y;
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t bfp8_launch_gemv_batch_mfma(float* Y, const uint32_t* xsplit, const float* xscale, const uint8_t* mant,
+                                       const uint8_t* exps, int M, int K, int B, hipStream_t s) {
+    const int nt = bfp8_ntiles(M);
+    if (nt == 0) return hipSuccess;
+    if (B < 1 || B > kMfVec || K < 64 || (K & 63)) return hipErrorInvalidValue;
+    // few tiles: one residue per wavefront (8 per tile) so that more run
+    if (nt < 512)
+        hipLaunchKernelGGL(bfp8_gemv_batch_mfma_kernel<1>, dim3(nt), dim3(512), 0, s, Y, xsplit, xscale, mant, exps,
+                           M, K, B);
+    else
+        hipLaunchKernelGGL(bfp8_gemv_batch_mfma_kernel<2>, dim3(nt), dim3(256), 0, s, Y, xsplit, xscale, mant, exps,
+                           M, K, B);
+    return hipGetLastError();
+}

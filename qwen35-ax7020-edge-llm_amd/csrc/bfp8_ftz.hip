@@ -841,12 +841,10 @@ static int cu_count() {
     return n;
 }
 
-hipError_t bfp8_launch_gemv_batch(float* Y, const uint32_t* xsplit, const float* xscale,
-                                  const uint8_t* mant, const uint8_t* exps, int M, int K, int B,
-                                  hipStream_t s) {
+// One launch of the dot-product kernel for B in {1, 2, 4}.
+static hipError_t launch_batch_pow2(float* Y, const uint32_t* xsplit, const float* xscale, const uint8_t* mant,
+                                    const uint8_t* exps, int M, int K, int B, hipStream_t s) {
     const int nt = bfp8_ntiles(M);
-    if (nt == 0) return hipSuccess;
-    if (B != 1 && B != 2 && B != 4 && B != 8 && B != 16) return hipErrorInvalidValue;
     // while the tiles leave CUs idle, split the vectors over more workgroups
     // (each re-reads its tile's weights, from L2 / MALL for such small GEMVs)
     int groups = 1;
@@ -854,8 +852,27 @@ hipError_t bfp8_launch_gemv_batch(float* Y, const uint32_t* xsplit, const float*
     switch (B / groups) {
         case 1: return launch_batch_t<1>(Y, xsplit, xscale, mant, exps, M, K, groups, s);
         case 2: return launch_batch_t<2>(Y, xsplit, xscale, mant, exps, M, K, groups, s);
-        case 4: return launch_batch_t<4>(Y, xsplit, xscale, mant, exps, M, K, groups, s);
-        case 8: return launch_batch_t<8>(Y, xsplit, xscale, mant, exps, M, K, groups, s);
-        default: return launch_batch_t<16>(Y, xsplit, xscale, mant, exps, M, K, groups, s);
+        default: return launch_batch_t<4>(Y, xsplit, xscale, mant, exps, M, K, groups, s);
     }
+}
+
+hipError_t bfp8_launch_gemv_batch(float* Y, const uint32_t* xsplit, const float* xscale,
+                                  const uint8_t* mant, const uint8_t* exps, int M, int K, int B,
+                                  hipStream_t s) {
+    if (bfp8_ntiles(M) == 0) return hipSuccess;
+    if (B < 1 || B > 16) return hipErrorInvalidValue;
+    // from 8 vectors on, the matrix cores: their epilogue costs the same for
+    // 8 and for 16 vectors, the dot-product kernel's grows with B
+    if (B >= 8) return bfp8_launch_gemv_batch_mfma(Y, xsplit, xscale, mant, exps, M, K, B, s);
+    const int nb = K >> 6;
+    int done = 0;
+    while (done < B) {
+        int step = 4;
+        while (step > B - done) step >>= 1;
+        const hipError_t e = launch_batch_pow2(Y + (size_t)done * M, xsplit + (size_t)done * nb * 32,
+                                               xscale + (size_t)done * nb, mant, exps, M, K, step, s);
+        if (e != hipSuccess) return e;
+        done += step;
+    }
+    return hipSuccess;
 }

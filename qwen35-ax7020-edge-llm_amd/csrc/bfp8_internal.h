@@ -167,9 +167,17 @@ struct Bfp8SweepArgs {
 static inline int bfp8_sweep_slot_words(int K) { return ((K >> 6) * 33 + 3) & ~3; }
 int bfp8_sweep_grid();
 hipError_t bfp8_launch_sweep(const Bfp8SweepArgs& a, int nwg, int lds_words, hipStream_t s);
+// Y[v][M] for v < B (1..16): B split activations (rows of nb*32 words) and
+// scales (rows of nb floats); pair rows only (the odd last row is the tail
+// kernel's).  8..16 vectors run on the matrix cores (batch_mfma.hip), fewer
+// on the dot-product kernel, in power-of-two steps.
 hipError_t bfp8_launch_gemv_batch(float* Y, const uint32_t* xsplit, const float* xscale,
                                   const uint8_t* mant, const uint8_t* exps, int M, int K, int B,
                                   hipStream_t s);
+
+// ---- batch_mfma.hip -------------------------------------------------------
+hipError_t bfp8_launch_gemv_batch_mfma(float* Y, const uint32_t* xsplit, const float* xscale, const uint8_t* mant,
+                                       const uint8_t* exps, int M, int K, int B, hipStream_t s);
 
 // ---- bf16_head.hip --------------------------------------------------------
 hipError_t bf16_launch_lm_head(const Bf16HeadDesc& d, hipStream_t s);

@@ -615,20 +615,13 @@ void bfp8_gemv_batch(float* Y, const float* X, const int8_t* mantissas, const ui
     if (!rc) rc = g.h_out.reserve((size_t)B * M * 4);
     for (int b0 = 0; !rc && b0 < B; b0 += 16) {
         const int bc = std::min(16, B - b0);
-        int done = 0;
-        while (!rc && done < bc) {
-            int step = 16;
-            while (step > bc - done) step >>= 1;
-            const int v0 = b0 + done;
-            hipError_t e = bfp8_launch_gemv_batch(g.y.as<float>() + (size_t)v0 * M,
-                                                  g.xsplit.as<uint32_t>() + (size_t)v0 * nb * 32,
-                                                  g.xscale.as<float>() + (size_t)v0 * nb, w.mant, w.exps, M, K,
-                                                  step, g.stream);
-            if (e != hipSuccess) {
-                set_error("batched GEMV launch: %s", hipGetErrorString(e));
-                rc = BFP8_EHIP;
-            }
-            done += step;
+        hipError_t e = bfp8_launch_gemv_batch(g.y.as<float>() + (size_t)b0 * M,
+                                              g.xsplit.as<uint32_t>() + (size_t)b0 * nb * 32,
+                                              g.xscale.as<float>() + (size_t)b0 * nb, w.mant, w.exps, M, K, bc,
+                                              g.stream);
+        if (e != hipSuccess) {
+            set_error("batched GEMV launch: %s", hipGetErrorString(e));
+            rc = BFP8_EHIP;
         }
     }
     for (int b = 0; !rc && b < B && (M & 1); ++b) {
@@ -877,14 +870,7 @@ int bfp8_dev_gemv_batch(float* Y, const uint32_t* xsplit, const float* xscale, c
     DEV_PROLOGUE();
     hipStream_t s = pick_stream(stream);
     const int nb = bfp8_nblocks(K);
-    int done = 0;
-    while (done < B) {
-        int step = 16;
-        while (step > B - done) step >>= 1;
-        HIP_OK(bfp8_launch_gemv_batch(Y + (size_t)done * M, xsplit + (size_t)done * nb * 32,
-                                      xscale + (size_t)done * nb, (const uint8_t*)mant_gpu, exps_gpu, M, K, step, s));
-        done += step;
-    }
+    HIP_OK(bfp8_launch_gemv_batch(Y, xsplit, xscale, (const uint8_t*)mant_gpu, exps_gpu, M, K, B, s));
     if (M & 1)
         for (int b = 0; b < B; ++b)
             HIP_OK(bfp8_launch_tail_row(Y + (size_t)b * M, xsplit + (size_t)b * nb * 32, xscale + (size_t)b * nb,

@@ -625,6 +625,32 @@ def test_batch16_matches_sixteen_single_calls(gpu, torch_mod, M):
         assert same_f32(Y[b], y_ref), (b, mismatch(Y[b], y_ref))
 
 
+@pytest.mark.parametrize("B,M,K", [(8, 131, 512), (11, 64, 4096), (16, 1000, 1088)])
+def test_batch_scale_edges(gpu, torch_mod, B, M, K):
+    """Batches of 8-16 vectors (the matrix-core kernel) whose block scales
+    span the float range: every exponent byte 0-255 across rows and blocks,
+    vectors scaled by 10^-40 .. 10^35 (subnormal to huge block scales, so that
+    2^(e-134) * xscale underflows or overflows for some blocks while the
+    reference's two products do not), zero blocks and single huge elements.
+    Each vector bit-exact against the restatement."""
+    qk = gpu
+    rng = np.random.default_rng(B * 1000 + M)
+    nb = K // 64
+    mant = rng.integers(-128, 128, size=(M, K), dtype=np.int8)
+    exps = ((np.arange(M)[:, None] * 7 + np.arange(nb)[None, :] * 29) % 256).astype(np.uint8)
+    X = np.empty((B, K), dtype=F32)
+    for b in range(B):
+        with np.errstate(over="ignore", under="ignore"):
+            X[b] = (rng.standard_normal(K) * 10.0 ** (-40 + 5 * (b % 16))).astype(F32)
+        X[b, (b % nb) * 64:(b % nb) * 64 + 64] = 0.0      # a zero block
+        X[b, rng.integers(0, K)] = F32(3.0e38) if b % 3 == 0 else F32(-1.0e-42)
+    say("batch scale edges", B, M, K)
+    Y = qk.Bfp8Kernels().gemv_batch(X, mant, exps, M, K)
+    for b in range(B):
+        y_ref, *_ = ol.gemv_neon(X[b], mant, exps)
+        assert same_f32(Y[b], y_ref), (B, M, K, b, mismatch(Y[b], y_ref))
+
+
 def test_batch_odd_sizes(gpu, torch_mod):
     qk = gpu
     M, K, B = 129, 2048, 5
