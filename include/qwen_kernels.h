@@ -20,8 +20,11 @@
  *     BFP8_E* code.  These keep weights and activations resident in HBM.
  *
  * Failure behaviour: the reference's bfp8_gemv has no error channel
- * (04/qwen_kernels_opt.c:207, void).  A void entry point of this library
- * that cannot run on the GPU prints the HIP error to stderr and aborts the
+ * (04/qwen_kernels_opt.c:207, void).  init_kernels() never aborts; without a
+ * usable GPU it prints why and bfp8_gpu_ready() returns 0, so an engine can
+ * keep its own numpy path (the reference engine's behaviour when the library
+ * does not load, 04/qwen_real_engine.py:663-671).  A void compute entry point
+ * called without a usable GPU prints the HIP error to stderr and aborts the
  * process: there is no silent CPU fallback.  Int-returning entry points
  * return their error value instead; bfp8_last_error() gives the message.
  *
@@ -49,8 +52,17 @@ extern "C" {
 /* ---- 1. reference symbols -------------------------------------------------- */
 
 /* Replaces init_kernels(), 04/qwen_kernels_opt.c:128-135.  Also selects the
- * GPU (current HIP device) and creates the library's stream.  Idempotent. */
+ * GPU (current HIP device) and creates the library's stream.  Idempotent.
+ * Does not fail: without a usable GPU it prints the reason to stderr and
+ * bfp8_gpu_ready() returns 0. */
 void init_kernels(void);
+
+/* 1 when the GPU path can run: a HIP device that is gfx950, this library's
+ * code object loaded on it.  0 otherwise, with bfp8_last_error() set.  No
+ * counterpart in the reference (whose CPU library is always usable); it is
+ * what an engine checks after init_kernels() to fall back to its own numpy
+ * path instead of calling entry points that would abort. */
+int bfp8_gpu_ready(void);
 
 /* Replaces bfp8_gemv(), 04/qwen_kernels_opt.c:207-326.
  * y[M] = BFP8 W[M][K] (mantissas int8 [M][K], row stride K; exps uint8

@@ -740,6 +740,11 @@ static int resident_grid(const void* kernel) {
     return cus * (occ < BFP8_STREAM_WG_PER_CU ? occ : BFP8_STREAM_WG_PER_CU);
 }
 
+hipError_t bfp8_probe_code_object() {
+    hipFuncAttributes attr;
+    return hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(bfp8_gemv_grouped_kernel));
+}
+
 int bfp8_stream_grid() {
     static const int a = resident_grid(reinterpret_cast<const void*>(bfp8_gemv_grouped_kernel));
     static const int b = resident_grid(reinterpret_cast<const void*>(bfp8_gemv_grouped_merge_kernel));

@@ -129,6 +129,9 @@ hipError_t bfp8_launch_gemv_head(const Bfp8HeadArgs& a, int nwg, hipStream_t s);
 #define BFP8_MERGE_COST_BLOCKS 16
 // Number of workgroups the persistent GEMV kernels keep resident.
 int bfp8_stream_grid();
+// hipSuccess when this library's gfx950 code object loads on the current
+// device (an attribute query of one of its kernels).
+hipError_t bfp8_probe_code_object();
 
 // ---- sweep.hip: a whole plan in one persistent launch -----------------------
 // Workgroup w takes its lm_head tiles (w, w + grid, ... of descs[head], whose

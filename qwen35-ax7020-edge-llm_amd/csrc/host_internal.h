@@ -125,6 +125,7 @@ struct StreamScratch {
 struct State {
     std::mutex mu;
     bool ready = false;
+    bool gpu_checked = false, gpu_ok = false;  // bfp8_gpu_ready()'s verdict, once per process
     int device = 0;
     hipStream_t stream = nullptr;
     PinnedBuf h_in, h_out;

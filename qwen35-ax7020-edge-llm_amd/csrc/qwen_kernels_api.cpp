@@ -565,16 +565,56 @@ using namespace qhost;
 // =========================== C ABI ================================================
 extern "C" {
 
+// Whether the GPU path can run here: a HIP device, gfx950, this library's code
+// object loaded on it, and the no-alloc scratch's address looked up.
+// Records the reason in bfp8_last_error() otherwise.
+static int gpu_ready_locked() {
+    if (g.gpu_checked) return g.gpu_ok ? BFP8_OK : BFP8_EHIP;
+    g.gpu_checked = true;
+    if (ensure_init_locked() != BFP8_OK) return BFP8_EHIP;
+    hipDeviceProp_t prop;
+    hipError_t e = hipGetDeviceProperties(&prop, g.device);
+    if (e != hipSuccess) {
+        set_error("hipGetDeviceProperties: %s", hipGetErrorString(e));
+        return BFP8_EHIP;
+    }
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        set_error("device %d is %s; this library is built for gfx950 only", g.device, prop.gcnArchName);
+        return BFP8_EHIP;
+    }
+    if ((e = bfp8_probe_code_object()) != hipSuccess) {
+        set_error("the gfx950 code object does not load: %s", hipGetErrorString(e));
+        return BFP8_EHIP;
+    }
+    void* scratch = nullptr;  // the no-alloc lm_head's device scratch: its address on this device
+    if ((e = bfp8_noalloc_setup(&scratch)) != hipSuccess) {
+        set_error("hipGetSymbolAddress of the no-alloc scratch: %s", hipGetErrorString(e));
+        return BFP8_EHIP;
+    }
+    g.gpu_ok = true;
+    return BFP8_OK;
+}
+
+// The reference's init_kernels cannot fail (04/qwen_kernels_opt.c:128-135),
+// and the engine calls it inside the try block that picks the library
+// (04/qwen_real_engine.py:663-671).  So it never aborts: without a usable GPU
+// it leaves the reason in bfp8_last_error() and bfp8_gpu_ready() returns 0,
+// which is what an engine checks to keep its own numpy path.
 void init_kernels(void) {
     std::lock_guard<std::mutex> lk(g.mu);
-    if (ensure_init_locked() != BFP8_OK) fatal("init_kernels");
-    // the no-alloc lm_head's device scratch: its address on this device
-    void* scratch = nullptr;
-    const hipError_t e = bfp8_noalloc_setup(&scratch);
-    if (e != hipSuccess) {
-        set_error("hipGetSymbolAddress of the no-alloc scratch: %s", hipGetErrorString(e));
-        fatal("init_kernels");
+    if (gpu_ready_locked() != BFP8_OK) {
+        std::string msg;
+        {
+            std::lock_guard<std::mutex> el(g_err_mu);
+            msg = g_err;
+        }
+        fprintf(stderr, "libqwen_kernels: init_kernels: GPU path unavailable: %s\n", msg.c_str());
     }
+}
+
+int bfp8_gpu_ready(void) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    return gpu_ready_locked() == BFP8_OK ? 1 : 0;
 }
 
 void bfp8_gemv(float* y, const float* x, const int8_t* mantissas, const uint8_t* exps, int M, int K) {

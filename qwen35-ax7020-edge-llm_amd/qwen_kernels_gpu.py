@@ -145,6 +145,8 @@ def bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.bfp8_dev_pack_rows.restype = i
     lib.bfp8_last_error.argtypes = []
     lib.bfp8_last_error.restype = ctypes.c_char_p
+    lib.bfp8_gpu_ready.argtypes = []
+    lib.bfp8_gpu_ready.restype = ctypes.c_int
     lib.bfp8_cache_clear.argtypes = []
     lib.bfp8_cache_clear.restype = None
     # device level

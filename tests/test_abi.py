@@ -132,6 +132,56 @@ def test_device_call_without_gpu_reports_error():
                                  x.ctypes.data) == 0  # invalid k: rejected before any GPU work
 
 
+def test_init_without_gpu_returns_and_reports_not_ready():
+    """init_kernels() cannot fail in the reference (04/qwen_kernels_opt.c:128-135)
+    and the engine calls it inside its library-selection try block: without a
+    GPU it returns, and bfp8_gpu_ready() says 0 with the reason."""
+    import torch
+
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    code = (
+        "import sys; sys.path.insert(0, %r)\n"
+        "import qwen_kernels_gpu as qk\n"
+        "k = qk.load(); k.init_kernels(); k.init_kernels()\n"
+        "print('READY', k.bfp8_gpu_ready(), k.bfp8_last_error().decode())\n" % str(ROOT / "qwen35-ax7020-edge-llm_amd"))
+    res = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120,
+                         env={"HIP_VISIBLE_DEVICES": "", "PATH": "/usr/bin:/bin"})
+    assert res.returncode == 0, res.stderr
+    assert "READY 0 no HIP device" in res.stdout
+    assert "GPU path unavailable" in res.stderr
+
+
+def test_engine_style_loader_keeps_its_numpy_path_without_gpu():
+    """The engine's loader (04/qwen_real_engine.py:656-671) with the one added
+    readiness check shown in INTEGRATION.md: without a GPU it ends with no
+    kernel library, i.e. on the engine's own numpy path, instead of a process
+    abort at the first GEMV."""
+    import torch
+
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    lib = ROOT / "qwen35-ax7020-edge-llm_amd" / "libqwen_kernels.so"
+    code = (
+        "import ctypes\n"
+        "kernels = None\n"
+        "for cand in [%r]:\n"
+        "    try:\n"
+        "        kernels = ctypes.CDLL(cand)\n"
+        "        if hasattr(kernels, 'init_kernels'):\n"
+        "            kernels.init_kernels()\n"
+        "        if hasattr(kernels, 'bfp8_gpu_ready') and not kernels.bfp8_gpu_ready():\n"
+        "            raise OSError('GPU path unavailable')\n"
+        "        break\n"
+        "    except Exception:\n"
+        "        kernels = None\n"
+        "print('KERNELS', kernels)\n" % str(lib))
+    res = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120,
+                         env={"HIP_VISIBLE_DEVICES": "", "PATH": "/usr/bin:/bin"})
+    assert res.returncode == 0, res.stderr
+    assert "KERNELS None" in res.stdout
+
+
 def test_void_entry_point_fails_loudly_without_gpu():
     """bfp8_gemv has no error channel (04/qwen_kernels_opt.c:207): without a GPU
     the library aborts with a message instead of computing on the CPU."""

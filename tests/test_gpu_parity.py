@@ -87,6 +87,15 @@ def run_gemv_dev(qk, torch, mant, exps, x, lanes=True):
 
 
 # ---- quantizer -------------------------------------------------------------------------------
+
+def test_gpu_ready_on_the_gpu_box(gpu):
+    """init_kernels() then bfp8_gpu_ready(): 1 on a gfx950 device with this
+    library's code object loaded (the check an engine makes to keep the GPU
+    path)."""
+    lib = gpu.load()
+    lib.init_kernels()
+    assert lib.bfp8_gpu_ready() == 1, lib.bfp8_last_error()
+
 def test_quantize_bit_exact_with_special_values(gpu, torch_mod):
     qk, torch = gpu, torch_mod
     rng = np.random.default_rng(11)
