@@ -184,11 +184,15 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="sweep",
                     choices=["sweep", "layers", "lm_head", "lm_head_plain", "gemv", "down", "batch16", "lm_head_bf16",
+                             "host_gemv",
                              "forward_token"])
     ap.add_argument("--rotate-gb", type=float, default=1.0, help="rotating weight copies totalling >= this")
     ap.add_argument("--bf16-layout", choices=["tiles", "rows"], default="tiles",
                     help="lm_head_bf16: the library's cached tile layout or a row-major device table")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--callback", choices=["none", "gemv4"], default="none",
+                    help="forward_token: the full-attention layers' host callback -- none, or the engine's "
+                         "rmsnorm + q/k/v/o bfp8_gemv calls through the host ABI (attention itself stubbed)")
     ap.add_argument("--batch-shape", choices=["all", "3584x1024", "65536x1024"], default="all",
                     help="batch16: the matrix shapes to run")
     args = ap.parse_args()
@@ -213,6 +217,8 @@ def main():
         return bench_lm_head_bf16(args, qk, torch, np)
     if args.workload == "forward_token":
         return bench_forward_token(args, qk, torch, np)
+    if args.workload == "host_gemv":
+        return bench_host_gemv(args, qk, torch, np)
 
     items = workload_items(args.workload)
     per_copy = sum(wbytes(M, K) for _, M, K, *_ in items)
@@ -619,6 +625,95 @@ class _SynthModel:
                   self.is_full.ctypes.data, self.final_w.ctypes.data, self.embed.ctypes.data, cb, None)
 
 
+# The full-attention callback's GEMVs (04/qwen_real_engine.py:1059-1087): q with
+# its gate (16 heads x 256, interleaved), k and v (2 kv heads x 256), o.
+CALLBACK_GEMVS = (("q", 4096, 1024), ("k", 512, 1024), ("v", 512, 1024), ("o", 1024, 2048))
+
+
+class _ReadOnlyPlanes:
+    """BFP8 planes (mantissas [M][K], exponents [M][K/64]) in a private mapping
+    made read-only afterwards, as the engine's PROT_READ mmap of its weight
+    image (04/qwen_real_engine.py:745-751): the library converts such weights
+    once and keeps the device copy."""
+
+    def __init__(self, lib, np, M, K, seed):
+        self.M, self.K = M, K
+        nm, ne = M * K, M * (K // 64)
+        self.map = mmap.mmap(-1, nm + ne)
+        buf = np.frombuffer(self.map, dtype=np.uint8)
+        self.mant, self.exps = buf[:nm].view(np.int8), buf[nm:]
+        lib.bfp8_synth_planes_host(self.mant.ctypes.data, self.exps.ctypes.data, M, K, seed, 122, 126)
+        libc = ctypes.CDLL(None)
+        libc.mprotect.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+        page = mmap.PAGESIZE
+        base = buf.ctypes.data & ~(page - 1)
+        if libc.mprotect(base, (buf.ctypes.data + nm + ne - base + page - 1) // page * page, mmap.PROT_READ) != 0:
+            raise OSError("mprotect of the weight planes failed")
+
+
+def bench_host_gemv(args, qk, torch, np):
+    """The engine's own bfp8_gemv calls through the host ABI (host pointers,
+    synchronous: x copied in, y copied back), at the full-attention
+    callback's shapes, weights in read-only pages (converted once, cached on
+    the device).  Per-call latency, median and mean over --steps calls each,
+    and the callback's four GEMVs per full-attention layer and per token (6
+    such layers)."""
+    lib = qk.load()
+    mats = {n: _ReadOnlyPlanes(lib, np, M, K, 4100 + i) for i, (n, M, K) in enumerate(CALLBACK_GEMVS)}
+    shapes = []
+    for n, M, K in CALLBACK_GEMVS:
+        w = mats[n]
+        x = qk.synth_normal(K, 4200)
+        y = np.empty(M, dtype=np.float32)
+        for _ in range(max(3, args.warmup)):
+            lib.bfp8_gemv(y.ctypes.data, x.ctypes.data, w.mant.ctypes.data, w.exps.ctypes.data, M, K)
+        ts = []
+        for _ in range(max(20, args.steps)):
+            t0 = time.perf_counter()
+            lib.bfp8_gemv(y.ctypes.data, x.ctypes.data, w.mant.ctypes.data, w.exps.ctypes.data, M, K)
+            ts.append(time.perf_counter() - t0)
+        ts.sort()
+        shapes.append({"gemv": n, "M": M, "K": K, "us_median": round(ts[len(ts) // 2] * 1e6, 2),
+                       "us_mean": round(sum(ts) / len(ts) * 1e6, 2), "us_min": round(ts[0] * 1e6, 2)})
+    per_layer = sum(sh["us_median"] for sh in shapes)
+    wb = sum(wbytes(M, K) for _, M, K in CALLBACK_GEMVS)
+    print(json.dumps({"metric": "host-ABI bfp8_gemv latency per call (engine callback shapes)",
+                      "value": round(per_layer, 2), "unit": "us per full-attention layer (4 GEMVs)",
+                      "n_gpus": 1, "steps": max(20, args.steps), "warmup": max(3, args.warmup),
+                      "higher_is_better": False, "dtype": "int8xint16->int32, f32 epilogue", "data": "synthetic",
+                      "config": {"workload": "host_gemv", "weights": "read-only mapping (device copy cached)",
+                                 "weight_bytes_per_layer": wb},
+                      "us_per_token_6_layers": round(6 * per_layer, 1), "shapes": shapes}), flush=True)
+
+
+def _callback_gemv4(qk, np, lib):
+    """The full-attention callback of 04/qwen_real_engine.py:1059-1087 through
+    this library's host ABI: rmsnorm of h, q/k/v GEMVs, the attention step
+    (libqwen_attn.so's, not part of this library: stubbed as the first 2048
+    q outputs), o GEMV, h += o.  Returns (callback, keepalive)."""
+    mats = {n: _ReadOnlyPlanes(lib, np, M, K, 4300 + i) for i, (n, M, K) in enumerate(CALLBACK_GEMVS)}
+    ln = (np.random.default_rng(5).standard_normal(1024) * 0.1).astype(np.float32)
+    normed = np.empty(1024, dtype=np.float32)
+    ys = {n: np.empty(M, dtype=np.float32) for n, M, _ in CALLBACK_GEMVS}
+    gated = np.empty(2048, dtype=np.float32)
+
+    def gemv(n, y, x):
+        w = mats[n]
+        lib.bfp8_gemv(y.ctypes.data, x.ctypes.data, w.mant.ctypes.data, w.exps.ctypes.data, w.M, w.K)
+
+    def cb(layer, h_ptr, ctx):
+        h = np.ctypeslib.as_array(ctypes.cast(h_ptr, ctypes.POINTER(ctypes.c_float)), shape=(1024,))
+        lib.rmsnorm(normed.ctypes.data, h_ptr, ln.ctypes.data, 1024, 1e-6)
+        gemv("q", ys["q"], normed)
+        gemv("k", ys["k"], normed)
+        gemv("v", ys["v"], normed)
+        gated[:] = ys["q"][:2048] * np.float32(1e-3)
+        gemv("o", ys["o"], gated)
+        np.add(h, ys["o"], out=h)
+
+    return qk.FULL_ATTN_CALLBACK(cb), (mats, ln, normed, ys, gated, cb)
+
+
 def bench_forward_token(args, qk, torch, np):
     """forward_token_c (04/qwen_kernels_opt.c:1008-1049) called exactly as the
     engine calls it (host pointers, synchronous): 18 linear-attention layers +
@@ -633,15 +728,19 @@ def bench_forward_token(args, qk, torch, np):
     print(f"[bench] forward_token: {m.weight_bytes / 1e6:.1f} MB BFP8 + {m.embed.nbytes / 1e6:.1f} MB bf16 table "
           f"+ {m.param_bytes / 1e6:.1f} MB params, {m.state_bytes / 1e6:.1f} MB states", flush=True)
 
+    if args.callback == "gemv4":
+        cb, cb_keep = _callback_gemv4(qk, np, lib)
+    else:
+        cb = qk.FULL_ATTN_CALLBACK()  # NULL: no full-attention callback
+
     def timed(resident, steps, warmup):
         lib.qwen_forward_state_resident(resident)
-        no_cb = qk.FULL_ATTN_CALLBACK()  # NULL: no full-attention callback
         for i in range(warmup):
-            m.run(lib.forward_token_c, 1000 + i, no_cb)
+            m.run(lib.forward_token_c, 1000 + i, cb)
         ts = []
         for i in range(steps):
             t0 = time.perf_counter()
-            m.run(lib.forward_token_c, 2000 + i, no_cb)
+            m.run(lib.forward_token_c, 2000 + i, cb)
             ts.append(time.perf_counter() - t0)
         lib.qwen_forward_state_resident(0)
         ts.sort()
@@ -675,7 +774,9 @@ def bench_forward_token(args, qk, torch, np):
         "us_per_token_state_copies": round(med_sync, 1), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32 (BFP8 int8 x int16 GEMV)", "data": "synthetic",
         "config": {"workload": "forward_token", "layers": N_LAYERS, "linear_attention_layers": 18,
-                   "hidden": 1024, "vocab": 65536, "state": "device-resident"},
+                   "hidden": 1024, "vocab": 65536, "state": "device-resident",
+                   "full_attention_callback": ("rmsnorm + q/k/v/o bfp8_gemv through the host ABI per full layer "
+                                               "(attention step stubbed)") if args.callback == "gemv4" else None},
         "roofline": {"bound": "hbm", "achieved": round(tb / med_res / 1e3, 1), "peak": PEAK_HBM_GBPS,
                      "unit": "GB/s", "frac": round(tb / med_res / 1e3 / PEAK_HBM_GBPS, 4), "traffic": None,
                      "scope": f"whole token: {tb / 1e6:.1f} MB algorithmic per token / wall time per token"},

@@ -466,9 +466,12 @@ int host_gemv(float* y, const float* x, const int8_t* mant, const uint8_t* exps,
     DevWeights w;
     if ((rc = weights_for(mant, exps, M, K, &w))) return rc;
     if ((rc = upload_x(x, (size_t)(K <= 4096 ? nb * 64 : K)))) return rc;
-    if ((rc = g.y.reserve((size_t)M * 4)) || (rc = g.h_out.reserve((size_t)M * 4))) return rc;
-    if ((rc = gemv_from_x(g.y.as<float>(), w, M, K))) return rc;
-    HIP_OK(hipMemcpyAsync(g.h_out.p, g.y.p, (size_t)M * 4, hipMemcpyDeviceToHost, g.stream));
+    if ((rc = g.h_out.reserve((size_t)M * 4))) return rc;
+    // the GEMV stores y straight into the pinned host buffer (no device
+    // buffer and copy back: 19.5-20.1 against 21.2-22.3 us per call at the
+    // engine callback's shapes); the stream synchronization makes the
+    // stores visible to the host
+    if ((rc = gemv_from_x(static_cast<float*>(g.h_out.p), w, M, K))) return rc;
     HIP_OK(hipStreamSynchronize(g.stream));
     memcpy(y, g.h_out.p, (size_t)M * 4);
     return BFP8_OK;
