@@ -95,5 +95,48 @@ def build(verbose: bool = False) -> Path:
     return OUT
 
 
+# Host code under AddressSanitizer + UndefinedBehaviorSanitizer, for the CPU
+# tests only (tests/test_sanitizers.py): the sanitizers apply to the host side
+# of every unit (-Xarch_host); the device code is built as usual.  The
+# sanitizer runtime is not linked in: the test preloads clang's into the
+# Python process.
+SAN_BUILD = PKG / "_build_san"
+SAN_OUT = PKG / "_san" / "libqwen_kernels.so"
+SAN_FLAGS = ["-O1", "-g", "-fPIC", "-std=c++17", "-ffp-contract=off", f"-I{CSRC}", f"-I{ROOT / 'include'}",
+             "-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+             "-Xarch_host", "-fno-sanitize-recover=undefined", "-Xarch_host", "-fno-omit-frame-pointer"]
+
+
+def build_sanitized(verbose: bool = False) -> Path:
+    SAN_BUILD.mkdir(exist_ok=True)
+    SAN_OUT.parent.mkdir(exist_ok=True)
+
+    def comp(src: str) -> Path:
+        obj = SAN_BUILD / (Path(src).stem + ".o")
+        dev = ["--offload-arch=" + ARCH, "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+               *UNITS[src]] if src.endswith(".hip") else []
+        res = subprocess.run([HIPCC, *dev, *SAN_FLAGS, "-c", str(CSRC / src), "-o", str(obj)], capture_output=True,
+                             text=True)
+        if res.returncode != 0:
+            sys.stderr.write(res.stdout + res.stderr)
+            raise RuntimeError(f"sanitized hipcc failed on {src}")
+        return obj
+
+    with ThreadPoolExecutor(max_workers=len(UNITS)) as ex:
+        objs = list(ex.map(comp, UNITS))
+    tmp = SAN_OUT.with_suffix(".so.tmp")
+    res = subprocess.run([HIPCC, "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)], capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise RuntimeError("sanitized link failed")
+    os.replace(tmp, SAN_OUT)
+    if verbose:
+        print(f"built {SAN_OUT}")
+    return SAN_OUT
+
+
 if __name__ == "__main__":
-    build(verbose=True)
+    if "--sanitize" in sys.argv[1:]:
+        build_sanitized(verbose=True)
+    else:
+        build(verbose=True)

@@ -6,13 +6,15 @@ Test infrastructure only.
 from __future__ import annotations
 
 import ctypes
+import os
 from ctypes import c_float, c_int, c_void_p
 from pathlib import Path
 
 import numpy as np
 
 ROOT = Path(__file__).resolve().parent.parent
-ORACLE = ROOT / "oracle" / "liboracle.so"
+# ORACLE_LIB_UNDER_TEST: another build of the same sources (the sanitizer run)
+ORACLE = Path(os.environ.get("ORACLE_LIB_UNDER_TEST") or ROOT / "oracle" / "liboracle.so")
 REF_KERNELS = ROOT / "oracle" / "_ref" / "libref_qwen_kernels.so"
 REF_SAMPLING = ROOT / "oracle" / "_ref" / "libref_qwen_sampling.so"
 

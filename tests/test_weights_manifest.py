@@ -14,8 +14,12 @@ MANIFEST = ROOT / "tests" / "golden" / "manifest_64k.json"
 
 @pytest.fixture(scope="module")
 def lib():
+    """The library; QWEN_KERNELS_LIB_UNDER_TEST names another build of it (the
+    sanitizer run, tests/test_sanitizers.py)."""
+    import os
+
     import qwen_kernels_gpu as qk
-    return qk.load()
+    return qk.load(os.environ.get("QWEN_KERNELS_LIB_UNDER_TEST") or None)
 
 
 def scan(lib, path, image_bytes):
