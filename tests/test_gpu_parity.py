@@ -439,17 +439,31 @@ def test_small_plan_one_tile_per_workgroup(gpu, torch_mod):
     plan.close()
 
 
-@pytest.mark.parametrize("case", ["one", "one_ragged_odd", "pair_shared_x", "pair_ragged_odd"])
+ROWS_CASES = {
+    "one": [(3584, 1024)],                              # 16-row sub-tiles
+    "one_ragged_odd": [(1023, 1000)],                   # 4-row sub-tiles, XCD-paired grid of 256
+    "one_8_rows": [(1500, 2048)],                       # 8-row sub-tiles (375 four-row groups > 256)
+    "one_4_rows_down": [(1024, 3584)],                  # the down projection's shape
+    "one_4_rows_unpaired": [(999, 3584)],               # 250 workgroups: no XCD pairing
+    "pair_shared_x": [(3584, 1024), (3584, 1024)],      # two 16-row sub-tiles per workgroup
+    "pair_ragged_odd": [(4001, 1000), (4001, 1000)],
+    "pair_4_rows": [(512, 1024), (512, 1024)],          # the k / v projections' shape
+    "pair_4_rows_odd_split": [(499, 1088), (523, 1088)],  # 125 + 131 groups, paired grid
+}
+
+
+@pytest.mark.parametrize("case", list(ROWS_CASES))
 def test_plan_rows_kernel_paths(gpu, torch_mod, case):
     """Plans of one GEMV, or of two reading the same activation, run on the
     16-row kernel, which quantizes the activation itself: odd M adds the
     tail-row kernel (reading the records the launch left), a ragged K uses its
-    K / 64 whole blocks, and more 16-row workgroups than CUs put two sub-tiles
-    in each workgroup (the pairs; the ragged pair ends in a half-used one)."""
+    K / 64 whole blocks, GEMVs with few rows use sub-tiles of 8 or 4 rows (one
+    workgroup per CU at most; 4-row sub-tiles sharing a 128-byte line on one
+    XCD when the grid is a multiple of 16), and more 16-row workgroups than CUs
+    put two sub-tiles in each workgroup (the pairs; the ragged pair ends in a
+    half-used one)."""
     qk, torch = gpu, torch_mod
-    shapes = {"one": [(3584, 1024)], "one_ragged_odd": [(1023, 1000)],
-              "pair_shared_x": [(3584, 1024), (3584, 1024)],
-              "pair_ragged_odd": [(4001, 1000), (4001, 1000)]}[case]
+    shapes = ROWS_CASES[case]
     K = shapes[0][1]
     x = qk.synth_normal(K, 5150)
     xd = torch.from_numpy(x).cuda()
@@ -470,6 +484,56 @@ def test_plan_rows_kernel_paths(gpu, torch_mod, case):
             mant, exps = qk.synth_planes(M, K, seed, 124, 130)
             y_ref = ol.gemv_neon(x, mant, exps)[0]
             assert same_f32(it["y"].cpu().numpy(), y_ref), (rep, M, K, mismatch(it["y"].cpu().numpy(), y_ref))
+    plan.close()
+
+
+def _special_blocks(K, seed, inf=False):
+    """An activation whose first blocks take every branch of the block
+    quantizer (04/qwen_kernels_opt.c:182-205): zeros, negative zeros, a block
+    at and one just above the 1e-20 amax threshold, NaN, exact .5 ties,
+    subnormals, values of 1e33; then blocks of seven decades.
+    With `inf`, block 5 holds an inf (its scale is inf, so y is all inf/NaN)."""
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal(K) * np.float32(10.0) ** rng.integers(-6, 4, size=K)).astype(F32)
+    blk = lambda b: slice(64 * b, 64 * b + 64)
+    x[blk(0)] = 0.0
+    x[blk(1)] = -0.0
+    t = np.float32(1e-20)
+    x[blk(2)] = rng.uniform(-1, 1, 64).astype(F32) * t
+    x[64 * 2] = t                                          # amax == 1e-20: not above, a zero record
+    x[blk(3)] = rng.uniform(-1, 1, 64).astype(F32) * t
+    x[64 * 3] = np.nextafter(t, np.float32(1.0))           # just above: quantized
+    x[64 * 4 + 3] = np.nan
+    x[64 * 4 + 40] = np.nan
+    if inf:
+        x[64 * 5 + 7] = np.inf                             # xscale inf, every other product 0
+    x[blk(6)] = (rng.integers(-64, 64, 64) + 0.5).astype(F32)
+    x[64 * 6] = 16384.0                                    # q = 1: the .5 values are ties
+    x[blk(7)] = (rng.standard_normal(64) * np.float32(1e-39)).astype(F32)
+    x[64 * 7 + 9] = 1e-3
+    x[blk(8)] = (rng.uniform(-1, 1, 64) * np.float32(3e33)).astype(F32)  # huge amax, y still finite
+    return x
+
+
+@pytest.mark.parametrize("M,K,inf", [(1024, 3584, False), (3584, 1024, False), (1500, 2048, False),
+                                     (999, 1000, False), (999, 1000, True)])
+def test_rows_kernel_quantizes_special_blocks(gpu, torch_mod, M, K, inf):
+    """The 16-row kernel's block quantizer (16 lanes per block, four elements
+    per lane) on special blocks, at each sub-tile size, twice in a row."""
+    qk, torch = gpu, torch_mod
+    x = _special_blocks(K, 6100 + M, inf)
+    dm = qk.DeviceMatrix.synth(M, K, 6000 + M, 118, 136)
+    y = torch.empty(M, dtype=torch.float32, device="cuda")
+    plan = qk.SweepPlan([{"mat": dm, "x": torch.from_numpy(x).cuda(), "y": y}])
+    assert plan.kernel_name(1) == "rt_rows_gemv_kernel"
+    mant, exps = qk.synth_planes(M, K, 6000 + M, 118, 136)
+    y_ref = ol.gemv_neon(x, mant, exps)[0]
+    say("rows special blocks", M, K)
+    for rep in range(2):
+        y.fill_(np.nan)
+        plan.run()
+        torch.cuda.synchronize()
+        assert same_f32(y.cpu().numpy(), y_ref), (rep, mismatch(y.cpu().numpy(), y_ref))
     plan.close()
 
 
