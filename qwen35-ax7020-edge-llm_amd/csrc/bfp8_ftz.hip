@@ -401,7 +401,8 @@ struct HeadLds {
 typedef __attribute__((address_space(1))) uint32_t* g_u32_ptr;
 typedef __attribute__((address_space(1))) float* g_f32_ptr;
 typedef __attribute__((address_space(1))) int16_t* g_i16_ptr;
-__device__ __forceinline__ void quantize_task(const Bfp8QuantDesc& d, int b, float xv, int lane, uint32_t* rec) {
+__device__ __forceinline__ void quantize_task(const Bfp8HeadTask& d, float xv, int lane, uint32_t* rec) {
+    const int b = d.b;
     const Bfp8QuantLane r = bfp8_quant_lane(xv);
     if (d.xq) ((g_i16_ptr)d.xq)[(size_t)b * 64 + lane] = (int16_t)r.xq;
     if (lane == 0) ((g_f32_ptr)d.xscale)[b] = r.xs;
@@ -476,7 +477,12 @@ __device__ __forceinline__ void head_reduce(HeadTile& T, const Bfp8HeadArgs& a, 
             fs = epilogue(fs, S, e, __uint_as_float(__builtin_amdgcn_readlane(xsv, b)));
         }
     }
-    const Bfp8GemvDesc& d = a.descs[a.head];
+    // (constant address space: scalar loads, not waited for with the weights)
+    const __attribute__((address_space(4))) Bfp8GemvDesc* dp =
+        (const __attribute__((address_space(4))) Bfp8GemvDesc*)a.descs + a.head;
+    float* const dy = dp->y;
+    uint64_t* const partials = dp->partials;
+    const int pair_rows = dp->pair_rows, topk = dp->topk;
     L.red[q * 64 + lane] = fs;
     __syncthreads();
     // wavefront q, lane (r, qq): row 16q + r of the tile (each quad computes
@@ -485,51 +491,81 @@ __device__ __forceinline__ void head_reduce(HeadTile& T, const Bfp8HeadArgs& a, 
     const float y = (L.red[tr] + L.red[128 + tr]) + (L.red[64 + tr] + L.red[192 + tr]);
     const int row = t * BFP8_TILE_ROWS + tr;
     if ((lane & 3) == 0) {
-        if (d.y && row < d.pair_rows) d.y[row] = y;
-        L.keys[tr] = tile_rank_key(y, row, row < d.pair_rows);
+        if (dy && row < pair_rows) dy[row] = y;
+        L.keys[tr] = tile_rank_key(y, row, row < pair_rows);
     }
-    if (d.topk > 0) {
+    if (topk > 0) {
         __syncthreads();
-        tile_topk_rank(L.keys, d.partials, t, d.topk, q, lane);
+        tile_topk_rank(L.keys, partials, t, topk, q, lane);
     }
     __syncthreads();  // L.red and L.keys are reused by the next tile
 }
 
-// Loads go out in the order they are needed, and nothing but the arguments
-// stands before the weights: a table lookup there would wait behind the
-// weight streams of the workgroups already running.  The quantization task's
-// descriptor (two scalar loads) and element follow the weights, so the task
-// runs last.
+// The lm_head activation, and this wavefront's quantization task (a record
+// and its 64 floats), are loaded and waited for before any weight goes out:
+// a workgroup's loads queue behind the weights already requested on its CU,
+// so a load issued after them returned only when those had drained (2-3 us
+// into the launch), and the tile could not be reduced before.  The record
+// comes in by a vector load (one 8-byte word per lane) and readlanes, not by
+// scalar loads: those count on the counter that the LDS barrier below waits
+// for, and under the weight streams they returned late.  Then the weights,
+// with nothing but the arguments before them.
 extern "C" __global__ __launch_bounds__(256) void bfp8_gemv_head_kernel(Bfp8HeadArgs a) {
-    constexpr int kPerWave = BFP8_HEAD_MAX_NB / kWaves;
     __shared__ HeadLds L;
     const int q = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int nb = a.K >> 6;  // 1 .. BFP8_HEAD_MAX_NB (host-checked)
+    const int wid = (int)blockIdx.x * kWaves + q, nw = (int)gridDim.x * kWaves;
 
-    // 0. the lm_head activation's blocks q, q + 4, ... (one element per lane),
-    // the first tile's weights, then this wavefront's task
-    float hv[kPerWave];
+    // 0. the lm_head activation: block 4q + lane / 16, elements 4 (lane % 16)
+    // + j (blocks past nb read block nb - 1 and are never stored); this
+    // wavefront's task record, one 8-byte word per lane 0..5; then its element
+    static_assert(BFP8_HEAD_MAX_NB == 4 * kWaves, "one block per row of 16 lanes");
+    static_assert(sizeof(Bfp8HeadTask) == 48, "six 8-byte words");
+    const int hb = 4 * q + (lane >> 4), hi = lane & 15;
+    float hv[4];
 #pragma unroll
-    for (int k = 0; k < kPerWave; ++k) hv[k] = a.hx[min(q + kWaves * k, nb - 1) * 64 + lane];
+    for (int j = 0; j < 4; ++j) hv[j] = a.hx[min(hb, nb - 1) * 64 + 4 * hi + j];
+    const int ti = min(wid, max(a.ntasks - 1, 0));
+    typedef const __attribute__((address_space(1))) uint64_t* g_u64_ptr;
+    const uint64_t tw = ((g_u64_ptr)(a.qtasks + ti))[min(lane, 5)];
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the activation and the record are in
+    __builtin_amdgcn_sched_barrier(0);
+    Bfp8HeadTask task;
+    {
+        const uint32_t lo[6] = {(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)tw, 0),
+                                (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)tw, 1),
+                                (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)tw, 2),
+                                (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)tw, 3),
+                                (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)tw, 4),
+                                (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)tw, 5)};
+        const uint32_t hw[6] = {(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(tw >> 32), 0),
+                                (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(tw >> 32), 1),
+                                (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(tw >> 32), 2),
+                                (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(tw >> 32), 3),
+                                (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(tw >> 32), 4),
+                                (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(tw >> 32), 5)};
+        uint64_t wd[6];
+#pragma unroll
+        for (int k = 0; k < 6; ++k) wd[k] = ((uint64_t)hw[k] << 32) | lo[k];
+        __builtin_memcpy(&task, wd, sizeof(task));
+    }
+    // (a global-address-space pointer: a flat load would count on both counters)
+    const float tv = ((const __attribute__((address_space(1))) float*)task.x)[lane];
     HeadTile T;
     int t = blockIdx.x;
     head_issue(T, a, t, nb, q, lane);
-    __builtin_amdgcn_sched_barrier(0);  // the task's dependent loads stay behind every weight load
-    const int wid = (int)blockIdx.x * kWaves + q, nw = (int)gridDim.x * kWaves;
-    typedef const __attribute__((address_space(4))) int* s_int_ptr;  // scalar loads
-    const int ti = min(wid, max(a.ntasks - 1, 0));
-    const int tq = ((s_int_ptr)a.qtasks)[2 * ti], tb = ((s_int_ptr)a.qtasks)[2 * ti + 1];
-    // (a global-address-space pointer: a flat load would count on both counters)
-    const float tv = ((const __attribute__((address_space(1))) float*)a.qdescs[tq].x)[(size_t)tb * 64 + lane];
+    __builtin_amdgcn_sched_barrier(0);
 
-    // 1. the lm_head activation, quantized into LDS (slots b >= nb hold a
-    // copy of block nb - 1 and are never read)
-#pragma unroll
-    for (int k = 0; k < kPerWave; ++k) {
-        const int b = q + kWaves * k;
-        bfp8_quant_block_lds(hv[k], lane, &L.xsc[b], &L.xs[b * 32]);
-    }
+    // 1. the lm_head activation, quantized into LDS while the weights are in
+    // flight: one block per row of 16 lanes, four blocks per wavefront
+    // (hb passed through an opaque move: left visible, the compiler derived the
+    // scale's address from the record's with a 64-bit multiply-add whose
+    // unused high half sat in a register a weight load targets, which made the
+    // quantization wait for the weights)
+    int hbs;
+    asm("v_mov_b32 %0, %1" : "=v"(hbs) : "v"(hb));
+    bfp8_quant4_store_lds(hv, hi, &L.xsc[hbs], &L.xs[hb * 32], hb < nb);
     __syncthreads();
 
     // 2. residue q's split words in registers: lane l holds word l & 7 of
@@ -547,11 +583,10 @@ extern "C" __global__ __launch_bounds__(256) void bfp8_gemv_head_kernel(Bfp8Head
     }
     // 4. the quantization tasks: this wavefront's, then those beyond one per
     // wavefront (more tasks than wavefronts)
-    if (wid < a.ntasks) quantize_task(a.qdescs[tq], tb, tv, lane, L.rec[q]);
+    if (wid < a.ntasks) quantize_task(task, tv, lane, L.rec[q]);
     for (int j = wid + nw; j < a.ntasks; j += nw) {
-        const int jq = ((s_int_ptr)a.qtasks)[2 * j], jb = ((s_int_ptr)a.qtasks)[2 * j + 1];
-        const Bfp8QuantDesc& dj = a.qdescs[jq];
-        quantize_task(dj, jb, dj.x[(size_t)jb * 64 + lane], lane, L.rec[q]);
+        const Bfp8HeadTask tj = a.qtasks[j];
+        quantize_task(tj, tj.x[lane], lane, L.rec[q]);
     }
 }
 

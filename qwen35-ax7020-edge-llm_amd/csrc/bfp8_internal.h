@@ -112,6 +112,17 @@ hipError_t bfp8_launch_gemv_grouped(const Bfp8GemvDesc* descs_dev, const Bfp8Til
 #define BFP8_HEAD_MAX_NB 16
 // The fused lm_head launch: everything its weight loads need is an argument
 // (no table lookups ahead of them); workgroup w takes tiles w, w + nwg, ...
+// One 64-element block of another activation, quantized by one wavefront of
+// the lm_head launch: everything the wavefront needs in one record, so that
+// it is read with the lm_head activation, before any weight load.
+struct Bfp8HeadTask {
+    const float* x;    // the block's 64 floats
+    int16_t* xq;       // the activation's outputs (bfp8_quantize's), block b of each
+    float* xscale;
+    uint32_t* xsplit;
+    int b;
+    int pad_[3];
+};
 struct Bfp8HeadArgs {
     const Bfp8GemvDesc* descs;    // descs[head]: the outputs (y, partials, topk, pair_rows)
     int head;
@@ -119,8 +130,7 @@ struct Bfp8HeadArgs {
     const uint8_t* exps;
     int K, ntiles;
     const float* hx;              // the lm_head's activation
-    const Bfp8QuantDesc* qdescs;  // the other activations, one 64-element block per task
-    const int* qtasks;            // (qdesc, block) pairs; at least one entry even when ntasks == 0
+    const Bfp8HeadTask* qtasks;   // the other activations' blocks; at least one entry even when ntasks == 0
     int ntasks;
 };
 hipError_t bfp8_launch_gemv_head(const Bfp8HeadArgs& a, int nwg, hipStream_t s);

@@ -103,8 +103,11 @@ __device__ __forceinline__ void bfp8_quant4_store_lds(const float (&x)[4], int i
     const float amax = row_max_nonneg(v);
     const bool live = amax > 1e-20f;
     const float q = __fdiv_rn(16384.0f, live ? amax : 1.0f);
-    uint8_t* rb = reinterpret_cast<uint8_t*>(xsplit_b);
-    if (store && ii == 0) *xscale_b = live ? amax * 0x1p-14f : 0.0f;  // = amax / 16384 exactly (normal)
+    // LDS pointers (32-bit offsets), not generic ones
+    typedef __attribute__((address_space(3))) uint8_t lds_u8;
+    typedef __attribute__((address_space(3))) float lds_f32;
+    lds_u8* rb = (lds_u8*)xsplit_b;
+    if (store && ii == 0) *(lds_f32*)xscale_b = live ? amax * 0x1p-14f : 0.0f;  // = amax / 16384 exactly (normal)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const float p = __fmul_rn(x[j], q);

@@ -1084,7 +1084,7 @@ struct Plan {
     std::vector<int> odd_items;    // items needing the odd-row kernel
     std::vector<int> float_items;  // K > 4096 items (float path, own launches)
     DevBuf descs, qdescs, xscale, xsplit, partials;
-    DevBuf qtasks;                 // fused head: (quantize descriptor, block) pairs
+    DevBuf qtasks;                 // fused head: Bfp8HeadTask per block of the other activations
     Launch head, rest;             // lm_head tiles, then every other GEMV's
     int nq = 0, max_nb = 0, ntasks = 0;
     bool fused_head = false;       // the lm_head launch quantizes every activation
@@ -1418,23 +1418,26 @@ void* bfp8_plan_create(const bfp8_plan_item* items, int n) {
     if (p->topk_desc >= 0 && !rc) {
         const bfp8_plan_item& ht = items[p->topk_desc];
         if ((ht.K & 63) == 0 && (ht.K >> 6) <= BFP8_HEAD_MAX_NB && p->head.nwg > 0) {
-            std::vector<int> tasks;
+            std::vector<Bfp8HeadTask> tasks;
+            auto task = [&](int qi, int b) {
+                Bfp8HeadTask t{};
+                t.x = hq[qi].x + (size_t)b * 64;
+                t.xq = hq[qi].xq;
+                t.xscale = hq[qi].xscale;
+                t.xsplit = hq[qi].xsplit;
+                t.b = b;
+                return t;
+            };
             for (int qi = 0; qi < (int)hq.size(); ++qi) {
                 if (qi == hq_of_item[p->topk_desc]) continue;  // quantized by every workgroup
-                for (int b = 0; b < bfp8_nblocks(hq[qi].K); ++b) {
-                    tasks.push_back(qi);
-                    tasks.push_back(b);
-                }
+                for (int b = 0; b < bfp8_nblocks(hq[qi].K); ++b) tasks.push_back(task(qi, b));
             }
-            p->ntasks = (int)tasks.size() / 2;
-            if (tasks.empty()) {  // the kernel always reads one entry
-                tasks.push_back(hq_of_item[p->topk_desc]);
-                tasks.push_back(0);
-            }
+            p->ntasks = (int)tasks.size();
+            if (tasks.empty()) tasks.push_back(task(hq_of_item[p->topk_desc], 0));  // the kernel always reads one entry
             {
-                rc = p->qtasks.reserve(tasks.size() * sizeof(int));
-                if (!rc && hipMemcpy(p->qtasks.p, tasks.data(), tasks.size() * sizeof(int), hipMemcpyHostToDevice) !=
-                               hipSuccess)
+                rc = p->qtasks.reserve(tasks.size() * sizeof(Bfp8HeadTask));
+                if (!rc && hipMemcpy(p->qtasks.p, tasks.data(), tasks.size() * sizeof(Bfp8HeadTask),
+                                     hipMemcpyHostToDevice) != hipSuccess)
                     rc = BFP8_EHIP;
             }
             p->fused_head = !rc;
@@ -1517,8 +1520,7 @@ int bfp8_plan_launch(void* plan, int stage, void* stream) {
             a.K = hd.K;
             a.ntiles = p->head.ntiles;
             a.hx = p->items[p->topk_desc].x;
-            a.qdescs = p->qdescs.as<Bfp8QuantDesc>();
-            a.qtasks = p->qtasks.as<int>();
+            a.qtasks = p->qtasks.as<Bfp8HeadTask>();
             a.ntasks = p->ntasks;
             HIP_OK(bfp8_launch_gemv_head(a, p->head.nwg, s));
         } else
