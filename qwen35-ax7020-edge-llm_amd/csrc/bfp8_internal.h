@@ -136,7 +136,9 @@ struct Bfp8HeadArgs {
 hipError_t bfp8_launch_gemv_head(const Bfp8HeadArgs& a, int nwg, hipStream_t s);
 // Extra load, in blocks of the byte-balanced dealing, that a folded merge
 // puts on workgroup 0 of a grouped launch.
-#define BFP8_MERGE_COST_BLOCKS 16
+// (the merge of the 24-layer sweep's 1024 lm_head lists took 20-23 us in
+// workgroup 0, about 32 blocks at a workgroup's streaming rate)
+#define BFP8_MERGE_COST_BLOCKS 32
 // Number of workgroups the persistent GEMV kernels keep resident.
 int bfp8_stream_grid();
 // hipSuccess when this library's gfx950 code object loads on the current
