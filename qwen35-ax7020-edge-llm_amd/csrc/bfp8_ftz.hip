@@ -509,7 +509,8 @@ __device__ __forceinline__ void head_reduce(HeadTile& T, const Bfp8HeadArgs& a, 
 // comes in by a vector load (one 8-byte word per lane) and readlanes, not by
 // scalar loads: those count on the counter that the LDS barrier below waits
 // for, and under the weight streams they returned late.  Then the weights,
-// with nothing but the arguments before them.
+// with nothing but the arguments before them, and the task is quantized with
+// the activation while they stream.
 extern "C" __global__ __launch_bounds__(256) void bfp8_gemv_head_kernel(Bfp8HeadArgs a) {
     __shared__ HeadLds L;
     const int q = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
@@ -566,6 +567,9 @@ extern "C" __global__ __launch_bounds__(256) void bfp8_gemv_head_kernel(Bfp8Head
     int hbs;
     asm("v_mov_b32 %0, %1" : "=v"(hbs) : "v"(hb));
     bfp8_quant4_store_lds(hv, hi, &L.xsc[hbs], &L.xs[hb * 32], hb < nb);
+    // this wavefront's quantization task now too (its element came in with the
+    // activation), so that its stores go out while the weights stream
+    if (wid < a.ntasks) quantize_task(task, tv, lane, L.rec[q]);
     __syncthreads();
 
     // 2. residue q's split words in registers: lane l holds word l & 7 of
@@ -581,9 +585,8 @@ extern "C" __global__ __launch_bounds__(256) void bfp8_gemv_head_kernel(Bfp8Head
         head_issue(T, a, t, nb, q, lane);
         head_reduce(T, a, t, nb, q, lane, xr0, xr1, xsv, L);
     }
-    // 4. the quantization tasks: this wavefront's, then those beyond one per
-    // wavefront (more tasks than wavefronts)
-    if (wid < a.ntasks) quantize_task(task, tv, lane, L.rec[q]);
+    // 4. the quantization tasks beyond one per wavefront (more tasks than
+    // wavefronts)
     for (int j = wid + nw; j < a.ntasks; j += nw) {
         const Bfp8HeadTask tj = a.qtasks[j];
         quantize_task(tj, tj.x[lane], lane, L.rec[q]);
