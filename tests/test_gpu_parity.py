@@ -579,6 +579,39 @@ def test_plan_lm_head_merge_paths(gpu, torch_mod, shape, plan_mode):
     plan.close()
 
 
+@pytest.mark.parametrize("with_other", [False, True])
+def test_plan_lm_head_quantizes_special_blocks(gpu, torch_mod, with_other, plan_mode):
+    """The lm_head launch quantizes its activation itself (16 lanes per block,
+    four elements per lane) and, with another GEMV in the plan, that GEMV's
+    activation as one-block tasks: special blocks in both (zeros, -0, the
+    1e-20 threshold, NaN, .5 ties, subnormals, 1e33), top-k, argmax and y
+    against the oracle."""
+    qk, torch = gpu, torch_mod
+    V, H, k = 16384, 1024, 40
+    say("plan lm_head special blocks", with_other, plan_mode)
+    xl = _special_blocks(H, 6301)
+    items = [{"mat": qk.DeviceMatrix.synth(V, H, 6300, 118, 136), "x": torch.from_numpy(xl).cuda(), "topk": k}]
+    if with_other:
+        xo = _special_blocks(2048, 6303)
+        items.append({"mat": qk.DeviceMatrix.synth(1000, 2048, 6302, 118, 136), "x": torch.from_numpy(xo).cuda(),
+                      "y": torch.empty(1000, dtype=torch.float32, device="cuda")})
+    plan = qk.SweepPlan(items)
+    mant, exps = qk.synth_planes(V, H, 6300, 118, 136)
+    y_ref, *_ = ol.gemv_neon(xl, mant, exps)
+    ids_ref, sc_ref = ol.topk(y_ref, k)
+    for rep in range(2):
+        plan.run()
+        torch.cuda.synchronize()
+        ids, sc, cnt = plan.topk_out
+        assert int(cnt[0].item()) == k and int(cnt[1].item()) == ol.argmax(y_ref), rep
+        assert np.array_equal(ids.cpu().numpy(), ids_ref) and same_f32(sc.cpu().numpy(), sc_ref), rep
+        if with_other:
+            om, oe = qk.synth_planes(1000, 2048, 6302, 118, 136)
+            y_o = items[1]["y"].cpu().numpy()
+            assert same_f32(y_o, ol.gemv_neon(xo, om, oe)[0]), (rep, mismatch(y_o, ol.gemv_neon(xo, om, oe)[0]))
+    plan.close()
+
+
 # ---- batch and sweep ---------------------------------------------------------------------------------
 def _random_cases(seed, n, kmax, k_whole):
     rng = np.random.default_rng(seed)
