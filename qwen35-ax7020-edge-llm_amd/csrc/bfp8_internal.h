@@ -175,6 +175,7 @@ struct Bfp8SweepArgs {
     uint32_t epoch;            // 1 .. 2^14 - 1, different from the previous launch's
 };
 #define BFP8_SWEEP_LDS_WORDS 8192  // activation slots per workgroup (32 KiB)
+#define BFP8_SWEEP_MAX_SLOTS 8     // activations per workgroup
 // Extra load, in blocks, that the in-launch top-k merge puts on the merging
 // workgroup of a single launch.
 #define BFP8_SWEEP_MERGE_COST_BLOCKS 64

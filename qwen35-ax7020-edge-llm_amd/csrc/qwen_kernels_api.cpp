@@ -1104,10 +1104,7 @@ struct Plan {
 };
 
 // The single launch is opt-in (BFP8_PLAN_SINGLE_LAUNCH=1 when the plan is
-// created): on the 24-layer sweep it measured 90 us against 83 us for the two
-// launches, the per-workgroup quantization of its activations (14 times the
-// blocks the two-launch path quantizes, and a memory round trip for x at every
-// activation switch) costing more than the launch boundary it removes.
+// created).
 bool single_launch_enabled() {
     const char* e = getenv("BFP8_PLAN_SINGLE_LAUNCH");
     return e && e[0] == '1';
@@ -1192,7 +1189,7 @@ bool deal_sweep(Plan* p, const bfp8_plan_item* items, int n) {
         std::vector<std::vector<char>> seen(n);
         for (int i = 0; i < n; ++i) seen[i].assign(bfp8_ntiles(items[i].M), 0);
         for (int w = 0; w < nwg; ++w) {
-            if (lds[w] > BFP8_SWEEP_LDS_WORDS) return false;
+            if (lds[w] > BFP8_SWEEP_LDS_WORDS || slots[w].size() > BFP8_SWEEP_MAX_SLOTS) return false;
             if (w < hnt && (slots[w].empty() || slot_item[w][0] != head || slots[w][0].xoff != 0)) return false;
             for (size_t k = 0; k < slots[w].size(); ++k)
                 if ((slots[w][k].xoff & 3) || slots[w][k].xoff + bfp8_sweep_slot_words(slots[w][k].K) > lds[w])

@@ -12,13 +12,13 @@
 // keeping the next 4-block chunk in flight across tile boundaries.
 //
 // What makes one launch possible:
-//   * Activations are quantized by the workgroup that reads them, into LDS.
-//     Workgroup w's work list is its lm_head tiles (w, w + grid, ...: no
-//     table lookup stands before their weights) then a host-built list of
-//     layer tiles, dealt GEMV by GEMV so that a workgroup reads few
-//     activations.  The first tile's activation is quantized while the first
-//     weights are in flight; every other slot at the end of the tile before
-//     its first use, while the next chunk is in flight.
+//   * Activations are quantized by the workgroup that reads them, into LDS,
+//     all of them before the stream starts: their x loads go out before the
+//     first weights (loads return in order per wavefront), the first weights
+//     are in flight while they are quantized, 16 lanes per block.  Workgroup
+//     w's work list is its lm_head tiles (w, w + grid, ...) then a host-built
+//     list of layer tiles, dealt GEMV by GEMV so that a workgroup reads few
+//     activations.
 //   * The lm_head's tiles publish their top-k lists as epoch-tagged keys
 //     (topk_merge.h: one agent-scope atomic store per key) and one workgroup,
 //     after its own tiles, merges them, re-reading any key of an older epoch
@@ -71,44 +71,80 @@ struct Tile {  // wave-uniform
     int nb, desc, tile, xoff, slot;
 };
 
-// The workgroup's activation slots and their background quantization.
-struct Slots {
-    cptr<Bfp8SweepAct> act;   // this workgroup's slots (slot 0 first)
-    int n;                    // number of slots
-    int tasks;                // total blocks to quantize
-    int next;                 // first block not yet started
+// The workgroup's activations, all quantized into their LDS slots before the
+// stream starts.  Block g of the workgroup (the slots' blocks in order) goes
+// to a row of 16 lanes in passes of 16 blocks: in pass u, row k of wavefront q
+// takes block 16u + 4q + k, each lane four consecutive elements.  Every x load of a group of passes is issued
+// before the first weights and waited for before the weights are: loads
+// return in order per wavefront, and x loads issued behind weight loads came
+// back microseconds later.
+constexpr int kMaxSlots = BFP8_SWEEP_MAX_SLOTS;
+constexpr int kPasses = 4;  // passes whose loads are in flight together (64 blocks)
+
+struct SlotTable {
+    const float* x[kMaxSlots];
+    int pre[kMaxSlots + 1];  // first block of each slot; pre[n] = all blocks
+    int xoff[kMaxSlots], nb[kMaxSlots];
+    int n;
 };
 
-// Slot of background task t (blocks of slot 0, then slot 1, ...), and its block.
-__device__ __forceinline__ void task_of(const Slots& S, int t, int& slot, int& b) {
-    slot = 0;
-    b = t;
-    while (slot + 1 < S.n && b >= (S.act[slot].K >> 6)) {
-        b -= S.act[slot].K >> 6;
-        ++slot;
+__device__ __forceinline__ void slot_table(cptr<Bfp8SweepAct> act, int n, SlotTable& S) {
+    S.n = n < kMaxSlots ? n : kMaxSlots;  // (the host deals at most kMaxSlots)
+    int acc = 0;
+#pragma unroll
+    for (int k = 0; k < kMaxSlots; ++k) {
+        const bool in = k < S.n;
+        S.x[k] = in ? act[k].x : nullptr;
+        S.nb[k] = in ? act[k].K >> 6 : 0;
+        S.xoff[k] = in ? act[k].xoff : 0;
+        S.pre[k] = acc;
+        acc += S.nb[k];
     }
+    S.pre[kMaxSlots] = acc;
 }
 
-__device__ __forceinline__ int slot_end(const Slots& S, int slot) {
-    int e = 0;
-    for (int i = 0; i <= slot; ++i) e += S.act[i].K >> 6;
-    return e;
+struct SlotBlock {
+    const float* x;  // the block's 64 floats
+    int rec, scl;    // LDS word offsets of its record and its scale
+};
+
+__device__ __forceinline__ SlotBlock slot_block(const SlotTable& S, int g) {
+    SlotBlock r{S.x[0], S.xoff[0], S.xoff[0] + S.nb[0] * 32};
+#pragma unroll
+    for (int k = 0; k < kMaxSlots; ++k) {
+        if (k < S.n && g >= S.pre[k]) {
+            const int b = g - S.pre[k];
+            r.x = S.x[k] + (size_t)b * 64;
+            r.rec = S.xoff[k] + b * 32;
+            r.scl = S.xoff[k] + S.nb[k] * 32 + b;
+        }
+    }
+    return r;
 }
 
-// x of task t for this lane; past the last task the last task's x is read
-// (and never used), so that every step issues the same loads.
-__device__ __forceinline__ float task_x(const Slots& S, int t, int lane) {
-    int sl, b;
-    task_of(S, min(t, S.tasks - 1), sl, b);
-    return S.act[sl].x[(size_t)b * 64 + lane];
-}
-
-__device__ __forceinline__ void task_run(const Slots& S, int t, float xv, int lane, uint32_t* xact) {
-    if (t >= S.tasks) return;
-    int sl, b;
-    task_of(S, t, sl, b);
-    const int nb = S.act[sl].K >> 6, xoff = S.act[sl].xoff;
-    bfp8_quant_block_lds(xv, lane, reinterpret_cast<float*>(xact + xoff + nb * 32 + b), xact + xoff + b * 32);
+// Blocks g0 .. g0 + 16 kPasses - 1 of the workgroup: every x load, then
+// `between` (the first weights, for the first group), then the quantization.
+template <class F>
+__device__ __forceinline__ void quantize_slots(const SlotTable& S, int g0, int q, int r, uint32_t* xact,
+                                               F between) {
+    const int row = r >> 4, ii = r & 15, total = S.pre[kMaxSlots];
+    float xv[kPasses][4];
+    SlotBlock sb[kPasses];
+#pragma unroll
+    for (int u = 0; u < kPasses; ++u) {
+        const int g = g0 + 16 * u + 4 * q + row;
+        sb[u] = slot_block(S, g < total ? g : 0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xv[u][j] = sb[u].x[4 * ii + j];
+    }
+    __builtin_amdgcn_sched_barrier(0);  // the x loads go out first
+    between();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < kPasses; ++u) {
+        const int g = g0 + 16 * u + 4 * q + row;
+        bfp8_quant4_store_lds(xv[u], ii, reinterpret_cast<float*>(xact + sb[u].scl), xact + sb[u].rec, g < total);
+    }
 }
 
 __device__ __forceinline__ void issue(WBuf& B, const Tile& T, int c, int voff, int eoff) {
@@ -234,30 +270,12 @@ struct Pos {
     float fs;
 };
 
-// Quantizes blocks [S.next, upto) into their slots now: wavefront q takes
-// blocks S.next + q, + 4, ..., up to 16 of them with all their x loads issued
-// before the first is used (one memory round trip per 64 blocks).
-constexpr int kBatch = 16;
-__device__ __forceinline__ void run_tasks_now(Slots& S, int upto, int q, int r, uint32_t* xact) {
-    while (S.next < upto) {
-        float xv[kBatch];
-#pragma unroll
-        for (int u = 0; u < kBatch; ++u) xv[u] = task_x(S, S.next + q + kWaves * u, r);
-#pragma unroll
-        for (int u = 0; u < kBatch; ++u)
-            if (S.next + q + kWaves * u < upto) task_run(S, S.next + q + kWaves * u, xv[u], r, xact);
-        S.next = min(S.next + kWaves * kBatch, upto);
-    }
-}
-
 // One chunk step: the next chunk (of this tile, or the next tile's first)
 // goes out into `nxt`, then chunk `cur` is reduced.  Called with the buffers'
 // roles alternating, so that no register a pending load targets is ever
-// copied.  At a tile's end, a slot the next tile needs is quantized (its x
-// loads wait behind the chunk in flight, which is needed next anyway).
-// Returns false after the last chunk.
-__device__ __forceinline__ bool sweep_step(const Ctx& C, Pos& P, WBuf& cur, WBuf& nxt, Tile& Tc, Tile& Tn, Slots& S,
-                                           uint32_t* xact, SweepLds& L) {
+// copied.  Returns false after the last chunk.
+__device__ __forceinline__ bool sweep_step(const Ctx& C, Pos& P, WBuf& cur, WBuf& nxt, Tile& Tc, Tile& Tn,
+                                           const uint32_t* xact, SweepLds& L) {
     int ni = P.i, nc = P.c + 1;
     bool more = true;
     if (nc * kChunk >= Tc.nb) {
@@ -278,10 +296,6 @@ __device__ __forceinline__ bool sweep_step(const Ctx& C, Pos& P, WBuf& cur, WBuf
         finish_tile(C.descs, Tc, P.fs, C.q, C.r, P.parity, P.i < C.nh, C.kf, L);
         P.fs = 0.0f;
         P.parity ^= 1;
-        if (more && slot_end(S, Tn.slot) > S.next) {  // the next tile's slot
-            run_tasks_now(S, slot_end(S, Tn.slot), C.q, C.r, xact);
-            __syncthreads();
-        }
     }
     P.i = ni;
     P.c = nc;
@@ -310,30 +324,26 @@ extern "C" __global__ __launch_bounds__(256) void bfp8_sweep_kernel(Bfp8SweepArg
     // work list: this workgroup's lm_head tiles (computed), then its table tiles
     Tile TA, TB;
     WBuf A, B;
-    if (C.nh > 0) {  // the lm_head tile's weights before anything else
-        C.tile_at(0, TA);
-        issue(A, TA, 0, C.voff, C.eoff);
-    }
     const int tbeg = cp(a.wg_off)[C.wg];
     C.ntot = C.nh + cp(a.wg_off)[C.wg + 1] - tbeg;
     C.tiles = cp(a.tiles) + tbeg;
     if (C.ntot == 0) return;  // uniform per workgroup
-    if (C.nh == 0) {
-        C.tile_at(0, TA);
+    C.tile_at(0, TA);
+    // the activations: every x load of a group of passes, then (the first
+    // group only) the first weights, then the quantization into LDS
+    SlotTable S;
+    slot_table(cp(a.acts) + cp(a.act_off)[C.wg], cp(a.act_off)[C.wg + 1] - cp(a.act_off)[C.wg], S);
+    if (S.pre[kMaxSlots] > 0)  // (always: every tile reads a slot) straight-line, so it waits for x only
+        quantize_slots(S, 0, C.q, C.r, xact, [&] { issue(A, TA, 0, C.voff, C.eoff); });
+    else
         issue(A, TA, 0, C.voff, C.eoff);
-    }
-    Slots S;
-    S.act = cp(a.acts) + cp(a.act_off)[C.wg];
-    S.n = cp(a.act_off)[C.wg + 1] - cp(a.act_off)[C.wg];
-    S.tasks = slot_end(S, S.n - 1);
-    S.next = 0;
-    // the first tile's slot now, while its weights are in flight
-    run_tasks_now(S, slot_end(S, TA.slot), C.q, C.r, xact);
+    for (int g0 = 16 * kPasses; g0 < S.pre[kMaxSlots]; g0 += 16 * kPasses)
+        quantize_slots(S, g0, C.q, C.r, xact, [] {});
     __syncthreads();
     Pos P{0, 0, 0, 0.0f};
     for (;;) {
-        if (!sweep_step(C, P, A, B, TA, TB, S, xact, L)) break;
-        if (!sweep_step(C, P, B, A, TB, TA, S, xact, L)) break;
+        if (!sweep_step(C, P, A, B, TA, TB, xact, L)) break;
+        if (!sweep_step(C, P, B, A, TB, TA, xact, L)) break;
     }
     // the lm_head's top-k: one workgroup, after its own tiles
     if (a.head >= 0 && C.wg == a.merger) {
