@@ -63,7 +63,7 @@ constexpr int kMergeWaves = 16;  // wavefronts of the stand-alone merge kernel
 
 // Folded merge for workgroup 0 of a grouped launch.
 __device__ __noinline__ void topk_merge_folded(TopkArgs d, MergeLds<kWaves>& L) {
-    topk_merge<kWaves, 4>(d, PlainKeys{}, L);
+    topk_merge<kWaves, 4, 4, false>(d, PlainKeys{}, L);
     __syncthreads();  // L is reused by the streaming code
 }
 
@@ -645,7 +645,7 @@ extern "C" __global__ __launch_bounds__(kWideWaves * 64) void bfp8_gemv_wide_gro
 // Stand-alone final top-k merge (one workgroup of 16 wavefronts).
 extern "C" __global__ __launch_bounds__(kMergeWaves * 64) void bfp8_topk_merge_kernel(Bfp8GemvDesc d) {
     __shared__ MergeLds<kMergeWaves> L;
-    topk_merge<kMergeWaves, 1>(topk_args(d), PlainKeys{}, L);
+    topk_merge<kMergeWaves, 1, 8, true>(topk_args(d), PlainKeys{}, L);
 }
 
 // Batched GEMV: B activation vectors against one weight matrix, weights read

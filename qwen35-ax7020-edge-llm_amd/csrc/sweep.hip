@@ -351,7 +351,7 @@ extern "C" __global__ __launch_bounds__(256) void bfp8_sweep_kernel(Bfp8SweepArg
         const TopkArgs ta{d->partials, d->out_ids, d->out_scores, d->out_count, d->out_argmax, d->topk,
                           a.head_ntiles};
         __syncthreads();
-        topk_merge<kWaves, 4>(ta, C.kf, L.merge);
+        topk_merge<kWaves, 4, 4, false>(ta, C.kf, L.merge);
     }
 }
 

@@ -33,6 +33,8 @@ constexpr int kTopkMaxK = 64;
 
 // A key is read in two steps, so that a lane's reads all go out before any
 // is waited for: peek() issues the read, settle() returns the final key.
+typedef uint64_t u64x2 __attribute__((ext_vector_type(2)));
+
 struct PlainKeys {
     __device__ static int id(uint64_t k) { return (int)~(uint32_t)k; }
     __device__ uint64_t peek(const uint64_t* p) const { return __builtin_nontemporal_load(p); }
@@ -81,10 +83,19 @@ struct TopkArgs {
     int topk, ntiles;
 };
 
+// Threshold selection (topk_select below): at most kSelCap candidates are
+// ranked.
+constexpr int kSelCap = 256;
+constexpr int kSelPad = kSelCap + 16;  // zero-padded: the ranking reads sixteen keys at a time
+
 template <int W>
 struct MergeLds {
     uint64_t xch[W][64];
+    uint64_t cand[kSelPad];
+    uint32_t tw[W];
+    uint64_t best;
     int list[kTopkMaxK];
+    int ncand;
     int stale;
 };
 
@@ -132,12 +143,197 @@ __device__ __forceinline__ uint64_t wave_max_key(uint64_t v) {
     return v;
 }
 
+// Largest high word (ordered score) of the wavefront's keys, wave-uniform:
+// DPP within each row of 16 lanes, then the four row maxima by v_readlane.
+__device__ __forceinline__ uint32_t wave_max_score(uint32_t v) {
+#pragma unroll
+    for (int j = 1; j < 16; j <<= 1) {
+        const uint32_t o = xor_lane32(v, j);
+        v = o > v ? o : v;
+    }
+    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+    const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
+    const uint32_t d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+    const uint32_t ab = a > b ? a : b, cd = c > d ? c : d;
+    return ab > cd ? ab : cd;
+}
+
+// The c-th largest distinct score among the lanes' representatives (0 when
+// there are fewer than c): at least c keys have a score >= it.
+__device__ __forceinline__ uint32_t wave_cth_score(uint64_t rep, int c) {
+    uint32_t r = (uint32_t)(rep >> 32), m = 0;
+    for (int it = 0; it < c; ++it) {
+        m = wave_max_score(r);
+        if (r == m) r = 0;
+    }
+    return m;
+}
+
+// Ranks the n <= kSelCap candidates of L.cand (zero-padded) and writes the
+// result: candidate j's position is the number of candidates above it (keys
+// are unique).  Eight lanes count for one candidate, each over keys
+// 16m + 2 part, 16m + 2 part + 1; wavefronts without a candidate skip.
+template <int W, class KF>
+__device__ __forceinline__ void select_rank_write(const TopkArgs& d, MergeLds<W>& L, int n, bool stale) {
+    constexpr int NT = W * 64, NJ = NT / 8;
+    const int tid = threadIdx.x, w = tid >> 6, kk = d.topk;
+    const int part = tid & 7;
+    const u64x2* c2 = reinterpret_cast<const u64x2*>(L.cand) + part;
+    for (int j0 = 0; j0 < n; j0 += NJ) {
+        if (j0 + w * 8 >= n) break;  // wave-uniform
+        const int j = j0 + (tid >> 3);
+        const uint64_t key = L.cand[j < kSelCap ? j : 0];
+        int rank = 0;
+        int m = 0;
+        for (; m + 64 <= n; m += 64) {
+            u64x2 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[u] = c2[(m >> 1) + 8 * u];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) rank += (v[u].x > key ? 1 : 0) + (v[u].y > key ? 1 : 0);
+        }
+        for (; m < n; m += 16) {
+            const u64x2 v = c2[m >> 1];
+            rank += (v.x > key ? 1 : 0) + (v.y > key ? 1 : 0);
+        }
+        rank += (int)xor_lane32((uint32_t)rank, 1);
+        rank += (int)xor_lane32((uint32_t)rank, 2);
+        rank += (int)xor_lane32((uint32_t)rank, 4);
+        if (part == 0 && j < n) {
+            if (rank < kk) {
+                d.out_ids[rank] = KF::id(key);
+                d.out_scores[rank] = key_score(key);
+            }
+            if (rank == 0) L.best = key;
+        }
+    }
+    for (int j = n + tid; j < kk; j += NT) {
+        d.out_ids[j] = -1;
+        d.out_scores[j] = 0.0f;
+    }
+    if (stale) L.stale = 1;
+    __syncthreads();
+    if (tid == 0) {
+        const uint64_t b = L.best;
+        const bool st = L.stale != 0;
+        *d.out_count = st ? -1 : (n < kk ? n : kk);
+        *d.out_argmax = st ? -1 : ((key_valid(b) && key_score(b) > -1e30f) ? KF::id(b) : 0);
+    }
+}
+
+// Gathers the rest of a list above T from entry j0 on (rare), in batches
+// of eight: each batch is read, its prefix above T counted, given slots by
+// one LDS atomic and stored.
+template <int W, class KF>
+__device__ __forceinline__ void list_offer(const KF& kf, const uint64_t* list, int j0, int kk, uint64_t T,
+                                           bool& stale, MergeLds<W>& L) {
+    for (; j0 < kk; j0 += 8) {
+        uint64_t k8[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) k8[u] = j0 + u < kk ? kf.peek(list + j0 + u) : 0ull;
+        int cnt = 0;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            if (j0 + u < kk) k8[u] = kf.settle(k8[u], list + j0 + u, stale);
+            cnt += (cnt == u && key_valid(k8[u]) && k8[u] >= T) ? 1 : 0;
+        }
+        if (cnt) {
+            const int off = atomicAdd(&L.ncand, cnt);
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (u < cnt && off + u < kSelCap) L.cand[off + u] = k8[u];
+        }
+        if (cnt < 8) break;
+    }
+}
+
+// Selection by threshold, the fast path of topk_merge for 2 <= kk <= 64.
+// A lane's representative is the best key it read; wavefront w takes the
+// c-th best distinct score t_w among its representatives (c = ceil(kk / W);
+// 0 when it has fewer than c), and T is the lowest key with the score
+// min_w t_w.  Each wavefront with t_w != 0 holds at least c distinct keys
+// >= T, so at least kk keys are >= T when every t_w is valid, and T = 0 admits
+// every valid key otherwise: the kk best keys are always among the keys
+// >= T.  Lists are sorted descending, so a list's candidates are a prefix.
+// The candidates are gathered in LDS and ranked (select_rank_write).
+// Returns false (uniformly) when there are more than kSelCap candidates or
+// more lists than the form covers; the caller then runs the tree merge.
+// Random scores give ~100 candidates at kk = 40 over 1,024 lists; tables of
+// equal scores overflow and take the tree.
+//
+// KEEP (latency form, the stand-alone merge): lane quad t >> 2 reads the
+// first four entries of lists (t >> 2) + (NT / 4) p, p < PASSES, one entry
+// per lane (one wavefront load touches 16 lists' 32-byte heads), and keeps
+// them; only a list whose fourth entry is >= T is read on.
+// Otherwise (few registers, the merge folded into a streaming launch): lane t
+// reads the heads of lists t + NT p, p < PASSES, then reads on only through
+// the lists whose head is >= T, one batch of eight entries at a time.
+template <int W, int PASSES, bool KEEP, class KF>
+__device__ __forceinline__ bool topk_select(const TopkArgs& d, const KF& kf, MergeLds<W>& L, bool& stale) {
+    constexpr int NT = W * 64, NQ = NT / 4;
+    const int kk = d.topk, ntiles = d.ntiles;
+    if (ntiles > PASSES * (KEEP ? NQ : NT)) return false;
+    const uint64_t* parts = d.partials;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int ent = KEEP ? (tid & 3) : 0, q = KEEP ? (tid >> 2) : tid;
+    auto list_of = [&](int p) { return q + p * (KEEP ? NQ : NT); };
+    auto at = [&](int p) -> const uint64_t* { return &parts[(size_t)list_of(p) * kk + ent]; };
+    auto mine = [&](int p) { return list_of(p) < ntiles && ent < kk; };
+    uint64_t e[PASSES];
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) e[p] = mine(p) ? kf.peek(at(p)) : 0ull;
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p)
+        if (mine(p)) e[p] = kf.settle(e[p], at(p), stale);
+    uint64_t rep = 0;  // any distinct keys serve: the lane's best entry
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) rep = e[p] > rep ? e[p] : rep;
+    const uint32_t tw = wave_cth_score(rep, (kk + W - 1) / W);
+    if (lane == 0) L.tw[w] = tw;
+    for (int j = tid; j < kSelPad; j += NT) L.cand[j] = 0;
+    if (tid == 0) {
+        L.ncand = 0;
+        L.best = 0;
+    }
+    __syncthreads();
+    uint32_t ts = ~0u;
+#pragma unroll
+    for (int v = 0; v < W; ++v) ts = L.tw[v] < ts ? L.tw[v] : ts;
+    const uint64_t T = (uint64_t)ts << 32;
+    auto above = [&](uint64_t k) { return key_valid(k) && k >= T; };
+    int total = 0;
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) total += above(e[p]) ? 1 : 0;
+    int off = total ? atomicAdd(&L.ncand, total) : 0;
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p)
+        if (above(e[p])) {
+            if (off < kSelCap) L.cand[off] = e[p];
+            ++off;
+        }
+    if (KEEP) {  // lane 3 of a quad holds entry 3: the list goes on above T (rare)
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p)
+            if (above(e[p]) && ent == 3 && kk > 4) list_offer(kf, at(p) - 3, 4, kk, T, stale, L);
+    } else {
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p)
+            if (above(e[p]) && kk > 1) list_offer(kf, at(p), 1, kk, T, stale, L);
+    }
+    __syncthreads();
+    const int n = L.ncand;
+    if (n > kSelCap) return false;
+    select_rank_write<W, KF>(d, L, n, stale);
+    return true;
+}
+
 // Final merge by one workgroup of W wavefronts, H list heads per lane per
 // pass.  Keys are unique (they carry the row), so an entry at position i of a
 // list whose head ranks h-th among all heads has at least h+i better keys:
 // only the lists of the kk best heads, and in them only i < kk - h, can reach
 // the top kk.
-template <int W, int H, class KF>
+template <int W, int H, int PASSES, bool KEEP, class KF>
 __device__ __forceinline__ void topk_merge(const TopkArgs& d, const KF& kf, MergeLds<W>& L) {
     const int kk = d.topk;
     const int ntiles = d.ntiles;
@@ -163,6 +359,7 @@ __device__ __forceinline__ void topk_merge(const TopkArgs& d, const KF& kf, Merg
         }
         return;
     }
+    if (topk_select<W, PASSES, KEEP>(d, kf, L, stale)) return;
     // 1. the 64 best list heads
     uint64_t v = 0;
     for (int base = w * 64 * H; base < ntiles; base += W * 64 * H) {

@@ -412,6 +412,47 @@ def test_random_lm_heads_against_the_oracle(gpu, torch_mod):
         assert kk.lm_head_argmax(x, mant, exps, V, H) == ol.argmax(y_ref), (V, H, seed)
 
 
+@pytest.mark.parametrize("k", [2, 5, 40, 64])
+def test_lm_head_one_tile_holds_the_best(gpu, torch_mod, k, plan_mode):
+    """One 64-row tile's exponents sit 8 above the others', so most of the best
+    rows share its partial list: the merge's threshold selection keeps reading
+    that list past the entries it loads up front.  Stand-alone merge (16
+    wavefronts), folded into a plan's second launch (4 wavefronts) or in the
+    single launch (epoch-tagged keys); ids, scores, count and argmax against
+    the restatement."""
+    qk, torch = gpu, torch_mod
+    V, H = 65536, 1024
+    mant, exps = qk.synth_planes(V, H, 910, 122, 128)
+    exps = exps.copy()
+    exps[64 * 517:64 * 518] += 8
+    x = qk.synth_normal(H, 911)
+    y_ref, *_ = ol.gemv_neon(x, mant, exps)
+    ids_ref, sc_ref = ol.topk(y_ref, k)
+    assert np.sum((ids_ref >= 64 * 517) & (ids_ref < 64 * 518)) >= min(k, 20)
+    say("lm_head one tile holds the best", k, plan_mode)
+    dm = qk.DeviceMatrix.from_soa(mant, exps)
+    xt = torch.from_numpy(x).cuda()
+    _, xs, xsp = qk.quantize(xt)
+    ids, sc, cnt, am = qk.lm_head_topk(dm, xsp, xs, k)
+    torch.cuda.synchronize()
+    assert int(cnt.item()) == k and int(am.item()) == ol.argmax(y_ref)
+    assert np.array_equal(ids.cpu().numpy(), ids_ref) and same_f32(sc.cpu().numpy(), sc_ref)
+    sm, se = qk.synth_planes(128, 256, 912, 124, 130)
+    xo = qk.synth_normal(256, 913)
+    items = [{"mat": dm, "x": xt, "topk": k},
+             {"mat": qk.DeviceMatrix.from_soa(sm, se), "x": torch.from_numpy(xo).cuda(),
+              "y": torch.empty(128, dtype=torch.float32, device="cuda")}]
+    plan = qk.SweepPlan(items)
+    for rep in range(2):
+        plan.run()
+        torch.cuda.synchronize()
+        ids, sc, cnt = plan.topk_out
+        assert int(cnt[0].item()) == k and int(cnt[1].item()) == ol.argmax(y_ref), rep
+        assert np.array_equal(ids.cpu().numpy(), ids_ref) and same_f32(sc.cpu().numpy(), sc_ref), rep
+        assert same_f32(items[1]["y"].cpu().numpy(), ol.gemv_neon(xo, sm, se)[0]), rep
+    plan.close()
+
+
 def test_small_plan_one_tile_per_workgroup(gpu, torch_mod):
     """A plan without an lm_head and with few row tiles runs its GEMVs one tile
     per 16-wavefront workgroup; an odd-M item adds the tail-row kernel and a
