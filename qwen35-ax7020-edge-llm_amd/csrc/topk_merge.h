@@ -39,6 +39,9 @@ struct PlainKeys {
     __device__ static int id(uint64_t k) { return (int)~(uint32_t)k; }
     __device__ uint64_t peek(const uint64_t* p) const { return __builtin_nontemporal_load(p); }
     __device__ uint64_t settle(uint64_t k, const uint64_t*, bool&) const { return k; }
+    // every key current (nothing to wait for)
+    __device__ void verify_all(const uint64_t*, int, bool&) const {}
+    __device__ PlainKeys verified() const { return *this; }
 };
 
 constexpr uint32_t kEpochRowBits = 18;
@@ -57,6 +60,7 @@ struct EpochKeys {
         return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __device__ uint64_t settle(uint64_t k, const uint64_t* p, bool& stale) const {
+        if (stale) return 0;  // already given up: the result is reported invalid anyway
         for (int i = 0; i < kEpochSpin; ++i) {
             if (((uint32_t)k >> kEpochRowBits) == epoch) return k;
             __builtin_amdgcn_s_sleep(2);
@@ -68,6 +72,28 @@ struct EpochKeys {
     __device__ void store(uint64_t* p, uint64_t k) const {
         __hip_atomic_store(p, k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    // Waits (bounded) until each of the n keys carries the run's epoch; the
+    // workgroup's threads share the keys.  After it (and a barrier) every
+    // key can be read as verified(): no waiting per read.
+    __device__ void verify_all(const uint64_t* p, int n, bool& stale) const {
+        const int nt = blockDim.x;
+        for (int i0 = threadIdx.x; i0 < n; i0 += 8 * nt) {  // eight reads in flight
+            uint64_t k[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) k[u] = i0 + u * nt < n ? peek(p + i0 + u * nt) : 0ull;
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (i0 + u * nt < n) (void)settle(k[u], p + i0 + u * nt, stale);
+        }
+    }
+    struct Current {  // keys already seen with the run's epoch
+        __device__ static int id(uint64_t k) { return EpochKeys::id(k); }
+        __device__ uint64_t peek(const uint64_t* p) const {
+            return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __device__ uint64_t settle(uint64_t k, const uint64_t*, bool&) const { return k; }
+    };
+    __device__ Current verified() const { return Current{}; }
 };
 
 __device__ __forceinline__ bool key_valid(uint64_t k) { return (k >> 32) != 0; }
@@ -328,38 +354,14 @@ __device__ __forceinline__ bool topk_select(const TopkArgs& d, const KF& kf, Mer
     return true;
 }
 
-// Final merge by one workgroup of W wavefronts, H list heads per lane per
-// pass.  Keys are unique (they carry the row), so an entry at position i of a
-// list whose head ranks h-th among all heads has at least h+i better keys:
-// only the lists of the kk best heads, and in them only i < kk - h, can reach
-// the top kk.
-template <int W, int H, int PASSES, bool KEEP, class KF>
-__device__ __forceinline__ void topk_merge(const TopkArgs& d, const KF& kf, MergeLds<W>& L) {
+// The bitonic tree merge (lists of every length, any key distribution).
+template <int W, int H, class KF>
+__device__ __forceinline__ void topk_tree(const TopkArgs& d, const KF& kf, MergeLds<W>& L, bool& stale) {
     const int kk = d.topk;
     const int ntiles = d.ntiles;
     const uint64_t* parts = d.partials;
     const int lane = threadIdx.x & 63;
     const int w = threadIdx.x >> 6;
-    bool stale = false;
-    if (threadIdx.x == 0) L.stale = 0;
-    if (kk == 1) {  // the best key is the largest list head: a max-reduction, no list merge
-        uint64_t m = 0;
-        for (int i = w * 64 + lane; i < ntiles; i += W * 64) {
-            const uint64_t h = kf.settle(kf.peek(&parts[i]), &parts[i], stale);
-            m = h > m ? h : m;
-        }
-        m = wave_max_key(m);
-        if (lane == 0) L.xch[0][w] = m;
-        __syncthreads();
-        if (stale) L.stale = 1;
-        __syncthreads();
-        if (w == 0) {
-            m = wave_max_key(lane < W ? L.xch[0][lane] : 0ull);
-            topk_write<KF>(d, m, lane, L.stale != 0);
-        }
-        return;
-    }
-    if (topk_select<W, PASSES, KEEP>(d, kf, L, stale)) return;
     // 1. the 64 best list heads
     uint64_t v = 0;
     for (int base = w * 64 * H; base < ntiles; base += W * 64 * H) {
@@ -416,6 +418,46 @@ __device__ __forceinline__ void topk_merge(const TopkArgs& d, const KF& kf, Merg
     if (stale) L.stale = 1;
     __syncthreads();
     if (w == 0) topk_write<KF>(d, v, lane, L.stale != 0);
+}
+
+
+// Final merge by one workgroup of W wavefronts, H list heads per lane per
+// pass.  Keys are unique (they carry the row), so an entry at position i of a
+// list whose head ranks h-th among all heads has at least h+i better keys:
+// only the lists of the kk best heads, and in them only i < kk - h, can reach
+// the top kk.
+template <int W, int H, int PASSES, bool KEEP, class KF>
+__device__ __forceinline__ void topk_merge(const TopkArgs& d, const KF& kf, MergeLds<W>& L) {
+    const int kk = d.topk;
+    const int ntiles = d.ntiles;
+    const uint64_t* parts = d.partials;
+    const int lane = threadIdx.x & 63;
+    const int w = threadIdx.x >> 6;
+    bool stale = false;
+    if (threadIdx.x == 0) L.stale = 0;
+    if (kk == 1) {  // the best key is the largest list head: a max-reduction, no list merge
+        uint64_t m = 0;
+        for (int i = w * 64 + lane; i < ntiles; i += W * 64) {
+            const uint64_t h = kf.settle(kf.peek(&parts[i]), &parts[i], stale);
+            m = h > m ? h : m;
+        }
+        m = wave_max_key(m);
+        if (lane == 0) L.xch[0][w] = m;
+        __syncthreads();
+        if (stale) L.stale = 1;
+        __syncthreads();
+        if (w == 0) {
+            m = wave_max_key(lane < W ? L.xch[0][lane] : 0ull);
+            topk_write<KF>(d, m, lane, L.stale != 0);
+        }
+        return;
+    }
+    if (topk_select<W, PASSES, KEEP>(d, kf, L, stale)) return;
+    // more candidates than the selection ranks: the bitonic tree, over keys
+    // first waited for all at once (its reads then wait for nothing)
+    kf.verify_all(parts, ntiles * kk, stale);
+    __syncthreads();
+    topk_tree<W, H>(d, kf.verified(), L, stale);
 }
 
 }  // namespace
