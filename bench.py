@@ -289,7 +289,7 @@ def main():
     head = [it for it in items if it[5]]
     rest = [it for it in items if not it[5]]
     stages = []
-    single = plans[0].kernel_name(0) in ("bfp8_sweep_kernel", "bfp8_gemv_fused_kernel")  # the whole step in one launch
+    single = plans[0].kernel_name(0) == "bfp8_sweep_kernel"  # the whole plan in one launch
     for stage, its in (((0, items),) if single else ((0, head), (1, rest))):
         name = plans[0].kernel_name(stage)
         if not name:

@@ -375,15 +375,7 @@ int bfp8_dev_pack_rows(int8_t* mant_gpu, uint8_t* exps_gpu, const uint8_t* row_s
  * GEMV's (larger K first), whose workgroup 0 first merges the lm_head's
  * per-tile top-k partials.  When the lm_head's K is a multiple of 64 and at
  * most 1024 its launch also quantizes every activation of the plan (else, and
- * without an lm_head, a quantize launch comes first).  Such a plan with other
- * GEMVs (and an lm_head of at most 2^18 rows) runs as one launch instead
- * unless BFP8_PLAN_FUSED=0 when it is created: each workgroup does its lm_head
- * tiles and quantization tasks, publishes the records inside the launch,
- * waits until every activation's records are complete, streams its share of
- * the other GEMVs, and one workgroup then merges the top-k.  That launch
- * needs all of its workgroups resident at once: runs of one plan must not
- * overlap, and other work on the GPU meanwhile can delay it (a wait that gives
- * up is reported by bfp8_plan_status).  A plan without an
+ * without an lm_head, a quantize launch comes first).  A plan without an
  * lm_head runs one GEMV, or two reading the same x, 16 rows per workgroup, and
  * other plans of few row tiles one tile per 16-wavefront workgroup.  Item i
  * reads x (device, K floats) and writes y (device, M floats), or, for the
@@ -411,17 +403,11 @@ int bfp8_plan_run_gemv(void* plan, void* stream);
 /* One stage of bfp8_plan_run_gemv, for timing each launch on its own:
  * 0 = the lm_head's tiles, 1 = the other GEMVs' tiles with the top-k merge
  * (or the stand-alone merge kernel when the plan has no other GEMV),
- * 2 = odd-row tails and K > 4096 items.  Stages must run in this order.  A
- * fused or single-launch plan does stages 0 and 1 in stage 0. */
+ * 2 = odd-row tails and K > 4096 items.  Stages must run in this order. */
 int bfp8_plan_launch(void* plan, int stage, void* stream);
 /* Name of the (main) kernel a stage launches, "" if the stage is empty. */
 const char* bfp8_plan_kernel_name(void* plan, int stage);
 int bfp8_plan_quantize(void* plan, void* stream);
-/* 0 when every run of the plan so far waited for its records to completion;
- * 1 when a fused launch gave up waiting (its results are then not valid);
- * synchronizes the device.  No reference counterpart (the reference has no
- * plans). */
-int bfp8_plan_status(void* plan);
 void bfp8_plan_destroy(void* plan);
 
 /* Synthetic reference-format planes on the device: mantissas uniform in

@@ -262,14 +262,8 @@ __device__ __forceinline__ bool stream_step(const Src& src, WBuf& cur, WBuf& nxt
     return more;
 }
 
-struct NoHook {
-    __device__ void operator()() const {}
-};
-
-// first_issued() runs once the first chunk's loads are out, before any
-// activation word is read (the fused launch waits for its records there).
-template <bool kLanes, class Src, class Hook = NoHook>
-__device__ __forceinline__ void stream_tiles(const Src& src, StreamLds& L, const Hook& first_issued = Hook{}) {
+template <bool kLanes, class Src>
+__device__ __forceinline__ void stream_tiles(const Src& src, StreamLds& L) {
     const int n = src.count();
     if (n <= 0) return;
     const int q = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
@@ -286,7 +280,6 @@ __device__ __forceinline__ void stream_tiles(const Src& src, StreamLds& L, const
         open_tile(TA, src.desc(di), di, ti);
     }
     issue(A, TA, 0, wv, ev);
-    first_issued();
     int i = 0, c = 0, parity = 0;
     float fs = 0.0f;
     for (;;) {
@@ -428,62 +421,6 @@ __device__ __forceinline__ void quantize_task(const Bfp8HeadTask& d, float xv, i
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-
-// The same task with its records published inside the launch (the fused
-// launch): the split words and the scale go out as agent-scope (write-through)
-// stores, the wavefront waits until they are complete, then adds one to its
-// activation's counter (agent scope).  A reader that has seen an activation's
-// count complete finds every record of it in memory: no line of a record is
-// read in the launch before that (caches start invalidated at the launch).
-// (the int16 values, read by no plan kernel, stay plain stores)
-__device__ __forceinline__ void quantize_task_published(const Bfp8HeadTask& d, float xv, int lane, uint32_t* rec,
-                                                        uint32_t* counters) {
-    const int b = d.b;
-    const Bfp8QuantLane r = bfp8_quant_lane(xv);
-    if (d.xq) ((g_i16_ptr)d.xq)[(size_t)b * 64 + lane] = (int16_t)r.xq;
-    if (lane == 0) __hip_atomic_store(&d.xscale[b], r.xs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int xl = (int)(int8_t)(r.xq & 0xff);
-    const int xh = (r.xq - xl) >> 8;
-    const int pos = bfp8_split_pos(lane);
-    uint8_t* rb = reinterpret_cast<uint8_t*>(rec);
-    rb[pos] = (uint8_t)xh;
-    rb[pos + 16] = (uint8_t)xl;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    if (lane < 32)
-        __hip_atomic_store(&d.xsplit[(size_t)b * 32 + lane], rec[lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // every store of this wavefront is complete
-    if (lane == 0) __hip_atomic_fetch_add(&counters[d.act], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// How the lm_head launch's body hands its results on: PlainPub for the
-// two-launch plan (the launch boundary publishes), FusedPub for the fused
-// launch (published records, epoch-tagged top-k keys).
-struct PlainPub {
-    __device__ void task(const Bfp8HeadTask& d, float xv, int lane, uint32_t* rec) const {
-        quantize_task(d, xv, lane, rec);
-    }
-    __device__ PlainKeyStore keys() const { return PlainKeyStore{}; }
-};
-struct EpochKeyStore {
-    EpochKeys kf;
-    __device__ void operator()(uint64_t* p, uint64_t rank_key) const {
-        kf.store(p, kf.make(tile_partial_key(rank_key), key_id(rank_key)));
-    }
-};
-struct FusedPub {
-    uint32_t* counters;
-    EpochKeys kf;
-    __device__ void task(const Bfp8HeadTask& d, float xv, int lane, uint32_t* rec) const {
-        quantize_task_published(d, xv, lane, rec, counters);
-    }
-    __device__ EpochKeyStore keys() const { return EpochKeyStore{kf}; }
-};
-
 }  // namespace
 
 // Every load is unconditional (indices clamped): the compiler can then count
@@ -513,10 +450,8 @@ __device__ __forceinline__ void head_issue(HeadTile& T, const Bfp8HeadArgs& a, i
 
 // fs_q of one tile (blocks in order), then y = (fs0 + fs2) + (fs1 + fs3) and
 // the tile's top-k partial
-template <class Store>
 __device__ __forceinline__ void head_reduce(HeadTile& T, const Bfp8HeadArgs& a, int t, int nb, int q, int lane,
-                                            uint32_t xr0, uint32_t xr1, uint32_t xsv, HeadLds& L,
-                                            const Store& store) {
+                                            uint32_t xr0, uint32_t xr1, uint32_t xsv, HeadLds& L) {
     const __amdgpu_buffer_rsrc_t wrs = head_wrs(a, t, nb);
     float fs = 0.0f;
 #pragma unroll
@@ -561,7 +496,7 @@ __device__ __forceinline__ void head_reduce(HeadTile& T, const Bfp8HeadArgs& a, 
     }
     if (topk > 0) {
         __syncthreads();
-        tile_topk_rank(L.keys, partials, t, topk, q, lane, store);
+        tile_topk_rank(L.keys, partials, t, topk, q, lane);
     }
     __syncthreads();  // L.red and L.keys are reused by the next tile
 }
@@ -576,8 +511,8 @@ __device__ __forceinline__ void head_reduce(HeadTile& T, const Bfp8HeadArgs& a, 
 // for, and under the weight streams they returned late.  Then the weights,
 // with nothing but the arguments before them, and the task is quantized with
 // the activation while they stream.
-template <class Pub>
-__device__ __forceinline__ void head_phase(const Bfp8HeadArgs& a, HeadLds& L, const Pub& pub) {
+extern "C" __global__ __launch_bounds__(256) void bfp8_gemv_head_kernel(Bfp8HeadArgs a) {
+    __shared__ HeadLds L;
     const int q = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int nb = a.K >> 6;  // 1 .. BFP8_HEAD_MAX_NB (host-checked)
@@ -634,7 +569,7 @@ __device__ __forceinline__ void head_phase(const Bfp8HeadArgs& a, HeadLds& L, co
     bfp8_quant4_store_lds(hv, hi, &L.xsc[hbs], &L.xs[hb * 32], hb < nb);
     // this wavefront's quantization task now too (its element came in with the
     // activation), so that its stores go out while the weights stream
-    if (wid < a.ntasks) pub.task(task, tv, lane, L.rec[q]);
+    if (wid < a.ntasks) quantize_task(task, tv, lane, L.rec[q]);
     __syncthreads();
 
     // 2. residue q's split words in registers: lane l holds word l & 7 of
@@ -645,88 +580,16 @@ __device__ __forceinline__ void head_phase(const Bfp8HeadArgs& a, HeadLds& L, co
     const uint32_t xsv = lane < nb ? __float_as_uint(L.xsc[lane]) : 0u;
 
     // 3. the tiles
-    head_reduce(T, a, t, nb, q, lane, xr0, xr1, xsv, L, pub.keys());
+    head_reduce(T, a, t, nb, q, lane, xr0, xr1, xsv, L);
     for (t += gridDim.x; t < a.ntiles; t += gridDim.x) {
         head_issue(T, a, t, nb, q, lane);
-        head_reduce(T, a, t, nb, q, lane, xr0, xr1, xsv, L, pub.keys());
+        head_reduce(T, a, t, nb, q, lane, xr0, xr1, xsv, L);
     }
     // 4. the quantization tasks beyond one per wavefront (more tasks than
     // wavefronts)
     for (int j = wid + nw; j < a.ntasks; j += nw) {
         const Bfp8HeadTask tj = a.qtasks[j];
-        pub.task(tj, tj.x[lane], lane, L.rec[q]);
-    }
-}
-
-extern "C" __global__ __launch_bounds__(256) void bfp8_gemv_head_kernel(Bfp8HeadArgs a) {
-    __shared__ HeadLds L;
-    head_phase(a, L, PlainPub{});
-}
-
-// ---- the whole plan step in one launch ------------------------------------------------
-// Every workgroup first runs the lm_head launch's part above with its results
-// published inside the launch (FusedPub), then waits until every activation's
-// counter shows its records complete -- by then, its own lm_head tile done,
-// the tasks (run first in every workgroup) are long finished -- then streams
-// its slice of the other GEMVs' tiles as the grouped launch does (scalar
-// loads of the records: no line of them was read in the launch before the
-// wait), and the merging workgroup ends with the lm_head's top-k, read as
-// epoch-tagged keys.  One launch instead of two: no second dispatch, and the
-// lm_head tiles' slow finishers overlap the layer tiles of the others.
-constexpr int kPublishSpin = 1 << 14;  // polls of the counters before a wait gives up
-
-__device__ __forceinline__ void topk_merge_fused(TopkArgs d, EpochKeys kf, MergeLds<kWaves>& L) {
-    topk_merge<kWaves, 4, 4, false>(d, kf, L);
-}
-
-// The first look at the counters is a plain load, which the L2 serves to all
-// but the first workgroup of each XCD (1,024 workgroups polling the same
-// lines past the L2 queue at one memory channel).  A counter only grows within
-// the launch (and the L2 starts the launch without its lines), so a cached
-// value can only be too low: a count it shows complete is complete, and only
-// an incomplete one makes the wavefront poll past the L2.
-__device__ __forceinline__ void wait_published(const Bfp8FusedArgs& f) {
-    if (threadIdx.x < 64) {
-        const int lane = threadIdx.x;
-        auto complete = [&](bool coherent) {
-            bool ok = true;
-            for (int i = lane; i < f.nacts; i += 64) {
-                const uint32_t c = coherent ? __hip_atomic_load(&f.counters[i], __ATOMIC_RELAXED,
-                                                                __HIP_MEMORY_SCOPE_AGENT)
-                                            : f.counters[i];
-                ok = ok && (int32_t)(c - f.run * (uint32_t)f.act_nb[i]) >= 0;
-            }
-            return __builtin_amdgcn_ballot_w64(!ok) == 0;
-        };
-        if (!complete(false)) {
-            for (int spin = 0;; ++spin) {
-                if (complete(true)) break;
-                if (spin == kPublishSpin) {
-                    if (lane == 0) __hip_atomic_store(f.status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(8);
-            }
-        }
-    }
-    __syncthreads();
-}
-
-extern "C" __global__ __launch_bounds__(256) void bfp8_gemv_fused_kernel(Bfp8HeadArgs a, Bfp8FusedArgs f) {
-    __shared__ HeadLds LH;
-    __shared__ StreamLds LS;
-    const EpochKeys kf{f.epoch};
-    head_phase(a, LH, FusedPub{f.counters, kf});
-    if ((int)blockIdx.x < f.rest_nwg) {  // the first weights go out before the wait
-        const int beg = f.wg_off[blockIdx.x];
-        TableTiles src{a.descs, f.tiles, beg, f.wg_off[blockIdx.x + 1] - beg};
-        stream_tiles<false>(src, LS, [&] { wait_published(f); });
-    }
-    if ((int)blockIdx.x == f.merger) {
-        const Bfp8GemvDesc& d = a.descs[a.head];
-        __syncthreads();
-        topk_merge_fused(TopkArgs{d.partials, d.out_ids, d.out_scores, d.out_count, d.out_argmax, d.topk, a.ntiles},
-                         kf, LS.merge);
+        quantize_task(tj, tj.x[lane], lane, L.rec[q]);
     }
 }
 
@@ -985,18 +848,6 @@ hipError_t bfp8_launch_gemv_grouped(const Bfp8GemvDesc* descs_dev, const Bfp8Til
     else
         hipLaunchKernelGGL(bfp8_gemv_grouped_kernel, dim3(nwg), dim3(256), 0, s, descs_dev, tiles_dev,
                            wg_off_dev);
-    return hipGetLastError();
-}
-
-int bfp8_fused_grid() {
-    static const int g = resident_grid(reinterpret_cast<const void*>(bfp8_gemv_fused_kernel));
-    return g;
-}
-
-hipError_t bfp8_launch_gemv_fused(const Bfp8HeadArgs& a, const Bfp8FusedArgs& f, int nwg, hipStream_t s) {
-    if (nwg <= 0 || a.ntiles < nwg || nwg > bfp8_fused_grid() || f.rest_nwg > nwg || f.merger < 0 || f.merger >= nwg)
-        return hipErrorInvalidValue;
-    hipLaunchKernelGGL(bfp8_gemv_fused_kernel, dim3(nwg), dim3(256), 0, s, a, f);
     return hipGetLastError();
 }
 

@@ -121,8 +121,7 @@ struct Bfp8HeadTask {
     float* xscale;
     uint32_t* xsplit;
     int b;
-    int act;           // the activation's index (its publication counter in the fused launch)
-    int pad_[2];
+    int pad_[3];
 };
 struct Bfp8HeadArgs {
     const Bfp8GemvDesc* descs;    // descs[head]: the outputs (y, partials, topk, pair_rows)
@@ -135,32 +134,6 @@ struct Bfp8HeadArgs {
     int ntasks;
 };
 hipError_t bfp8_launch_gemv_head(const Bfp8HeadArgs& a, int nwg, hipStream_t s);
-
-// The whole plan step in one launch: every workgroup runs its part of the
-// lm_head launch above (lm_head tiles; quantization tasks whose records are
-// published with write-through stores and counted per activation), waits
-// until every activation's count says its records are complete, streams its
-// slice of the other GEMVs' tile table (wg_off / tiles, as the grouped
-// launch), and workgroup `merger` then merges the lm_head's top-k from
-// epoch-tagged keys.  All workgroups must be resident at once (the waits spin):
-// nwg <= bfp8_fused_grid().  Counters grow by each activation's block count
-// per run: run r waits for counters[a] >= r * act_nb[a] (mod 2^32).
-struct Bfp8FusedArgs {
-    const Bfp8TileRef* tiles;
-    const int* wg_off;           // [rest_nwg + 1]
-    int rest_nwg;                // workgroups with a slice (<= the grid)
-    int merger;                  // workgroup that merges the lm_head top-k
-    uint32_t* counters;          // [nacts] blocks published per activation, never reset
-    const int* act_nb;           // [nacts] blocks per activation
-    int nacts;
-    uint32_t run;                // 1, 2, ... per launch of the plan
-    uint32_t epoch;              // of the lm_head keys, 1 .. 2^14 - 1
-    int* status;                 // set to 1 when a wait gave up (results then invalid)
-};
-hipError_t bfp8_launch_gemv_fused(const Bfp8HeadArgs& a, const Bfp8FusedArgs& f, int nwg, hipStream_t s);
-int bfp8_fused_grid();
-// Extra load, in blocks, of the fused launch's merging workgroup.
-#define BFP8_FUSED_MERGE_COST_BLOCKS 16
 // Extra load, in blocks of the byte-balanced dealing, that a folded merge
 // puts on workgroup 0 of a grouped launch (the threshold selection of the
 // 24-layer sweep's 1024 lm_head lists, ~7 us in one workgroup, about 11 blocks

@@ -208,9 +208,7 @@ void forward_cache_clear();
 // Forgets the preloaded tensors' names (qwen_weights.cpp); g.mu held.
 void weights_index_clear();
 
-// Deals the tiles of items[idx] over a launch (persistent or wide), over at
-// most `grid` workgroups (0: bfp8_stream_grid()).
-int deal_tiles(Launch& L, const std::vector<int>& idx, const bfp8_plan_item* items, int wg0_extra, bool allow_wide,
-               int grid = 0);
+// Deals the tiles of items[idx] over a launch (persistent or wide).
+int deal_tiles(Launch& L, const std::vector<int>& idx, const bfp8_plan_item* items, int wg0_extra, bool allow_wide);
 
 }  // namespace qhost

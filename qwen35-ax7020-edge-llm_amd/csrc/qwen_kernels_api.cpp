@@ -1101,27 +1101,12 @@ struct Plan {
     DevBuf s_tiles, s_wgoff, s_acts, s_actoff;
     int s_nwg = 0, s_lds = 0, s_merger = -1;
     uint32_t epoch = 0;            // of the last launch; the partials start zeroed (epoch 0)
-    // fused launch (bfp8_ftz.hip): the whole step in one launch
-    bool fused = false;
-    int f_nwg = 0;
-    uint32_t f_run = 0;            // launches so far
-    DevBuf f_counters, f_actnb, f_status;
 };
 
 // The single launch is opt-in (BFP8_PLAN_SINGLE_LAUNCH=1 when the plan is
 // created).
 bool single_launch_enabled() {
     const char* e = getenv("BFP8_PLAN_SINGLE_LAUNCH");
-    return e && e[0] == '1';
-}
-
-// rows of an lm_head whose keys carry the run's epoch (topk_merge.h EpochKeys)
-constexpr int kEpochRowBitsHost = 18;
-
-// The fused launch (one launch per step, the records published in-launch)
-// is opt-in: BFP8_PLAN_FUSED=1 when the plan is created.
-bool fused_launch_enabled() {
-    const char* e = getenv("BFP8_PLAN_FUSED");
     return e && e[0] == '1';
 }
 
@@ -1252,8 +1237,7 @@ bool deal_sweep(Plan* p, const bfp8_plan_item* items, int n) {
 // workgroups, longest first onto the least-loaded workgroup (bytes), and
 // uploads the table.  `wg0_extra` blocks of load are pre-charged to
 // workgroup 0 (a folded merge).
-int deal_tiles(Launch& L, const std::vector<int>& idx, const bfp8_plan_item* items, int wg0_extra, bool allow_wide,
-               int grid) {
+int deal_tiles(Launch& L, const std::vector<int>& idx, const bfp8_plan_item* items, int wg0_extra, bool allow_wide) {
     std::vector<Bfp8TileRef> order;
     for (int i : idx) {
         for (int t = 0; t < bfp8_ntiles(items[i].M); ++t) order.push_back(Bfp8TileRef{i, t});
@@ -1268,7 +1252,7 @@ int deal_tiles(Launch& L, const std::vector<int>& idx, const bfp8_plan_item* ite
         HIP_OK(hipMemcpy(L.tiles.p, order.data(), order.size() * sizeof(Bfp8TileRef), hipMemcpyHostToDevice));
         return BFP8_OK;
     }
-    const int nwg = std::min<int>((int)order.size(), grid > 0 ? grid : bfp8_stream_grid());
+    const int nwg = std::min<int>((int)order.size(), bfp8_stream_grid());
     std::vector<std::vector<Bfp8TileRef>> per(nwg);
     using Load = std::pair<long long, int>;
     std::priority_queue<Load, std::vector<Load>, std::greater<Load>> heap;
@@ -1301,7 +1285,6 @@ void release_plan(Plan* p) {
     p->logits.release(); p->gen_partials.release(); p->gen_keys.release();
     p->s_tiles.release(); p->s_wgoff.release(); p->s_acts.release(); p->s_actoff.release();
     p->head.tiles.release(); p->head.wg_off.release(); p->rest.tiles.release(); p->rest.wg_off.release();
-    p->f_counters.release(); p->f_actnb.release(); p->f_status.release();
 }
 
 }  // namespace qhost
@@ -1440,7 +1423,6 @@ void* bfp8_plan_create(const bfp8_plan_item* items, int n) {
                 t.xscale = hq[qi].xscale;
                 t.xsplit = hq[qi].xsplit;
                 t.b = b;
-                t.act = qi;
                 return t;
             };
             for (int qi = 0; qi < (int)hq.size(); ++qi) {
@@ -1456,36 +1438,6 @@ void* bfp8_plan_create(const bfp8_plan_item* items, int n) {
                     rc = BFP8_EHIP;
             }
             p->fused_head = !rc;
-        }
-    }
-    // The fused launch: a fused lm_head (one tile per workgroup or more) and
-    // other GEMVs on the streaming kernel, every workgroup resident at once.
-    if (!rc && p->fused_head && fold && !rows && p->ntasks > 0 && fused_launch_enabled() &&
-        !single_launch_enabled() && items[p->topk_desc].M <= (1 << kEpochRowBitsHost)) {
-        const int grid = std::min(bfp8_fused_grid(), p->head.ntiles);
-        std::vector<int> act_nb(hq.size(), 0);
-        for (int qi = 0; qi < (int)hq.size(); ++qi)
-            if (qi != hq_of_item[p->topk_desc]) act_nb[qi] = bfp8_nblocks(hq[qi].K);
-        Launch rest;
-        int frc = deal_tiles(rest, rest_idx, items, BFP8_FUSED_MERGE_COST_BLOCKS, false, grid);
-        frc = frc ? frc : p->f_counters.reserve(hq.size() * 4);
-        frc = frc ? frc : p->f_actnb.reserve(hq.size() * 4);
-        frc = frc ? frc : p->f_status.reserve(4);
-        if (!frc && (hipMemset(p->f_counters.p, 0, hq.size() * 4) != hipSuccess ||
-                     hipMemcpy(p->f_actnb.p, act_nb.data(), act_nb.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
-                     hipMemset(p->f_status.p, 0, 4) != hipSuccess ||
-                     hipMemset(p->partials.p, 0, p->partials.n) != hipSuccess))  // epoch 0: never a run's
-            frc = BFP8_EHIP;
-        if (!frc && rest.nwg <= grid) {
-            p->rest.tiles.release();
-            p->rest.wg_off.release();
-            p->rest = std::move(rest);
-            p->fused = true;
-            p->f_nwg = grid;
-        } else {
-            rest.tiles.release();
-            rest.wg_off.release();
-            rc = frc;
         }
     }
     // one launch for the whole plan when every item is a quantized GEMV of
@@ -1554,36 +1506,6 @@ int bfp8_plan_launch(void* plan, int stage, void* stream) {
         HIP_OK(bfp8_launch_sweep(a, p->s_nwg, p->s_lds, s));
         return BFP8_OK;
     }
-    if (p->fused) {  // stages 0 and 1 in one launch
-        if (stage == 0) {
-            const Bfp8GemvDesc& hd = p->hdesc[p->topk_desc];
-            Bfp8HeadArgs a{};
-            a.descs = descs;
-            a.head = p->topk_desc;
-            a.mant = hd.mant;
-            a.exps = hd.exps;
-            a.K = hd.K;
-            a.ntiles = p->head.ntiles;
-            a.hx = p->items[p->topk_desc].x;
-            a.qtasks = p->qtasks.as<Bfp8HeadTask>();
-            a.ntasks = p->ntasks;
-            Bfp8FusedArgs f{};
-            f.tiles = p->rest.tiles.as<Bfp8TileRef>();
-            f.wg_off = p->rest.wg_off.as<int>();
-            f.rest_nwg = p->rest.nwg;
-            f.merger = 0;
-            f.counters = p->f_counters.as<uint32_t>();
-            f.act_nb = p->f_actnb.as<int>();
-            f.nacts = p->nq;
-            f.run = ++p->f_run;
-            p->epoch = p->epoch % 16383u + 1u;
-            f.epoch = p->epoch;
-            f.status = p->f_status.as<int>();
-            HIP_OK(bfp8_launch_gemv_fused(a, f, p->f_nwg, s));
-            return BFP8_OK;
-        }
-        if (stage == 1) return BFP8_OK;
-    }
     if (stage == 0) {
         if (p->fused_head) {
             const Bfp8GemvDesc& hd = p->hdesc[p->topk_desc];
@@ -1650,7 +1572,6 @@ const char* bfp8_plan_kernel_name(void* plan, int stage) {
     const Plan* p = static_cast<const Plan*>(plan);
     if (!p) return "";
     if (p->sweep) return stage == 0 ? "bfp8_sweep_kernel" : "";
-    if (p->fused && stage < 2) return stage == 0 ? "bfp8_gemv_fused_kernel" : "";
     const bool fold = p->topk_desc >= 0 && p->rest.nwg > 0;
     if (stage == 0) return p->head.nwg > 0 ? (p->fused_head ? "bfp8_gemv_head_kernel" : "bfp8_gemv_grouped_kernel") : "";
     if (stage == 1) {
@@ -1681,16 +1602,6 @@ int bfp8_plan_run(void* plan, void* stream) {
     // the single launch, a fused lm_head launch or a 16-row launch quantizes its activations itself
     int rc = (p && (p->sweep || p->fused_head || p->rows_float)) ? BFP8_OK : bfp8_plan_quantize(plan, stream);
     return rc ? rc : bfp8_plan_run_gemv(plan, stream);
-}
-
-int bfp8_plan_status(void* plan) {
-    Plan* p = static_cast<Plan*>(plan);
-    if (!p) return BFP8_EINVAL;
-    if (!p->fused) return 0;
-    int st = 0;
-    HIP_OK(hipDeviceSynchronize());
-    HIP_OK(hipMemcpy(&st, p->f_status.p, sizeof st, hipMemcpyDeviceToHost));
-    return st;
 }
 
 void bfp8_plan_destroy(void* plan) {

@@ -49,14 +49,8 @@ __device__ __forceinline__ uint64_t tile_partial_key(uint64_t k) { return (k >> 
 // keys[16qq .. 16qq+15] above its row's key 16w + r, the quad adds the four
 // counts (DPP), and quarter 0 stores the key at its rank.  Distinct keys make
 // the ranks a permutation of 0..63, so slots 0..topk-1 are all written.
-// `store` gets the row's rank key (PlainKeyStore: its tile_partial_key form,
-// a plain store).
-struct PlainKeyStore {
-    __device__ void operator()(uint64_t* p, uint64_t rank_key) const { *p = tile_partial_key(rank_key); }
-};
-template <class Store = PlainKeyStore>
 __device__ __forceinline__ void tile_topk_rank(const uint64_t* keys, uint64_t* partials, int tile, int topk, int w,
-                                               int lane, const Store& store = Store{}) {
+                                               int lane) {
     const int r = lane >> 2, qq = lane & 3;
     const uint64_t mine = keys[16 * w + r];
     const uint64_t* quarter = keys + 16 * qq;
@@ -65,7 +59,7 @@ __device__ __forceinline__ void tile_topk_rank(const uint64_t* keys, uint64_t* p
     for (int i = 0; i < 16; ++i) cnt += quarter[i] > mine ? 1 : 0;
     cnt += __builtin_amdgcn_update_dpp(0, cnt, 0xB1, 0xF, 0xF, false);  // + quad lane ^ 1
     cnt += __builtin_amdgcn_update_dpp(0, cnt, 0x4E, 0xF, 0xF, false);  // + quad lane ^ 2
-    if (qq == 0 && cnt < topk) store(&partials[(size_t)tile * topk + cnt], mine);
+    if (qq == 0 && cnt < topk) partials[(size_t)tile * topk + cnt] = tile_partial_key(mine);
 }
 
 // ---- wavefront exchange ----------------------------------------------------

@@ -187,8 +187,6 @@ def bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.bfp8_plan_kernel_name.restype = ctypes.c_char_p
     lib.bfp8_plan_destroy.argtypes = [vp]
     lib.bfp8_plan_destroy.restype = None
-    lib.bfp8_plan_status.argtypes = [vp]
-    lib.bfp8_plan_status.restype = i
     lib.bfp8_synth_planes_host.argtypes = [vp, vp, i, i, c_uint64, i, i]
     lib.bfp8_synth_planes_host.restype = None
     lib.bfp8_synth_normal.argtypes = [vp, i, c_uint64]
@@ -495,10 +493,6 @@ class SweepPlan:
     def launch(self, stage):
         """One GEMV stage: 0 lm_head tiles, 1 other tiles + merge, 2 tails."""
         check(load().bfp8_plan_launch(self.handle, stage, _stream()), "plan_launch")
-
-    def status(self):
-        """0 when every fused run waited for its records to completion (syncs)."""
-        return load().bfp8_plan_status(self.handle)
 
     def close(self):
         if self.handle:
