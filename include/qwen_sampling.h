@@ -20,14 +20,15 @@ extern "C" {
 /* Replaces lm_head_topk(), 04/qwen_sampling.c:283-353: streaming top-k of the
  * bf16 lm_head (board-build dot products; hidden % 8 trailing elements
  * added), sorted by (score desc, id asc) among scores above -FLT_MAX.
- * Returns min(k, vocab_size) candidates or fewer; 0 on invalid arguments and,
- * here, for k above 64. */
+ * Returns min(k, vocab_size) candidates or fewer; 0 on invalid arguments
+ * (here also a vocabulary above 2^28 rows).  k <= 64 runs fused into the
+ * scoring launch, larger k through the scores and a sort of their keys. */
 int lm_head_topk(const float* h, const uint16_t* embed_table, int vocab_size, int hidden_dim, int k, int* out_ids,
                  float* out_scores);
 
 /* Replaces sample_from_topk(), 04/qwen_sampling.c:384-529: temperature /
  * top-k / top-p sampling with the xorshift32 state *rng_state.  Returns the
- * chosen id, -1 on invalid arguments (and, here, above 4096 candidates). */
+ * chosen id, -1 on invalid arguments (here also above 2^28 candidates). */
 int sample_from_topk(const int* ids, const float* scores, int n, float temperature, int top_k, float top_p,
                      unsigned int* rng_state);
 
