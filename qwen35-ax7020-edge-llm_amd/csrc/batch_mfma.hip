@@ -61,40 +61,75 @@ struct MfLds {
 // the end's exchange: 3 residue groups x 2 halves x 8 values x 64 lanes at most
 static_assert(sizeof(MfLds::xa) >= 3 * 2 * 8 * 64 * sizeof(float), "the fs exchange fits in the staging area");
 
-// Stages blocks c0 .. c0+nbc-1 of the B split activations and scales (vectors
-// >= B and blocks >= nbc as zeros), then each block's exponent range
-// [lo, hi] inside which es * xs is a normal float for every normal scale xs of
-// the batch: biased exponent of es * xs = e - 134 + E(xs), normal for
-// 1..254, and e <= 236 keeps float(S) * es finite.
-__device__ void mf_stage(MfLds& L, const uint32_t* __restrict__ xsplit, const float* __restrict__ xscale, int nb,
-                         int B, int c0, int nbc) {
-    // 16 bytes of xsplit = one part of one residue (both k halves): item
-    // ((u * 4 + q) * 2 + p) * 16 + v, vectors fastest, so the LDS stores of
-    // consecutive threads are consecutive
-    for (int i = threadIdx.x; i < kMfChunk * 4 * 2 * kMfVec; i += blockDim.x) {
-        const int v = i % kMfVec, p = (i / kMfVec) % 2, q = (i / (2 * kMfVec)) % 4, u = i / (8 * kMfVec);
-        u32x4 val = {0u, 0u, 0u, 0u};
-        if (v < B && u < nbc)
-            val = *reinterpret_cast<const u32x4*>(xsplit + ((size_t)v * nb + c0 + u) * BFP8_XSPLIT_WORDS_PER_BLOCK +
-                                                  q * 8 + p * 4);
-        L.xa[u][q][p * 16 + v] = ((uint64_t)val.y << 32) | val.x;       // k half 0: bytes 0..7
-        L.xa[u][q][32 + p * 16 + v] = ((uint64_t)val.w << 32) | val.z;  // k half 1: bytes 8..15
-    }
-    for (int i = threadIdx.x; i < kMfChunk * kMfVec; i += blockDim.x) {
-        const int v = i % kMfVec, u = i / kMfVec;
-        const float xs = (v < B && u < nbc) ? xscale[(size_t)v * nb + c0 + u] : 0.0f;
-        L.xs[u][v] = xs;
-        const int E = (int)((__float_as_uint(xs) >> 23) & 0xffu);
-        const bool normal = E >= 1 && E <= 254;
-        int emin = normal ? E : 255, emax = normal ? E : 0;
+// Staging of blocks c0 .. c0+nbc-1 of the B split activations and scales
+// (vectors >= B and blocks >= nbc as zeros) into LDS, with each block's
+// exponent range [lo, hi] inside which es * xs is a normal float for every
+// normal scale xs of the batch: biased exponent of es * xs = e - 134 + E(xs),
+// normal for 1..254, and e <= 236 keeps float(S) * es finite.  In two halves
+// so that a caller can issue other loads between them: mf_stage_load issues
+// every load of the NT threads (one round trip to L2 for all of them),
+// mf_stage_store waits for them, writes LDS and synchronizes the workgroup.
+constexpr int kMfItems = kMfChunk * 4 * 2 * kMfVec;  // 16-byte pieces of split activations
+constexpr int kMfScales = kMfChunk * kMfVec;
+
+template <int NT>
+struct MfStaged {
+    static_assert(kMfItems % NT == 0, "whole staging rounds");
+    static constexpr int kScaleRounds = (kMfScales + NT - 1) / NT;
+    u32x4 val[kMfItems / NT];
+    float xs[kScaleRounds];
+};
+
+// 16 bytes of xsplit = one part of one residue (both k halves): item
+// ((u * 4 + q) * 2 + p) * 16 + v, vectors fastest, so the LDS stores of
+// consecutive threads are consecutive
+template <int NT>
+__device__ __forceinline__ void mf_stage_load(MfStaged<NT>& S, const uint32_t* __restrict__ xsplit,
+                                              const float* __restrict__ xscale, int nb, int B, int c0, int nbc) {
 #pragma unroll
-        for (int m = 1; m < kMfVec; m <<= 1) {  // over the 16 lanes of block u
-            emin = min(emin, __shfl_xor(emin, m, 64));
-            emax = max(emax, __shfl_xor(emax, m, 64));
-        }
-        if (v == 0) {
-            L.lo[u] = 135 - emin;
-            L.hi[u] = min(236, 388 - emax);
+    for (int j = 0; j < kMfItems / NT; ++j) {
+        const int i = threadIdx.x + j * NT;
+        const int v = i % kMfVec, p = (i / kMfVec) % 2, q = (i / (2 * kMfVec)) % 4, u = i / (8 * kMfVec);
+        S.val[j] = u32x4{0u, 0u, 0u, 0u};
+        if (v < B && u < nbc)
+            S.val[j] = *reinterpret_cast<const u32x4*>(
+                xsplit + ((size_t)v * nb + c0 + u) * BFP8_XSPLIT_WORDS_PER_BLOCK + q * 8 + p * 4);
+    }
+#pragma unroll
+    for (int j = 0; j < MfStaged<NT>::kScaleRounds; ++j) {
+        const int i = threadIdx.x + j * NT, v = i % kMfVec, u = i / kMfVec;
+        S.xs[j] = (i < kMfScales && v < B && u < nbc) ? xscale[(size_t)v * nb + c0 + u] : 0.0f;
+    }
+}
+
+template <int NT>
+__device__ __forceinline__ void mf_stage_store(MfLds& L, const MfStaged<NT>& S) {
+#pragma unroll
+    for (int j = 0; j < kMfItems / NT; ++j) {
+        const int i = threadIdx.x + j * NT;
+        const int v = i % kMfVec, p = (i / kMfVec) % 2, q = (i / (2 * kMfVec)) % 4, u = i / (8 * kMfVec);
+        L.xa[u][q][p * 16 + v] = ((uint64_t)S.val[j].y << 32) | S.val[j].x;       // k half 0: bytes 0..7
+        L.xa[u][q][32 + p * 16 + v] = ((uint64_t)S.val[j].w << 32) | S.val[j].z;  // k half 1: bytes 8..15
+    }
+#pragma unroll
+    for (int j = 0; j < MfStaged<NT>::kScaleRounds; ++j) {
+        const int i = threadIdx.x + j * NT;
+        if (i < kMfScales) {  // whole wavefronts (kMfScales is a multiple of 64)
+            const int v = i % kMfVec, u = i / kMfVec;
+            const float xs = S.xs[j];
+            L.xs[u][v] = xs;
+            const int E = (int)((__float_as_uint(xs) >> 23) & 0xffu);
+            const bool normal = E >= 1 && E <= 254;
+            int emin = normal ? E : 255, emax = normal ? E : 0;
+#pragma unroll
+            for (int m = 1; m < kMfVec; m <<= 1) {  // over the 16 lanes of block u
+                emin = min(emin, __shfl_xor(emin, m, 64));
+                emax = max(emax, __shfl_xor(emax, m, 64));
+            }
+            if (v == 0) {
+                L.lo[u] = 135 - emin;
+                L.hi[u] = min(236, 388 - emax);
+            }
         }
     }
     __syncthreads();
@@ -105,14 +140,15 @@ struct MfState {
     float fs[kRes][8];  // [residue of the group][i]: vector 8(i/4) + 4*kh + i%4, the lane's row
 };
 
+template <int kRes>
 struct MfLoads {
-    uint64_t w[kMfGroup][2];  // [block][residue of the group] (the second unused for kRes = 1)
+    uint64_t w[kMfGroup][kRes];  // [block][residue of the group]
     uint32_t e;
 };
 
 // One block: an MFMA per residue of the group and the epilogue.
 template <int kRes>
-__device__ __forceinline__ void mf_block(MfState<kRes>& st, const MfLds& L, const uint64_t (&w)[2], uint32_t e,
+__device__ __forceinline__ void mf_block(MfState<kRes>& st, const MfLds& L, const uint64_t (&w)[kRes], uint32_t e,
                                          int u, int q0, int lane) {
     i32x16 d[kRes];
     const i32x16 zero = {};
@@ -155,7 +191,7 @@ __device__ __forceinline__ void mf_block(MfState<kRes>& st, const MfLds& L, cons
 // range check covers: groups past the tile read zeros without touching memory.
 static_assert(4 % kMfGroup == 0, "a group's exponents share one dword");
 template <int kRes>
-__device__ __forceinline__ void mf_issue(MfLoads& ld, __amdgpu_buffer_rsrc_t wrs, __amdgpu_buffer_rsrc_t ers, int wv,
+__device__ __forceinline__ void mf_issue(MfLoads<kRes>& ld, __amdgpu_buffer_rsrc_t wrs, __amdgpu_buffer_rsrc_t ers, int wv,
                                          int ev, int gi) {
 #pragma unroll
     for (int uu = 0; uu < kMfGroup; ++uu)
@@ -170,13 +206,16 @@ __device__ __forceinline__ void mf_issue(MfLoads& ld, __amdgpu_buffer_rsrc_t wrs
 }
 
 template <int kRes>
-__device__ __forceinline__ void mf_group(MfState<kRes>& st, MfLds& L, const MfLoads& ld, int gi, int nb,
+__device__ __forceinline__ void mf_group(MfState<kRes>& st, MfLds& L, const MfLoads<kRes>& ld, int gi, int nb,
                                          const uint32_t* __restrict__ xsplit, const float* __restrict__ xscale, int B,
                                          int q0, int lane) {
     const int b0 = gi * kMfGroup;
-    if (b0 % kMfChunk == 0) {
+    if (b0 % kMfChunk == 0 && b0 > 0) {  // the first chunk is staged before the loop
+        constexpr int NT = 128 * (4 / kRes);
         __syncthreads();  // every wavefront is done with the previous chunk
-        mf_stage(L, xsplit, xscale, nb, B, b0, min(kMfChunk, nb - b0));
+        MfStaged<NT> S;
+        mf_stage_load<NT>(S, xsplit, xscale, nb, B, b0, min(kMfChunk, nb - b0));
+        mf_stage_store<NT>(L, S);
     }
 #pragma unroll
     for (int uu = 0; uu < kMfGroup; ++uu) {
@@ -186,7 +225,7 @@ __device__ __forceinline__ void mf_group(MfState<kRes>& st, MfLds& L, const MfLo
 }
 
 template <int kRes>
-__global__ __launch_bounds__(64 * 2 * (4 / kRes)) void bfp8_gemv_batch_mfma_kernel(
+__global__ __launch_bounds__(64 * 2 * (4 / kRes)) __attribute__((amdgpu_waves_per_eu(4))) void bfp8_gemv_batch_mfma_kernel(
     float* __restrict__ Y, const uint32_t* __restrict__ xsplit, const float* __restrict__ xscale,
     const uint8_t* __restrict__ mant, const uint8_t* __restrict__ exps, int M, int K, int B) {
     __shared__ MfLds L;
@@ -207,14 +246,22 @@ __global__ __launch_bounds__(64 * 2 * (4 / kRes)) void bfp8_gemv_batch_mfma_kern
 #pragma unroll
         for (int i = 0; i < 8; ++i) st.fs[r][i] = 0.0f;
     const int ng = (nb + kMfGroup - 1) / kMfGroup;
-    MfLoads A, Bq;
+    // the first chunk's activation loads go out first, then the first two
+    // weight groups: the staging then waits for its own loads only (a
+    // wavefront's loads complete in the order issued)
+    constexpr int NT = 128 * (4 / kRes);
+    MfStaged<NT> S0;
+    mf_stage_load<NT>(S0, xsplit, xscale, nb, B, 0, min(kMfChunk, nb));
+    MfLoads<kRes> A, Bq;
     mf_issue<kRes>(A, wrs, ers, wv, ev, 0);
+    mf_issue<kRes>(Bq, wrs, ers, wv, ev, 1);
+    mf_stage_store<NT>(L, S0);
     for (int gi = 0; gi < ng; gi += 2) {
         // two load sets in alternating roles: the next group is always in flight
-        mf_issue<kRes>(Bq, wrs, ers, wv, ev, gi + 1);
         mf_group<kRes>(st, L, A, gi, nb, xsplit, xscale, B, q0, lane);
         mf_issue<kRes>(A, wrs, ers, wv, ev, gi + 2);
         if (gi + 1 < ng) mf_group<kRes>(st, L, Bq, gi + 1, nb, xsplit, xscale, B, q0, lane);
+        mf_issue<kRes>(Bq, wrs, ers, wv, ev, gi + 3);
     }
     float (&fs)[kRes][8] = st.fs;
 
