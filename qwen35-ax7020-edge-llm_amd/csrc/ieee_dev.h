@@ -38,6 +38,9 @@ __device__ __forceinline__ bool normal_f(float x) {
     const uint32_t e = (__float_as_uint(x) >> 23) & 0xffu;
     return e != 0u && e != 0xffu;
 }
+// The same test as 0 / 1, for conjunctions of many tests with a bitwise `&`
+// (no branch per test).
+__device__ __forceinline__ uint32_t normal_u(float x) { return normal_f(x) ? 1u : 0u; }
 __device__ __forceinline__ float ieee_mul(float a, float b) {
     const float r = __fmul_rn(a, b);
     return (normal_f(a) && normal_f(b) && normal_f(r)) ? r : narrow(widen(a) * widen(b));

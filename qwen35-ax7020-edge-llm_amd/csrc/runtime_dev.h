@@ -158,7 +158,7 @@ __device__ __forceinline__ float rms_scale(float ss, int n, float eps) {
     const float t = m + eps;
     const float q = (float)__builtin_sqrt((double)t);
     const float r = __fdiv_rn(1.0f, q);
-    if (normal_f(ss) & normal_f(fn) & normal_f(m) & normal_f(eps) & normal_f(t) & normal_f(r)) return r;
+    if (normal_u(ss) & normal_u(fn) & normal_u(m) & normal_u(eps) & normal_u(t) & normal_u(r)) return r;
     return ieee_div(1.0f, ieee_sqrt(ieee_add(ieee_div(ss, fn), eps)));
 }
 
@@ -167,7 +167,7 @@ __device__ __forceinline__ float div_sqrt_add(float num, float x, float eps) {
     const float t = x + eps;
     const float q = (float)__builtin_sqrt((double)t);
     const float r = __fdiv_rn(num, q);
-    if (normal_f(num) & normal_f(x) & normal_f(eps) & normal_f(t) & normal_f(r)) return r;
+    if (normal_u(num) & normal_u(x) & normal_u(eps) & normal_u(t) & normal_u(r)) return r;
     return ieee_div(num, ieee_sqrt(ieee_add(x, eps)));
 }
 
@@ -178,14 +178,14 @@ __device__ __forceinline__ float silu_scalar(float z) {
     const float e = (float)exp(-(double)z);
     const float d = 1.0f + e;
     const float r = __fdiv_rn(z, d);
-    if (normal_f(z) & normal_f(e) & normal_f(d) & normal_f(r)) return r;
+    if (normal_u(z) & normal_u(e) & normal_u(d) & normal_u(r)) return r;
     return ieee_div(z, ieee_add(1.0f, libm_expf(-z)));
 }
 
 // gated RMSNorm element: ((x * r) * w) * silu(z), scalar
 __device__ __forceinline__ float gated_mul(float x, float r, float w, float silu) {
     const float a = x * r, b = a * w, c = b * silu;  // one combined normality test, as in rms_scale
-    if (normal_f(x) & normal_f(r) & normal_f(a) & normal_f(w) & normal_f(b) & normal_f(silu) & normal_f(c)) return c;
+    if (normal_u(x) & normal_u(r) & normal_u(a) & normal_u(w) & normal_u(b) & normal_u(silu) & normal_u(c)) return c;
     return ieee_mul(ieee_mul(ieee_mul(x, r), w), silu);
 }
 __device__ __forceinline__ float gated_elem(float x, float r, float w, float z) {
@@ -205,8 +205,8 @@ __device__ __forceinline__ void gates_scalar(float av, float bv, float nea, floa
     const float l = (float)log1p((double)e2);
     const float m = nea * l;
     const float al = (float)exp((double)m);
-    if (normal_f(bv) & normal_f(e1) & normal_f(d1) & normal_f(b) & normal_f(av) & normal_f(dt) & normal_f(z) &
-        normal_f(e2) & normal_f(l) & normal_f(nea) & normal_f(m) & normal_f(al)) {
+    if (normal_u(bv) & normal_u(e1) & normal_u(d1) & normal_u(b) & normal_u(av) & normal_u(dt) & normal_u(z) &
+        normal_u(e2) & normal_u(l) & normal_u(nea) & normal_u(m) & normal_u(al)) {
         *beta = b;
         *alpha = al;
         return;
