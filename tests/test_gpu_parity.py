@@ -578,34 +578,40 @@ def test_rows_kernel_quantizes_special_blocks(gpu, torch_mod, M, K, inf):
     plan.close()
 
 
-@pytest.mark.parametrize("shape", ["alone", "with_small_gemv", "ragged_2049_tiles"])
+@pytest.mark.parametrize("shape", ["alone", "alone_65536", "alone_ragged_2049_tiles", "alone_k1",
+                                   "with_small_gemv", "ragged_2049_tiles"])
 def test_plan_lm_head_merge_paths(gpu, torch_mod, shape, plan_mode):
     """A plan's lm_head merge runs as the stand-alone merge kernel (lm_head
-    alone) or folded into workgroup 0 of the second launch (other GEMVs
-    present, here a 2-tile one); a 2049-tile ragged vocabulary takes several
-    passes over the list heads.  The second run uses new activations written
-    in place: the lm_head launch quantizes them all again (no stale records)."""
+    alone: 256 and 1024 tiles, a ragged 2049-tile vocabulary with several tiles
+    per workgroup, and k = 1) or folded into workgroup 0 of the second launch
+    (other GEMVs present, here a 2-tile one); a 2049-tile ragged vocabulary
+    takes several passes over the list heads.  Later runs use new activations
+    written in place: the lm_head launch quantizes them all again (no stale
+    records)."""
     qk, torch = gpu, torch_mod
-    V, H, k = {"alone": (16384, 1024, 64), "with_small_gemv": (65536, 1024, 40),
-               "ragged_2049_tiles": (131074, 1024, 40)}[shape]
+    V, H, k = {"alone": (16384, 1024, 64), "alone_65536": (65536, 1024, 40),
+               "alone_ragged_2049_tiles": (131074, 1024, 40), "alone_k1": (65536, 1024, 1),
+               "with_small_gemv": (65536, 1024, 40), "ragged_2049_tiles": (131074, 1024, 40)}[shape]
     say("plan lm_head", shape, V, H, k, plan_mode)
     lm = qk.DeviceMatrix.synth(V, H, 777, 122, 128)
     xl = qk.synth_normal(H, 778)
     items = [{"mat": lm, "x": torch.from_numpy(xl).cuda(), "topk": k}]
     small = None
-    if shape != "alone":
+    if not shape.startswith("alone"):
         small = (128, 256, 779)
         xs = qk.synth_normal(256, 780)
         items.append({"mat": qk.DeviceMatrix.synth(128, 256, 779, 124, 130), "x": torch.from_numpy(xs).cuda(),
                       "y": torch.empty(128, dtype=torch.float32, device="cuda")})
     plan = qk.SweepPlan(items)
+    if shape.startswith("alone"):
+        assert plan.kernel_name(1) == "bfp8_topk_merge_kernel"
     mant, exps = qk.synth_planes(V, H, 777, 122, 128)
-    for rep in range(2):
-        if rep == 1:  # new activations, same device buffers
-            xl = qk.synth_normal(H, 878)
+    for rep in range(3):
+        if rep > 0:  # new activations, same device buffers
+            xl = qk.synth_normal(H, 778 + 100 * rep)
             items[0]["x"].copy_(torch.from_numpy(xl))
             if small:
-                xs = qk.synth_normal(256, 880)
+                xs = qk.synth_normal(256, 780 + 100 * rep)
                 items[1]["x"].copy_(torch.from_numpy(xs))
         y_ref, *_ = ol.gemv_neon(xl, mant, exps)
         ids_ref, sc_ref = ol.topk(y_ref, k)
