@@ -205,13 +205,12 @@ __device__ __forceinline__ void mf_issue(MfLoads<kRes>& ld, __amdgpu_buffer_rsrc
     ld.e = load_e(ers, ev + (gi * kMfGroup / 4) * 256, 0);
 }
 
-template <int kRes>
+template <int kRes, int NT>
 __device__ __forceinline__ void mf_group(MfState<kRes>& st, MfLds& L, const MfLoads<kRes>& ld, int gi, int nb,
                                          const uint32_t* __restrict__ xsplit, const float* __restrict__ xscale, int B,
                                          int q0, int lane) {
     const int b0 = gi * kMfGroup;
     if (b0 % kMfChunk == 0 && b0 > 0) {  // the first chunk is staged before the loop
-        constexpr int NT = 128 * (4 / kRes);
         __syncthreads();  // every wavefront is done with the previous chunk
         MfStaged<NT> S;
         mf_stage_load<NT>(S, xsplit, xscale, nb, B, b0, min(kMfChunk, nb - b0));
@@ -224,17 +223,20 @@ __device__ __forceinline__ void mf_group(MfState<kRes>& st, MfLds& L, const MfLo
     }
 }
 
-template <int kRes>
-__global__ __launch_bounds__(64 * 2 * (4 / kRes)) __attribute__((amdgpu_waves_per_eu(4))) void bfp8_gemv_batch_mfma_kernel(
+// kHalves: halves of a tile per workgroup (2: both, workgroup per tile; 1:
+// workgroup per 32-row half, twice the workgroups for GEMVs with few tiles).
+template <int kRes, int kHalves>
+__global__ __launch_bounds__(64 * kHalves * (4 / kRes)) __attribute__((amdgpu_waves_per_eu(4))) void bfp8_gemv_batch_mfma_kernel(
     float* __restrict__ Y, const uint32_t* __restrict__ xsplit, const float* __restrict__ xscale,
     const uint8_t* __restrict__ mant, const uint8_t* __restrict__ exps, int M, int K, int B) {
     __shared__ MfLds L;
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
-    const int s = w & 1, grp = w >> 1;  // 32-row half, residue group
+    // 32-row half, residue group
+    const int s = kHalves == 2 ? (w & 1) : (int)(blockIdx.x & 1), grp = kHalves == 2 ? (w >> 1) : w;
     const int q0 = grp * kRes;
     const int col = lane & 31, kh = lane >> 5;
-    const int t = blockIdx.x;
+    const int t = kHalves == 2 ? (int)blockIdx.x : (int)(blockIdx.x >> 1);
     const int nb = K >> 6, nb4 = (nb + 3) >> 2;
     const __amdgpu_buffer_rsrc_t wrs = make_rsrc(mant + (size_t)t * nb * 4096u, (uint32_t)nb * 4096u);
     const __amdgpu_buffer_rsrc_t ers = make_rsrc(exps + (size_t)t * nb4 * 256u, (uint32_t)nb4 * 256u);
@@ -249,7 +251,7 @@ __global__ __launch_bounds__(64 * 2 * (4 / kRes)) __attribute__((amdgpu_waves_pe
     // the first chunk's activation loads go out first, then the first two
     // weight groups: the staging then waits for its own loads only (a
     // wavefront's loads complete in the order issued)
-    constexpr int NT = 128 * (4 / kRes);
+    constexpr int NT = 64 * kHalves * (4 / kRes);
     MfStaged<NT> S0;
     mf_stage_load<NT>(S0, xsplit, xscale, nb, B, 0, min(kMfChunk, nb));
     MfLoads<kRes> A, Bq;
@@ -258,9 +260,9 @@ __global__ __launch_bounds__(64 * 2 * (4 / kRes)) __attribute__((amdgpu_waves_pe
     mf_stage_store<NT>(L, S0);
     for (int gi = 0; gi < ng; gi += 2) {
         // two load sets in alternating roles: the next group is always in flight
-        mf_group<kRes>(st, L, A, gi, nb, xsplit, xscale, B, q0, lane);
+        mf_group<kRes, NT>(st, L, A, gi, nb, xsplit, xscale, B, q0, lane);
         mf_issue<kRes>(A, wrs, ers, wv, ev, gi + 2);
-        if (gi + 1 < ng) mf_group<kRes>(st, L, Bq, gi + 1, nb, xsplit, xscale, B, q0, lane);
+        if (gi + 1 < ng) mf_group<kRes, NT>(st, L, Bq, gi + 1, nb, xsplit, xscale, B, q0, lane);
         mf_issue<kRes>(Bq, wrs, ers, wv, ev, gi + 3);
     }
     float (&fs)[kRes][8] = st.fs;
@@ -301,12 +303,13 @@ hipError_t bfp8_launch_gemv_batch_mfma(float* Y, const uint32_t* xsplit, const f
     const int nt = bfp8_ntiles(M);
     if (nt == 0) return hipSuccess;
     if (B < 1 || B > kMfVec || K < 64 || (K & 63)) return hipErrorInvalidValue;
-    // few tiles: one residue per wavefront (8 per tile) so that more run
+    // few tiles: one residue per wavefront and a workgroup per 32-row half
+    // (8 wavefronts per tile over two CUs) so that more run
     if (nt < 512)
-        hipLaunchKernelGGL(bfp8_gemv_batch_mfma_kernel<1>, dim3(nt), dim3(512), 0, s, Y, xsplit, xscale, mant, exps,
-                           M, K, B);
+        hipLaunchKernelGGL((bfp8_gemv_batch_mfma_kernel<1, 1>), dim3(2 * nt), dim3(256), 0, s, Y, xsplit, xscale, mant,
+                           exps, M, K, B);
     else
-        hipLaunchKernelGGL(bfp8_gemv_batch_mfma_kernel<2>, dim3(nt), dim3(256), 0, s, Y, xsplit, xscale, mant, exps,
-                           M, K, B);
+        hipLaunchKernelGGL((bfp8_gemv_batch_mfma_kernel<2, 2>), dim3(nt), dim3(256), 0, s, Y, xsplit, xscale, mant,
+                           exps, M, K, B);
     return hipGetLastError();
 }
