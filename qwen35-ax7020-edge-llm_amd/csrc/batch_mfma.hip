@@ -29,11 +29,12 @@
 // and takes the two products otherwise; e < 8 (es = 0) and zero, infinite or
 // NaN scales give the same result either way.
 //
-// Work split: a workgroup per 64-row tile; wavefront (s, g) takes the tile's
-// 32-row half s and the residues of group g (kRes residues per wavefront: 2 or,
-// for GEMVs with few tiles, 1, so that more wavefronts run), keeping fs_q of
-// its residues; the wavefronts of a half combine their fs_q into y at the end
-// through LDS.
+// Work split: wavefront (s, g) takes a 64-row tile's 32-row half s and the
+// residues of group g (kRes residues per wavefront), keeping fs_q of its
+// residues; the wavefronts of a half combine their fs_q into y at the end
+// through LDS.  GEMVs with many tiles: a workgroup per tile, 2 residues per
+// wavefront.  GEMVs with few tiles: a workgroup per half, 1 residue per
+// wavefront, so that more wavefronts run on more CUs.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
