@@ -31,3 +31,33 @@ def test_cpu_baseline_reports_both_thread_counts():
     if out["kind"] == "reference":
         one = out["single_thread"]
         assert one["cores"] == 1 and one["value"] > 0
+
+
+def test_profiles_hold_the_traffic_the_bench_reports():
+    """Every `roofline.traffic` the bench reads has its line in the committed
+    PMC summaries, within a few percent above the launch's algorithmic bytes
+    (a missing or stale summary fails here, not silently as null)."""
+    sys.path.insert(0, str(ROOT))
+    import bench
+
+    def items(w, lm=None):
+        its = bench.workload_items(w)
+        return its if lm is None else [it for it in its if bool(it[5]) == lm]
+
+    B = 16
+
+    def batch_bytes(M, K):
+        return bench.wbytes(M, K) + B * (2 * K + 4 * (K // 64)) + B * 4 * M
+
+    cases = [
+        ("sweep", "bfp8_gemv_grouped_merge_kernel", bench.kernel_bytes(items("sweep", lm=False))),
+        ("lm_head", "bfp8_gemv_head_kernel", bench.kernel_bytes(items("lm_head", lm=True))),
+        ("gemv", "rt_rows_gemv_kernel", bench.kernel_bytes(items("gemv"))),
+        ("down", "rt_rows_gemv_kernel", bench.kernel_bytes(items("down"))),
+        ("batch16", "bfp8_gemv_batch_mfma_kernel@3584x1024", batch_bytes(3584, 1024)),
+        ("batch16", "bfp8_gemv_batch_mfma_kernel@65536x1024", batch_bytes(65536, 1024)),
+    ]
+    for workload, kernel, alg in cases:
+        t = bench.read_traffic(workload, kernel)
+        assert t is not None, (workload, kernel)
+        assert 0.99 <= t / alg <= 1.12, (workload, kernel, t, alg, t / alg)
