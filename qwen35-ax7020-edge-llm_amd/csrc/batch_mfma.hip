@@ -303,7 +303,9 @@ hipError_t bfp8_launch_gemv_batch_mfma(float* Y, const uint32_t* xsplit, const f
                                        const uint8_t* exps, int M, int K, int B, hipStream_t s) {
     const int nt = bfp8_ntiles(M);
     if (nt == 0) return hipSuccess;
-    if (B < 1 || B > kMfVec || K < 64 || (K & 63)) return hipErrorInvalidValue;
+    // a ragged K drops its last K % 64 elements, as every other GEMV path does
+    // (nb = K / 64 blocks; the split activation's stride is nb blocks)
+    if (B < 1 || B > kMfVec || K < 64) return hipErrorInvalidValue;
     // few tiles: one residue per wavefront and a workgroup per 32-row half
     // (8 wavefronts per tile over two CUs) so that more run
     if (nt < 512)

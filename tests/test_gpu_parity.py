@@ -804,6 +804,21 @@ def test_batch_scale_edges(gpu, torch_mod, B, M, K):
         assert same_f32(Y[b], y_ref), (B, M, K, b, mismatch(Y[b], y_ref))
 
 
+@pytest.mark.parametrize("B,M,K", [(8, 200, 1000), (16, 1000, 1105), (12, 3584, 4095)])
+def test_batch_ragged_k(gpu, torch_mod, B, M, K):
+    """Batches of 8-16 vectors (the matrix-core kernel) with K not a multiple
+    of 64: the trailing K % 64 elements are dropped, as in the single-vector
+    path; each vector bit-exact against the restatement."""
+    qk = gpu
+    mant, exps = qk.synth_planes(M, K, 90 + B, 124, 130)
+    X = np.stack([qk.synth_normal(K, 900 + b) for b in range(B)])
+    say("batch ragged K", B, M, K)
+    Y = qk.Bfp8Kernels().gemv_batch(X, mant, exps, M, K)
+    for b in range(B):
+        y_ref, *_ = ol.gemv_neon(X[b], mant, exps)
+        assert same_f32(Y[b], y_ref), (B, M, K, b, mismatch(Y[b], y_ref))
+
+
 def test_batch_odd_sizes(gpu, torch_mod):
     qk = gpu
     M, K, B = 129, 2048, 5
