@@ -10,7 +10,7 @@ Translation units:
   csrc/bf16_head.hip         bf16 tied-embedding lm_head, f32 flush-to-zero
   csrc/runtime_ftz.hip       decode runtime kernels (norms, conv, GDN, swiglu), f32 flush-to-zero
   csrc/fused_gemv.hip        the forward's GEMVs with their activation prologue, f32 flush-to-zero
-  csrc/sweep.hip             a whole sweep plan in one launch (LDS-quantized activations, in-launch top-k)
+  csrc/sweep.hip             a whole plan in one launch (a tile queue, LDS-quantized activations, in-launch top-k)
   csrc/batch_mfma.hip        the batched GEMV (8..16 vectors) on the matrix cores, f32 flush-to-zero
   csrc/qwen_kernels_api.cpp  C ABI host code (include/qwen_kernels.h)
   csrc/qwen_runtime_api.cpp  C ABI of the runtime kernels and the forward loop
@@ -47,7 +47,9 @@ UNITS = {
     "bf16_head.hip": ["-fgpu-flush-denormals-to-zero"],
     "runtime_ftz.hip": ["-fgpu-flush-denormals-to-zero"],
     "fused_gemv.hip": ["-fgpu-flush-denormals-to-zero"],
-    "sweep.hip": ["-fgpu-flush-denormals-to-zero"],
+    # (the ticket atomic stays one plain atomic: no wave-level combining,
+    # whose result arithmetic would wait for every load in flight)
+    "sweep.hip": ["-fgpu-flush-denormals-to-zero", "-mllvm", "-amdgpu-atomic-optimizer-strategy=None"],
     # MFMA results straight into VGPRs (no accumulator-register copies)
     "batch_mfma.hip": ["-fgpu-flush-denormals-to-zero", "-mllvm", "-amdgpu-mfma-vgpr-form=1"],
     "bfp8_ieee.hip": [],

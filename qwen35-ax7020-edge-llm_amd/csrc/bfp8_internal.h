@@ -147,43 +147,52 @@ int bfp8_stream_grid();
 hipError_t bfp8_probe_code_object();
 
 // ---- sweep.hip: a whole plan in one persistent launch -----------------------
-// Workgroup w takes its lm_head tiles (w, w + grid, ... of descs[head], whose
-// planes and width are arguments) then tiles[wg_off[w] .. wg_off[w+1]).  Its
-// activation slots are acts[act_off[w] .. act_off[w+1]) (slot 0: the
-// lm_head's when it has lm_head tiles), each quantized into LDS at word
-// offset xoff (a multiple of 4; nb*32 split words then nb scale words).
-struct Bfp8SweepTile {
-    int desc, tile;
-    int xoff;  // LDS word offset of the tile's activation slot
-    int slot;  // index of that slot in the workgroup's list
-};
-struct Bfp8SweepAct {
-    const float* x;
-    int K;
-    int xoff;
+// One GEMV of the launch's queue: its row tiles are queue units first ..
+// first + ntiles - 1 (the table is ordered by first unit).  48 bytes.
+struct Bfp8SweepGemv {
+    const uint8_t* mant;  // GPU planes
+    const uint8_t* exps;
+    const float* x;       // activation, nb * 64 floats
+    float* y;             // outputs, rows < pair_rows written
+    int nb, pair_rows;
+    int first, ntiles;
 };
 struct Bfp8SweepArgs {
-    const Bfp8GemvDesc* descs;
-    const Bfp8SweepTile* tiles;
-    const int* wg_off;
-    const Bfp8SweepAct* acts;
-    const int* act_off;
-    const uint8_t* head_mant;  // descs[head]'s planes and width (head >= 0)
+    const Bfp8SweepGemv* gemvs;
+    int ngemv, nunits;
+    int ticket0;           // the queue unit the first ticket of sub-queue 0 stands for
+    int nqueues;           // sub-queues (1, or up to BFP8_SWEEP_QUEUES with 8 nqueues <= the grid): sub-queue
+                           // s holds units ticket0 + s + nqueues t, taken by workgroups (w / 8) mod nqueues = s
+    uint32_t* counters;    // BFP8_SWEEP_QUEUES tickets-taken counters, then the finished-workgroup count
+                           // (BFP8_SWEEP_CTR_STRIDE words apart; zero between launches)
+    // the lm_head (head_ntiles > 0): workgroup w < grid - 1 takes its tiles w, w + grid - 1, ...
+    // first; the last workgroup merges their top-k lists
+    const uint8_t* head_mant;
     const uint8_t* head_exps;
-    int head_K, head_ntiles;
-    int head;                  // -1: no lm_head
-    int merger;                // the workgroup that merges the lm_head's top-k
-    uint32_t epoch;            // 1 .. 2^14 - 1, different from the previous launch's
+    const float* head_x;
+    int head_nb, head_ntiles, head_pair_rows, topk;
+    uint64_t* partials;    // [head_ntiles][topk] epoch keys
+    int* out_ids;
+    float* out_scores;
+    int* out_count;
+    int* out_argmax;
+    uint32_t epoch;        // 1 .. 2^14 - 1, different from the previous launch's
 };
-#define BFP8_SWEEP_LDS_WORDS 8192  // activation slots per workgroup (32 KiB)
-#define BFP8_SWEEP_MAX_SLOTS 8     // activations per workgroup
-// Extra load, in blocks, that the in-launch top-k merge puts on the merging
-// workgroup of a single launch.
-#define BFP8_SWEEP_MERGE_COST_BLOCKS 64
-// Words of one activation slot of K elements (split words + scales, padded).
-static inline int bfp8_sweep_slot_words(int K) { return ((K >> 6) * 33 + 3) & ~3; }
-int bfp8_sweep_grid();
-hipError_t bfp8_launch_sweep(const Bfp8SweepArgs& a, int nwg, int lds_words, hipStream_t s);
+#define BFP8_SWEEP_MAX_GEMV 128
+// Workgroups per CU of the single launch (5 wavefronts each) with queue
+// units; a lone lm_head takes one tile per workgroup (up to what is resident).
+#define BFP8_SWEEP_WG_PER_CU 3
+#define BFP8_SWEEP_QUEUES 64
+#define BFP8_SWEEP_CTR_STRIDE 1024  // words (4 KiB apart: counters in different memory channels)
+#define BFP8_SWEEP_CTR_BYTES ((BFP8_SWEEP_QUEUES + 1) * BFP8_SWEEP_CTR_STRIDE * 4)
+// Units of a sweep launch have an even number of 4-block chunks (nb % 8 == 0,
+// 8 <= nb <= 64): their chunks alternate between two register buffers.
+#define BFP8_SWEEP_MIN_NB 8
+// Resident workgroups of the single launch with at most per_cu per CU (every
+// workgroup of a launch must be resident: the merging one waits for the
+// others' lists).
+int bfp8_sweep_grid(int per_cu);
+hipError_t bfp8_launch_sweep(const Bfp8SweepArgs& a, int nwg, hipStream_t s);
 // Y[v][M] for v < B (1..16): B split activations (rows of nb*32 words) and
 // scales (rows of nb floats); pair rows only (the odd last row is the tail
 // kernel's).  8..16 vectors run on the matrix cores (batch_mfma.hip), fewer

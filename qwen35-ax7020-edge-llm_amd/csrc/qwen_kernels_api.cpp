@@ -1096,140 +1096,78 @@ struct Plan {
     bfp8_plan_item gen_out{};      // its outputs and k
     DevBuf logits, gen_partials, gen_keys;
     std::vector<Bfp8GemvDesc> hdesc;
-    // single launch (sweep.hip): the whole plan, activations quantized in LDS
+    // single launch (sweep.hip): the whole plan, a tile queue, activations quantized in LDS
     bool sweep = false;
-    DevBuf s_tiles, s_wgoff, s_acts, s_actoff;
-    int s_nwg = 0, s_lds = 0, s_merger = -1;
+    DevBuf s_gemvs, s_counters;
+    int s_nwg = 0, s_ngemv = 0, s_nunits = 0;
     uint32_t epoch = 0;            // of the last launch; the partials start zeroed (epoch 0)
 };
 
-// The single launch is opt-in (BFP8_PLAN_SINGLE_LAUNCH=1 when the plan is
-// created).
-bool single_launch_enabled() {
-    const char* e = getenv("BFP8_PLAN_SINGLE_LAUNCH");
-    return e && e[0] == '1';
+// Sub-queues of a single launch on nwg workgroups: each is shared by the
+// workgroups (w / 8) mod n = s, so that n divides nwg / 8 evenly (every
+// sub-queue the same number of workgroups, from every XCD) -- at most
+// BFP8_SWEEP_QUEUES, at least two groups of 8 per sub-queue.
+int sweep_queues(int nwg) {
+    const int groups = nwg / 8;
+    int best = 1;
+    for (int n = 1; n <= BFP8_SWEEP_QUEUES && 2 * n <= groups; ++n)
+        if (groups % n == 0) best = n;
+    return best;
 }
 
-// The single launch's work lists: workgroup w's lm_head tiles are w, w + nwg,
-// ... (the kernel computes them); the other GEMVs' tiles go GEMV by GEMV
-// (larger K first) onto the workgroups in order, first fit under an even
-// share of the blocks plus a little slack, so that a workgroup reads few
-// activations; each new activation of a workgroup takes an LDS slot within
-// BFP8_SWEEP_LDS_WORDS.  The merging workgroup is pre-charged with the
-// merge's cost.  Returns false when the slots do not fit (the plan then takes
-// the two-launch path).
-bool deal_sweep(Plan* p, const bfp8_plan_item* items, int n) {
+// A unit of the single launch has an even number of 4-block chunks.
+bool sweep_nb_ok(int K) {
+    const int nb = bfp8_nblocks(K);
+    return (K & 63) == 0 && nb >= BFP8_SWEEP_MIN_NB && nb <= 64 && nb % 8 == 0;
+}
+
+// The single launch (sweep.hip) for a plan whose every GEMV fits it: even M,
+// whole units (sweep_nb_ok), 1 .. BFP8_SWEEP_MAX_GEMV GEMVs besides a fused
+// lm_head.  Builds the queue table -- the GEMVs with the most blocks
+// first, each GEMV's tiles consecutive -- and the zeroed ticket counters.
+// Returns false (the plan keeps its launches) when the plan does not fit.
+bool build_sweep(Plan* p, const bfp8_plan_item* items, int n) {
     const int head = p->topk_desc;
-    const int hnt = head >= 0 ? bfp8_ntiles(items[head].M) : 0;
-    const int hnb = head >= 0 ? bfp8_nblocks(items[head].K) : 0;
+    if (!p->odd_items.empty() || !p->float_items.empty() || p->gen_head >= 0) return false;
     std::vector<int> rest;
-    long long total = (long long)hnt * hnb;
-    int ntiles = hnt;
+    int total_tiles = 0;
     for (int i = 0; i < n; ++i) {
-        if (i == head) continue;
-        rest.push_back(i);
-        total += (long long)bfp8_ntiles(items[i].M) * bfp8_nblocks(items[i].K);
-        ntiles += bfp8_ntiles(items[i].M);
+        if (!sweep_nb_ok(items[i].K) || (items[i].M & 1)) return false;
+        total_tiles += bfp8_ntiles(items[i].M);
+        if (i != head) rest.push_back(i);
     }
+    // a lone lm_head takes the two launches (per-tile lists, then the merge
+    // kernel): its scoring ends long before one workgroup's merge of every
+    // list could
+    if (rest.empty() || (int)rest.size() > BFP8_SWEEP_MAX_GEMV) return false;
+    if (head < 0 && total_tiles <= BFP8_WIDE_MAX_TILES) return false;  // (small plans: one tile per workgroup)
     std::stable_sort(rest.begin(), rest.end(), [&](int a, int b) { return items[a].K > items[b].K; });
-    const int nwg = std::min(bfp8_sweep_grid(), ntiles);
-    if (nwg <= 0) return false;
-    const int merger = head >= 0 ? 0 : -1;
-    std::vector<long long> load(nwg, 0);
-    std::vector<int> lds(nwg, 0);
-    std::vector<std::vector<Bfp8SweepAct>> slots(nwg);
-    std::vector<std::vector<int>> slot_item(nwg);
-    std::vector<std::vector<Bfp8SweepTile>> tl(nwg);
-    for (int w = 0; w < nwg; ++w) {
-        const int nh = w < hnt ? (hnt - w + nwg - 1) / nwg : 0;
-        load[w] = (long long)nh * hnb + (w == merger ? BFP8_SWEEP_MERGE_COST_BLOCKS : 0);
-        if (nh > 0) {
-            slots[w].push_back(Bfp8SweepAct{items[head].x, items[head].K, 0});
-            slot_item[w].push_back(head);
-            lds[w] = bfp8_sweep_slot_words(items[head].K);
-        }
+    std::vector<Bfp8SweepGemv> tab;
+    int first = 0;
+    for (int i : rest) {
+        const bfp8_plan_item& it = items[i];
+        Bfp8SweepGemv g{};
+        g.mant = (const uint8_t*)it.mant_gpu;
+        g.exps = it.exps_gpu;
+        g.x = it.x;
+        g.y = it.y;
+        g.nb = bfp8_nblocks(it.K);
+        g.pair_rows = it.M & ~1;
+        g.first = first;
+        g.ntiles = bfp8_ntiles(it.M);
+        first += g.ntiles;
+        tab.push_back(g);
     }
-    const long long cap = (total + (merger >= 0 ? BFP8_SWEEP_MERGE_COST_BLOCKS : 0) + nwg - 1) / nwg + 4;
-    int cur = 0;
-    for (int g : rest) {
-        const int nb = bfp8_nblocks(items[g].K), sw = bfp8_sweep_slot_words(items[g].K);
-        for (int t = 0; t < bfp8_ntiles(items[g].M); ++t) {
-            auto slot_of = [&](int w) {
-                for (size_t k = 0; k < slot_item[w].size(); ++k)
-                    if (slot_item[w][k] == g) return (int)k;
-                return -1;
-            };
-            int pick = -1;
-            for (int k = 0; k < nwg && pick < 0; ++k) {
-                const int w = (cur + k) % nwg;
-                if (load[w] + nb <= cap && (slot_of(w) >= 0 || lds[w] + sw <= BFP8_SWEEP_LDS_WORDS)) pick = w;
-            }
-            if (pick < 0) {  // every workgroup is at the cap: the least loaded one with room
-                for (int w = 0; w < nwg; ++w)
-                    if ((slot_of(w) >= 0 || lds[w] + sw <= BFP8_SWEEP_LDS_WORDS) && (pick < 0 || load[w] < load[pick]))
-                        pick = w;
-                if (pick < 0) return false;
-            }
-            cur = pick;
-            int sl = slot_of(pick);
-            if (sl < 0) {
-                slots[pick].push_back(Bfp8SweepAct{items[g].x, items[g].K, lds[pick]});
-                slot_item[pick].push_back(g);
-                sl = (int)slots[pick].size() - 1;
-                lds[pick] += sw;
-            }
-            tl[pick].push_back(Bfp8SweepTile{g, t, slots[pick][sl].xoff, sl});
-            load[pick] += nb;
-        }
-    }
-    // invariants the kernel's indexing relies on: every tile dealt once, each
-    // tile's slot is its GEMV's and inside the LDS budget, slot 0 of a
-    // workgroup with lm_head tiles is the lm_head's activation at offset 0
-    {
-        std::vector<std::vector<char>> seen(n);
-        for (int i = 0; i < n; ++i) seen[i].assign(bfp8_ntiles(items[i].M), 0);
-        for (int w = 0; w < nwg; ++w) {
-            if (lds[w] > BFP8_SWEEP_LDS_WORDS || slots[w].size() > BFP8_SWEEP_MAX_SLOTS) return false;
-            if (w < hnt && (slots[w].empty() || slot_item[w][0] != head || slots[w][0].xoff != 0)) return false;
-            for (size_t k = 0; k < slots[w].size(); ++k)
-                if ((slots[w][k].xoff & 3) || slots[w][k].xoff + bfp8_sweep_slot_words(slots[w][k].K) > lds[w])
-                    return false;
-            for (const Bfp8SweepTile& st : tl[w]) {
-                if (st.desc < 0 || st.desc >= n || st.desc == head || st.slot < 0 || st.slot >= (int)slots[w].size() ||
-                    slot_item[w][st.slot] != st.desc || slots[w][st.slot].xoff != st.xoff || st.tile < 0 ||
-                    st.tile >= bfp8_ntiles(items[st.desc].M) || seen[st.desc][st.tile])
-                    return false;
-                seen[st.desc][st.tile] = 1;
-            }
-        }
-        for (int g : rest)
-            for (char c : seen[g])
-                if (!c) return false;
-    }
-    std::vector<Bfp8SweepTile> tiles;
-    std::vector<Bfp8SweepAct> acts;
-    std::vector<int> wg_off(1, 0), act_off(1, 0);
-    int lds_max = 0;
-    for (int w = 0; w < nwg; ++w) {
-        tiles.insert(tiles.end(), tl[w].begin(), tl[w].end());
-        acts.insert(acts.end(), slots[w].begin(), slots[w].end());
-        wg_off.push_back((int)tiles.size());
-        act_off.push_back((int)acts.size());
-        lds_max = std::max(lds_max, lds[w]);
-    }
-    if (tiles.empty()) tiles.push_back(Bfp8SweepTile{0, 0, 0, 0});  // never read
-    if (acts.empty()) acts.push_back(Bfp8SweepAct{nullptr, 0, 0});
-    if (p->s_tiles.reserve(tiles.size() * sizeof(Bfp8SweepTile)) || p->s_wgoff.reserve(wg_off.size() * 4) ||
-        p->s_acts.reserve(acts.size() * sizeof(Bfp8SweepAct)) || p->s_actoff.reserve(act_off.size() * 4))
+    const int grid = bfp8_sweep_grid(BFP8_SWEEP_WG_PER_CU);
+    p->s_nwg = head >= 0 ? grid : std::min(grid, first);
+    p->s_ngemv = (int)tab.size();
+    p->s_nunits = first;
+
+    if (p->s_gemvs.reserve(tab.size() * sizeof(Bfp8SweepGemv)) || p->s_counters.reserve(BFP8_SWEEP_CTR_BYTES))
         return false;
-    if (hipMemcpy(p->s_tiles.p, tiles.data(), tiles.size() * sizeof(Bfp8SweepTile), hipMemcpyHostToDevice) != hipSuccess ||
-        hipMemcpy(p->s_wgoff.p, wg_off.data(), wg_off.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
-        hipMemcpy(p->s_acts.p, acts.data(), acts.size() * sizeof(Bfp8SweepAct), hipMemcpyHostToDevice) != hipSuccess ||
-        hipMemcpy(p->s_actoff.p, act_off.data(), act_off.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
+    if (hipMemcpy(p->s_gemvs.p, tab.data(), tab.size() * sizeof(Bfp8SweepGemv), hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemset(p->s_counters.p, 0, BFP8_SWEEP_CTR_BYTES) != hipSuccess)
         return false;
-    p->s_nwg = nwg;
-    p->s_lds = lds_max;
-    p->s_merger = merger;
     return true;
 }
 
@@ -1283,7 +1221,7 @@ void release_plan(Plan* p) {
     p->descs.release(); p->qdescs.release(); p->xscale.release(); p->xsplit.release();
     p->partials.release(); p->qtasks.release();
     p->logits.release(); p->gen_partials.release(); p->gen_keys.release();
-    p->s_tiles.release(); p->s_wgoff.release(); p->s_acts.release(); p->s_actoff.release();
+    p->s_gemvs.release(); p->s_counters.release();
     p->head.tiles.release(); p->head.wg_off.release(); p->rest.tiles.release(); p->rest.wg_off.release();
 }
 
@@ -1440,22 +1378,12 @@ void* bfp8_plan_create(const bfp8_plan_item* items, int n) {
             p->fused_head = !rc;
         }
     }
-    // one launch for the whole plan when every item is a quantized GEMV of
-    // even M (or the fused lm_head) and the plan is larger than the small-plan
-    // kernels' range
-    {
-        int total_tiles = 0;
-        for (int i = 0; i < n; ++i) total_tiles += bfp8_ntiles(items[i].M);
-        // (an lm_head alone keeps its two launches: the stand-alone 16-wavefront
-        // merge is quicker than the one a single launch runs in one workgroup)
-        const bool head_only = p->topk_desc >= 0 && n == 1;
-        if (!rc && single_launch_enabled() && !head_only && p->odd_items.empty() && p->float_items.empty() &&
-            p->gen_head < 0 && (p->topk_desc >= 0 || total_tiles > BFP8_WIDE_MAX_TILES)) {
-            p->sweep = deal_sweep(p, items, n);
-            if (p->sweep && p->topk_desc >= 0 &&
-                hipMemset(p->partials.p, 0, p->partials.n) != hipSuccess)  // epoch 0: never a run's
-                rc = BFP8_EHIP;
-        }
+    // one launch for the whole plan when every GEMV fits it (build_sweep)
+    if (!rc) {
+        p->sweep = build_sweep(p, items, n);
+        if (p->sweep && p->topk_desc >= 0 &&
+            hipMemset(p->partials.p, 0, p->partials.n) != hipSuccess)  // epoch 0: never a run's
+            rc = BFP8_EHIP;
     }
     rc = rc ? rc : p->descs.reserve(p->hdesc.size() * sizeof(Bfp8GemvDesc));
     rc = rc ? rc : p->qdescs.reserve(hq.size() * sizeof(Bfp8QuantDesc));
@@ -1487,23 +1415,33 @@ int bfp8_plan_launch(void* plan, int stage, void* stream) {
     if (p->sweep) {  // everything in stage 0
         if (stage != 0) return BFP8_OK;
         Bfp8SweepArgs a{};
-        a.descs = descs;
-        a.tiles = p->s_tiles.as<Bfp8SweepTile>();
-        a.wg_off = p->s_wgoff.as<int>();
-        a.acts = p->s_acts.as<Bfp8SweepAct>();
-        a.act_off = p->s_actoff.as<int>();
-        a.head = p->topk_desc;
-        if (a.head >= 0) {
-            const Bfp8GemvDesc& hd = p->hdesc[a.head];
+        a.gemvs = p->s_gemvs.as<Bfp8SweepGemv>();
+        a.ngemv = p->s_ngemv;
+        a.nunits = p->s_nunits;
+        a.counters = p->s_counters.as<uint32_t>();
+        a.nqueues = sweep_queues(p->s_nwg);
+        if (p->topk_desc >= 0) {
+            const Bfp8GemvDesc& hd = p->hdesc[p->topk_desc];
+            const bfp8_plan_item& it = p->items[p->topk_desc];
             a.head_mant = hd.mant;
             a.head_exps = hd.exps;
-            a.head_K = hd.K;
+            a.head_x = it.x;
+            a.head_nb = bfp8_nblocks(hd.K);
             a.head_ntiles = bfp8_ntiles(hd.M);
+            a.head_pair_rows = hd.pair_rows;
+            a.topk = hd.topk;
+            a.partials = hd.partials;
+            a.out_ids = hd.out_ids;
+            a.out_scores = hd.out_scores;
+            a.out_count = hd.out_count;
+            a.out_argmax = hd.out_argmax;
+            a.ticket0 = 0;
+        } else {
+            a.ticket0 = p->s_nwg;  // queue units 0 .. nwg - 1 are the workgroups' first
         }
-        a.merger = p->s_merger;
         p->epoch = p->epoch % 16383u + 1u;
         a.epoch = p->epoch;
-        HIP_OK(bfp8_launch_sweep(a, p->s_nwg, p->s_lds, s));
+        HIP_OK(bfp8_launch_sweep(a, p->s_nwg, s));
         return BFP8_OK;
     }
     if (stage == 0) {

@@ -40,6 +40,7 @@ struct PlainKeys {
     __device__ uint64_t peek(const uint64_t* p) const { return __builtin_nontemporal_load(p); }
     __device__ uint64_t settle(uint64_t k, const uint64_t*, bool&) const { return k; }
     // every key current (nothing to wait for)
+    template <int NT>
     __device__ void verify_all(const uint64_t*, int, bool&) const {}
     __device__ PlainKeys verified() const { return *this; }
 };
@@ -73,10 +74,11 @@ struct EpochKeys {
         __hip_atomic_store(p, k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     // Waits (bounded) until each of the n keys carries the run's epoch; the
-    // workgroup's threads share the keys.  After it (and a barrier) every
-    // key can be read as verified(): no waiting per read.
+    // merge's NT threads (threadIdx.x < NT) share the keys.  After it (and a
+    // barrier) every key can be read as verified(): no waiting per read.
+    template <int NT>
     __device__ void verify_all(const uint64_t* p, int n, bool& stale) const {
-        const int nt = blockDim.x;
+        constexpr int nt = NT;
         for (int i0 = threadIdx.x; i0 < n; i0 += 8 * nt) {  // eight reads in flight
             uint64_t k[8];
 #pragma unroll
@@ -455,7 +457,7 @@ __device__ __forceinline__ void topk_merge(const TopkArgs& d, const KF& kf, Merg
     if (topk_select<W, PASSES, KEEP>(d, kf, L, stale)) return;
     // more candidates than the selection ranks: the bitonic tree, over keys
     // first waited for all at once (its reads then wait for nothing)
-    kf.verify_all(parts, ntiles * kk, stale);
+    kf.template verify_all<W * 64>(parts, ntiles * kk, stale);
     __syncthreads();
     topk_tree<W, H>(d, kf.verified(), L, stale);
 }

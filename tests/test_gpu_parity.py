@@ -412,14 +412,16 @@ def test_random_lm_heads_against_the_oracle(gpu, torch_mod):
         assert kk.lm_head_argmax(x, mant, exps, V, H) == ol.argmax(y_ref), (V, H, seed)
 
 
+@pytest.mark.parametrize("other", ["small", "queue"])
 @pytest.mark.parametrize("k", [2, 5, 40, 64])
-def test_lm_head_one_tile_holds_the_best(gpu, torch_mod, k, plan_mode):
+def test_lm_head_one_tile_holds_the_best(gpu, torch_mod, k, other):
     """One 64-row tile's exponents sit 8 above the others', so most of the best
     rows share its partial list: the merge's threshold selection keeps reading
     that list past the entries it loads up front.  Stand-alone merge (16
-    wavefronts), folded into a plan's second launch (4 wavefronts) or in the
-    single launch (epoch-tagged keys); ids, scores, count and argmax against
-    the restatement."""
+    wavefronts), then in a plan with another GEMV: folded into the second
+    launch (4 wavefronts; a 128 x 256 GEMV, too narrow for the single launch)
+    or in the single launch (epoch-tagged keys; a 256 x 1024 GEMV); ids,
+    scores, count and argmax against the restatement."""
     qk, torch = gpu, torch_mod
     V, H = 65536, 1024
     mant, exps = qk.synth_planes(V, H, 910, 122, 128)
@@ -429,7 +431,7 @@ def test_lm_head_one_tile_holds_the_best(gpu, torch_mod, k, plan_mode):
     y_ref, *_ = ol.gemv_neon(x, mant, exps)
     ids_ref, sc_ref = ol.topk(y_ref, k)
     assert np.sum((ids_ref >= 64 * 517) & (ids_ref < 64 * 518)) >= min(k, 20)
-    say("lm_head one tile holds the best", k, plan_mode)
+    say("lm_head one tile holds the best", k, other)
     dm = qk.DeviceMatrix.from_soa(mant, exps)
     xt = torch.from_numpy(x).cuda()
     _, xs, xsp = qk.quantize(xt)
@@ -437,12 +439,14 @@ def test_lm_head_one_tile_holds_the_best(gpu, torch_mod, k, plan_mode):
     torch.cuda.synchronize()
     assert int(cnt.item()) == k and int(am.item()) == ol.argmax(y_ref)
     assert np.array_equal(ids.cpu().numpy(), ids_ref) and same_f32(sc.cpu().numpy(), sc_ref)
-    sm, se = qk.synth_planes(128, 256, 912, 124, 130)
-    xo = qk.synth_normal(256, 913)
+    OM, OK = (128, 256) if other == "small" else (256, 1024)
+    sm, se = qk.synth_planes(OM, OK, 912, 124, 130)
+    xo = qk.synth_normal(OK, 913)
     items = [{"mat": dm, "x": xt, "topk": k},
              {"mat": qk.DeviceMatrix.from_soa(sm, se), "x": torch.from_numpy(xo).cuda(),
-              "y": torch.empty(128, dtype=torch.float32, device="cuda")}]
+              "y": torch.empty(OM, dtype=torch.float32, device="cuda")}]
     plan = qk.SweepPlan(items)
+    assert plan.kernel_name(0) == ("bfp8_gemv_head_kernel" if other == "small" else "bfp8_sweep_kernel")
     for rep in range(2):
         plan.run()
         torch.cuda.synchronize()
@@ -579,39 +583,50 @@ def test_rows_kernel_quantizes_special_blocks(gpu, torch_mod, M, K, inf):
 
 
 @pytest.mark.parametrize("shape", ["alone", "alone_65536", "alone_ragged_2049_tiles", "alone_k1",
-                                   "with_small_gemv", "ragged_2049_tiles"])
-def test_plan_lm_head_merge_paths(gpu, torch_mod, shape, plan_mode):
-    """A plan's lm_head merge runs as the stand-alone merge kernel (lm_head
-    alone: 256 and 1024 tiles, a ragged 2049-tile vocabulary with several tiles
-    per workgroup, and k = 1) or folded into workgroup 0 of the second launch
-    (other GEMVs present, here a 2-tile one); a 2049-tile ragged vocabulary
-    takes several passes over the list heads.  Later runs use new activations
-    written in place: the lm_head launch quantizes them all again (no stale
-    records)."""
+                                   "with_small_gemv", "ragged_2049_tiles", "queue_gemv", "queue_ragged_2049_tiles",
+                                   "queue_k1", "queue_small_vocab"])
+def test_plan_lm_head_merge_paths(gpu, torch_mod, shape):
+    """A plan's lm_head merge runs in the merging workgroup of the single
+    launch (with a 2048 x 1024 GEMV: the 2049-tile vocabulary gives some
+    workgroups three lm_head tiles, a 64-tile one leaves most workgroups to
+    start from the queue, and k = 1), as the stand-alone merge kernel after
+    the per-tile lists (a lone lm_head: 256, 1024 and a ragged 2049 tiles, and
+    k = 1), or folded into workgroup 0 of the second launch (another GEMV too
+    narrow for the single launch, here 128 x 256); a 2049-tile ragged
+    vocabulary takes several passes over the list heads.  Later runs use new
+    activations written in place: every activation is quantized again (no
+    stale records)."""
     qk, torch = gpu, torch_mod
     V, H, k = {"alone": (16384, 1024, 64), "alone_65536": (65536, 1024, 40),
                "alone_ragged_2049_tiles": (131074, 1024, 40), "alone_k1": (65536, 1024, 1),
-               "with_small_gemv": (65536, 1024, 40), "ragged_2049_tiles": (131074, 1024, 40)}[shape]
-    say("plan lm_head", shape, V, H, k, plan_mode)
+               "with_small_gemv": (65536, 1024, 40), "ragged_2049_tiles": (131074, 1024, 40),
+               "queue_gemv": (65536, 1024, 40), "queue_ragged_2049_tiles": (131074, 1024, 40),
+               "queue_k1": (65536, 1024, 1), "queue_small_vocab": (4096, 512, 64)}[shape]
+    say("plan lm_head", shape, V, H, k)
     lm = qk.DeviceMatrix.synth(V, H, 777, 122, 128)
     xl = qk.synth_normal(H, 778)
     items = [{"mat": lm, "x": torch.from_numpy(xl).cuda(), "topk": k}]
     small = None
     if not shape.startswith("alone"):
-        small = (128, 256, 779)
-        xs = qk.synth_normal(256, 780)
-        items.append({"mat": qk.DeviceMatrix.synth(128, 256, 779, 124, 130), "x": torch.from_numpy(xs).cuda(),
-                      "y": torch.empty(128, dtype=torch.float32, device="cuda")})
+        small = (128, 256, 779) if not shape.startswith("queue") else (2048, 1024, 779)
+        SM, SK, sseed = small
+        xs = qk.synth_normal(SK, 780)
+        items.append({"mat": qk.DeviceMatrix.synth(SM, SK, sseed, 124, 130), "x": torch.from_numpy(xs).cuda(),
+                      "y": torch.empty(SM, dtype=torch.float32, device="cuda")})
     plan = qk.SweepPlan(items)
-    if shape.startswith("alone"):
-        assert plan.kernel_name(1) == "bfp8_topk_merge_kernel"
+    if shape.startswith("alone"):  # per-tile lists, then the merge kernel
+        assert plan.kernel_name(0) == "bfp8_gemv_head_kernel" and plan.kernel_name(1) == "bfp8_topk_merge_kernel"
+    elif shape.startswith("queue"):
+        assert plan.kernel_name(0) == "bfp8_sweep_kernel"
+    else:
+        assert plan.kernel_name(0) == "bfp8_gemv_head_kernel"
     mant, exps = qk.synth_planes(V, H, 777, 122, 128)
     for rep in range(3):
         if rep > 0:  # new activations, same device buffers
             xl = qk.synth_normal(H, 778 + 100 * rep)
             items[0]["x"].copy_(torch.from_numpy(xl))
             if small:
-                xs = qk.synth_normal(256, 780 + 100 * rep)
+                xs = qk.synth_normal(small[1], 780 + 100 * rep)
                 items[1]["x"].copy_(torch.from_numpy(xs))
         y_ref, *_ = ol.gemv_neon(xl, mant, exps)
         ids_ref, sc_ref = ol.topk(y_ref, k)
@@ -621,28 +636,33 @@ def test_plan_lm_head_merge_paths(gpu, torch_mod, shape, plan_mode):
         assert int(cnt[0].item()) == k and int(cnt[1].item()) == ol.argmax(y_ref), rep
         assert np.array_equal(ids.cpu().numpy(), ids_ref) and same_f32(sc.cpu().numpy(), sc_ref), rep
         if small:
-            sm, se = qk.synth_planes(128, 256, 779, 124, 130)
+            sm, se = qk.synth_planes(*small, 124, 130)
             assert same_f32(items[1]["y"].cpu().numpy(), ol.gemv_neon(xs, sm, se)[0]), rep
     plan.close()
 
 
-@pytest.mark.parametrize("with_other", [False, True])
-def test_plan_lm_head_quantizes_special_blocks(gpu, torch_mod, with_other, plan_mode):
-    """The lm_head launch quantizes its activation itself (16 lanes per block,
-    four elements per lane) and, with another GEMV in the plan, that GEMV's
-    activation as one-block tasks: special blocks in both (zeros, -0, the
-    1e-20 threshold, NaN, .5 ties, subnormals, 1e33), top-k, argmax and y
+@pytest.mark.parametrize("other_k", [0, 2048, 1984])
+def test_plan_lm_head_quantizes_special_blocks(gpu, torch_mod, other_k):
+    """The launch that streams the lm_head quantizes its activation itself (16
+    lanes per block, four elements per lane) and, with another GEMV in the
+    plan, that GEMV's activation: in LDS in the single launch (K = 2048), as
+    one-block tasks of the two-launch path (K = 1984, whose 31 blocks the
+    single launch does not take).  Special blocks in both (zeros, -0, the
+    1e-20 threshold, NaN, .5 ties, subnormals, 1e33): top-k, argmax and y
     against the oracle."""
     qk, torch = gpu, torch_mod
     V, H, k = 16384, 1024, 40
-    say("plan lm_head special blocks", with_other, plan_mode)
+    with_other = other_k > 0
+    say("plan lm_head special blocks", other_k)
     xl = _special_blocks(H, 6301)
     items = [{"mat": qk.DeviceMatrix.synth(V, H, 6300, 118, 136), "x": torch.from_numpy(xl).cuda(), "topk": k}]
     if with_other:
-        xo = _special_blocks(2048, 6303)
-        items.append({"mat": qk.DeviceMatrix.synth(1000, 2048, 6302, 118, 136), "x": torch.from_numpy(xo).cuda(),
+        xo = _special_blocks(other_k, 6303)
+        items.append({"mat": qk.DeviceMatrix.synth(1000, other_k, 6302, 118, 136), "x": torch.from_numpy(xo).cuda(),
                       "y": torch.empty(1000, dtype=torch.float32, device="cuda")})
     plan = qk.SweepPlan(items)
+    if with_other:
+        assert plan.kernel_name(0) == ("bfp8_sweep_kernel" if other_k == 2048 else "bfp8_gemv_head_kernel")
     mant, exps = qk.synth_planes(V, H, 6300, 118, 136)
     y_ref, *_ = ol.gemv_neon(xl, mant, exps)
     ids_ref, sc_ref = ol.topk(y_ref, k)
@@ -653,7 +673,7 @@ def test_plan_lm_head_quantizes_special_blocks(gpu, torch_mod, with_other, plan_
         assert int(cnt[0].item()) == k and int(cnt[1].item()) == ol.argmax(y_ref), rep
         assert np.array_equal(ids.cpu().numpy(), ids_ref) and same_f32(sc.cpu().numpy(), sc_ref), rep
         if with_other:
-            om, oe = qk.synth_planes(1000, 2048, 6302, 118, 136)
+            om, oe = qk.synth_planes(1000, other_k, 6302, 118, 136)
             y_o = items[1]["y"].cpu().numpy()
             assert same_f32(y_o, ol.gemv_neon(xo, om, oe)[0]), (rep, mismatch(y_o, ol.gemv_neon(xo, om, oe)[0]))
     plan.close()
@@ -708,19 +728,26 @@ def test_random_batches_against_the_oracle(gpu, torch_mod):
             assert same_f32(Y[b], y_ref), (B, M, K, seed, b, mismatch(Y[b], y_ref))
 
 
-def test_random_plans_against_the_oracle(gpu, torch_mod, plan_mode):
+@pytest.mark.parametrize("kind", ["any", "queue"])
+def test_random_plans_against_the_oracle(gpu, torch_mod, kind):
     """Six seeded plans of 1-10 GEMVs (1-4,999 rows; K whole blocks up to 4,096
     or ragged; some sharing an activation tensor), most with one fused lm_head
     (even vocabularies up to 140,000, hidden 64-1,024, k in 1-64) at a random
     place in the list: every y bit-exact, the top-k and argmax identical, on
-    two runs."""
+    two runs.  "queue": shapes the single launch takes (even M up to 9,998, K
+    a multiple of 512, hidden 512 or 1,024), so that the tile queue, its
+    LDS quantization and its in-launch merge see random plans."""
     qk, torch = gpu, torch_mod
-    rng = np.random.default_rng(31337)
+    rng = np.random.default_rng(31337 if kind == "any" else 4711)
     for p in range(6):
         items, refs = [], []
         for j in range(int(rng.integers(1, 11))):
-            M = int(rng.integers(1, 5000))
-            K = int(rng.integers(1, 65)) * 64 if rng.random() < 0.8 else int(rng.integers(64, 4097))
+            if kind == "queue":
+                M = int(rng.integers(1, 5000)) * 2
+                K = int(rng.integers(1, 9)) * 512
+            else:
+                M = int(rng.integers(1, 5000))
+                K = int(rng.integers(1, 65)) * 64 if rng.random() < 0.8 else int(rng.integers(64, 4097))
             seed = int(rng.integers(0, 2**31))
             if refs and refs[-1][1] == K and rng.random() < 0.5:
                 xd, x = items[-1]["x"], refs[-1][3]  # the same activation tensor
@@ -733,14 +760,18 @@ def test_random_plans_against_the_oracle(gpu, torch_mod, plan_mode):
         head = None
         if rng.random() < 0.7:
             V, H, k = int(rng.integers(1, 70001)) * 2, int(rng.integers(1, 17)) * 64, int(rng.integers(1, 65))
+            if kind == "queue":
+                H = int(rng.choice([512, 1024]))
             seed = int(rng.integers(0, 2**31))
             x = qk.synth_normal(H, seed + 1)
             pos = int(rng.integers(0, len(items) + 1))
             items.insert(pos, {"mat": qk.DeviceMatrix.synth(V, H, seed, 122, 128),
                                "x": torch.from_numpy(x).cuda(), "topk": k})
             head = (V, H, k, seed, x)
-        say("random plan", plan_mode, p, [(M, K) for M, K, *_ in refs], head[:3] if head else None)
+        say("random plan", kind, p, [(M, K) for M, K, *_ in refs], head[:3] if head else None)
         plan = qk.SweepPlan(items)
+        if kind == "queue" and (head or sum((M + 63) // 64 for M, *_ in refs) > 384):
+            assert plan.kernel_name(0) == "bfp8_sweep_kernel", p
         for rep in range(2):
             for it in items:
                 if "y" in it:
@@ -830,25 +861,12 @@ def test_batch_odd_sizes(gpu, torch_mod):
         assert same_f32(Y[b], ol.gemv_neon(X[b], mant, exps)[0]), b
 
 
-@pytest.fixture(params=["two_launches", "single_launch"])
-def plan_mode(request):
-    """Plans created under this fixture take the default two launches, or the
-    opt-in single launch (BFP8_PLAN_SINGLE_LAUNCH=1 when the plan is created)."""
-    import os
-
-    old = os.environ.get("BFP8_PLAN_SINGLE_LAUNCH")
-    os.environ["BFP8_PLAN_SINGLE_LAUNCH"] = "1" if request.param == "single_launch" else "0"
-    yield request.param
-    if old is None:
-        del os.environ["BFP8_PLAN_SINGLE_LAUNCH"]
-    else:
-        os.environ["BFP8_PLAN_SINGLE_LAUNCH"] = old
-
-
-def test_sweep_plan_24_layers_and_lm_head(gpu, torch_mod, plan_mode):
+@pytest.mark.parametrize("with_head", [True, False])
+def test_sweep_plan_24_layers_and_lm_head(gpu, torch_mod, with_head):
     """The full synthetic decode sweep in one plan: 24 x {gate, up, down, in, out}
-    plus the fused lm_head, every output bit-exact, three runs in a row (the
-    second with new activations written in place), in every launch mode."""
+    plus the fused lm_head (or without it: every tile from the queue), in the
+    single launch, every output bit-exact, three runs in a row (the second
+    with new activations written in place)."""
     qk, torch = gpu, torch_mod
     shapes = [(3584, 1024), (3584, 1024), (1024, 3584), (6144, 1024), (1024, 2048)]
     items, refs = [], []
@@ -864,11 +882,10 @@ def test_sweep_plan_24_layers_and_lm_head(gpu, torch_mod, plan_mode):
     lm = qk.DeviceMatrix.synth(65536, 1024, 99_999, 122, 128)
     xl = qk.synth_normal(1024, 99_998)
     items.insert(0, {"mat": lm, "x": torch.from_numpy(xl).cuda(), "topk": 40})
-    plan = qk.SweepPlan(items)
-    assert plan.kernel_name(0) == {"two_launches": "bfp8_gemv_head_kernel",
-                                   "single_launch": "bfp8_sweep_kernel"}[plan_mode]
+    plan = qk.SweepPlan(items if with_head else items[1:])
+    assert plan.kernel_name(0) == "bfp8_sweep_kernel"
     for rep in range(3):
-        say("sweep plan run", plan_mode, rep)
+        say("sweep plan run", with_head, rep)
         if rep == 1:  # new activations in the same buffers: no record of the last run may be read
             for i, (it, (M, K, seed, x)) in enumerate(zip(items[1:], refs)):
                 x = qk.synth_swiglu(K, seed + 7) if K == 3584 else qk.synth_normal(K, seed + 7)
@@ -884,6 +901,8 @@ def test_sweep_plan_24_layers_and_lm_head(gpu, torch_mod, plan_mode):
             mant, exps = qk.synth_planes(M, K, seed, 124, 130)
             y_ref, *_ = ol.gemv_neon(x, mant, exps)
             assert same_f32(it["y"].cpu().numpy(), y_ref), (M, K, seed)
+        if not with_head:
+            continue
         mant, exps = qk.synth_planes(65536, 1024, 99_999, 122, 128)
         y_ref, *_ = ol.gemv_neon(xl, mant, exps)
         ids, sc, cnt = plan.topk_out
