@@ -6,7 +6,9 @@ answer follows from the arithmetic, ARM ARM flush-to-zero rules, and brute
 force on small inputs.
 """
 import ctypes
+import json
 import math
+import re
 from pathlib import Path
 
 import numpy as np
@@ -523,6 +525,104 @@ def test_exp_neon_accuracy_and_special_points():
     assert ol.exp_neon(np.inf) == ol.exp_neon(88.0) and ol.exp_neon(-np.inf) == ol.exp_neon(-87.0)
     assert ol.exp_neon(1000.0) == ol.exp_neon(88.0) and ol.exp_neon(-1000.0) == ol.exp_neon(-87.0)
     assert math.isnan(ol.exp_neon(float("nan")))
+
+
+_EXP_LITERALS = Path(__file__).resolve().parent / "golden" / "exp_neon_literals.json"
+_FLOAT_LIT = re.compile(r"(?<![\w.])-?\d+\.\d*(?:[eE][-+]?\d+)?f")
+
+
+def _function_body(text, head):
+    """The text of the brace block that follows the first line containing
+    head."""
+    i = text.index(head)
+    j = text.index("{", i)
+    depth = 0
+    for k in range(j, len(text)):
+        depth += {"{": 1, "}": -1}.get(text[k], 0)
+        if depth == 0:
+            return text[j:k + 1]
+    raise AssertionError(head)
+
+
+def _distinct_f32(literals):
+    out = []
+    for t in literals:
+        v = np.float32(float(t.rstrip("f")))
+        if not any(v.view(np.uint32) == o.view(np.uint32) for o in out):
+            out.append(v)
+    return [int(v.view(np.uint32)) for v in out]
+
+
+def test_exp_neon_literals_are_the_references():
+    """exp_neon's constants -- the clamps, log2(e), the 1.5 * 2^23 rounding
+    constant, the six Horner coefficients and 1 -- are the reference's
+    (04/qwen_kernels_opt.c:332-352), literal by literal as float32 and in
+    order, in the oracle (orc_exp_neon) and in the device code (runtime_dev.h
+    exp_neon); the exponent bias 127 and shift 23 too.  The fixture holds the
+    reference's literal text (tests/golden/make_exp_neon_literals.py); where
+    the reference is present it is parsed again and must agree."""
+    fx = json.loads(_EXP_LITERALS.read_text(encoding="utf-8"))
+    ref_src = Path("/root/reference/04-板载脚本与工具/qwen_kernels_opt.c")
+    if ref_src.exists():
+        import importlib.util
+        spec = importlib.util.spec_from_file_location("mk_exp", _EXP_LITERALS.parent / "make_exp_neon_literals.py")
+        mk = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mk)
+        assert mk.parse(ref_src.read_text(encoding="utf-8")) == fx
+    want = _distinct_f32(fx["floats"])
+    assert len(want) == 11 and fx["ints"] == ["127", "23"]
+    root = Path(__file__).resolve().parents[1]
+    bodies = {
+        "oracle": _function_body((root / "oracle" / "runtime_oracle.c").read_text(), "float orc_exp_neon(float x)"),
+        "device": _function_body((root / "qwen35-ax7020-edge-llm_amd" / "csrc" / "runtime_dev.h").read_text(),
+                                 "float exp_neon(float x)"),
+    }
+    for name, body in bodies.items():
+        assert _distinct_f32(_FLOAT_LIT.findall(body)) == want, name
+        assert re.search(r"\b127\b", body) and re.search(r"<<\s*23\b", body), name
+
+
+def _exp_neon_from_literals(x):
+    """exp_neon in float32 numpy arithmetic from the fixture's literals, in
+    the reference's operation order: vmax/vmin clamps (a NaN stays NaN),
+    fx = x * log2e, t = fx + magic, n = t - magic, f = fx - n, p = c + p * f
+    (vmlaq: product and sum each rounded), e = (int)n + 127 (vcvtq truncates,
+    NaN -> 0), result p * bits(e << 23)."""
+    lit = [np.float32(float(t.rstrip("f"))) for t in json.loads(_EXP_LITERALS.read_text(encoding="utf-8"))["floats"]]
+    lo, hi, log2e, magic, *coef = lit
+    x = np.asarray(x, dtype=np.float32)
+    with np.errstate(invalid="ignore", over="ignore"):
+        x = np.where(x < lo, lo, x)
+        x = np.where(x > hi, hi, x)
+        fx = x * log2e
+        t = fx + magic
+        n = t - magic
+        f = fx - n
+        p = coef[0]
+        for c in coef[1:]:
+            p = c + (p * f).astype(np.float32)
+        e = np.where(np.isnan(n), 0, n.astype(np.float64)).astype(np.int64) + 127
+        sc = (e.astype(np.uint32) << np.uint32(23)).view(np.float32)
+        return (p * sc).astype(np.float32)
+
+
+def test_exp_neon_bit_exact_against_the_reference_literals():
+    """The oracle's exp_neon is bit for bit the reference's algorithm built
+    from the reference's own literals (the fixture), over the clamped range,
+    around the rounding points of n, at the clamps and beyond: a slip in any
+    coefficient's digits moves some of these results."""
+    rng = np.random.default_rng(332)
+    xs = np.concatenate([
+        np.linspace(-90.0, 90.0, 40001, dtype=np.float32),
+        rng.uniform(-87.0, 88.0, 40000).astype(np.float32),
+        (np.arange(-126, 128, dtype=np.float32) * np.float32(0.6931472)),  # n crossings
+        (np.arange(-200, 201, dtype=np.float32) * np.float32(0.34657359)),  # half-integer f
+        np.array([0.0, -0.0, 1e-30, -1e-30, 1e-7, -1e-7, -87.0, 88.0, -87.5, 88.5, np.inf, -np.inf], np.float32),
+    ])
+    want = _exp_neon_from_literals(xs)
+    got = np.array([ol.exp_neon(float(x)) for x in xs], dtype=np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert math.isnan(ol.exp_neon(float("nan"))) and np.isnan(_exp_neon_from_literals(np.float32(np.nan)))
 
 
 def test_swiglu_formula_and_scalar_tail():
