@@ -370,16 +370,29 @@ int qwen_weights_find(const char* name, const int8_t** mant_gpu, const uint8_t**
  * 02/tb_gemv_core.v:281-297).  K % 64 == 0. */
 int bfp8_dev_pack_rows(int8_t* mant_gpu, uint8_t* exps_gpu, const uint8_t* row_stream, int M, int K, void* stream);
 
-/* A sweep plan: many independent GEMVs (and at most one fused lm_head)
- * executed as two streaming launches: the lm_head's tiles, then every other
- * GEMV's (larger K first), whose workgroup 0 first merges the lm_head's
- * per-tile top-k partials.  When the lm_head's K is a multiple of 64 and at
- * most 1024 its launch also quantizes every activation of the plan (else, and
- * without an lm_head, a quantize launch comes first).  A plan without an
- * lm_head runs one GEMV, or two reading the same x, 16 rows per workgroup, and
- * other plans of few row tiles one tile per 16-wavefront workgroup.  Item i
- * reads x (device, K floats) and writes y (device, M floats), or, for the
- * lm_head item (topk > 0), the four top-k outputs. */
+/* A sweep plan: many independent GEMVs (and at most one fused lm_head).
+ * Item i reads x (device, K floats) and writes y (device, M floats), or, for
+ * the lm_head item (topk > 0), the four top-k outputs.
+ *
+ * A plan whose every item has an even M and K a multiple of 512 up to 4096,
+ * with 1..128 GEMVs besides the lm_head (and, without an lm_head, more than
+ * 384 row tiles in all) runs as ONE launch (bfp8_sweep_kernel): workgroups
+ * take 64-row tiles from a device tile queue, quantize each tile's
+ * activation in LDS, and the grid's last workgroup merges the lm_head's
+ * per-tile top-k lists as they are published.  That merge waits for each
+ * list a bounded time (milliseconds); a list that never comes -- possible
+ * only if the launch's workgroups are not all resident at once -- makes the
+ * run write *out_count = -1 and *out_argmax = -1 (the top-k outputs are then
+ * invalid; the caller must treat the run as failed).
+ *
+ * Other plans run as streaming launches: the lm_head's tiles, then every
+ * other GEMV's (larger K first), whose workgroup 0 first merges the lm_head's
+ * per-tile top-k partials (without other GEMVs: the stand-alone merge
+ * kernel).  When the lm_head's K is a multiple of 64 and at most 1024 its
+ * launch also quantizes every activation of the plan (else, and without an
+ * lm_head, a quantize launch comes first).  A plan without an lm_head runs
+ * one GEMV, or two reading the same x, 16 rows per workgroup, and other
+ * plans of few row tiles one tile per 16-wavefront workgroup. */
 typedef struct bfp8_plan_item {
     const float* x;
     float* y;
@@ -401,9 +414,10 @@ int bfp8_plan_run(void* plan, void* stream);
  * does so here too). */
 int bfp8_plan_run_gemv(void* plan, void* stream);
 /* One stage of bfp8_plan_run_gemv, for timing each launch on its own:
- * 0 = the lm_head's tiles, 1 = the other GEMVs' tiles with the top-k merge
- * (or the stand-alone merge kernel when the plan has no other GEMV),
- * 2 = odd-row tails and K > 4096 items.  Stages must run in this order. */
+ * 0 = the single launch, or the lm_head's tiles; 1 = the other GEMVs' tiles
+ * with the top-k merge (or the stand-alone merge kernel when the plan has no
+ * other GEMV); 2 = odd-row tails and K > 4096 items.  Stages must run in this
+ * order; a single-launch plan's stages 1 and 2 are empty. */
 int bfp8_plan_launch(void* plan, int stage, void* stream);
 /* Name of the (main) kernel a stage launches, "" if the stage is empty. */
 const char* bfp8_plan_kernel_name(void* plan, int stage);

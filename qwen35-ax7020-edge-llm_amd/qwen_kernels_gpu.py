@@ -480,6 +480,17 @@ class SweepPlan:
     def run(self):
         check(load().bfp8_plan_run(self.handle, _stream()), "plan_run")
 
+    def topk_result(self):
+        """(ids, scores, argmax) of the lm_head item after run(), waiting for
+        the stream; raises when the run reports its top-k invalid (count -1:
+        the single launch's merge gave up waiting for a tile's list)."""
+        ids, sc, cnt = self.topk_out
+        _torch().cuda.current_stream().synchronize()
+        n, am = (int(v) for v in cnt.cpu().tolist())
+        if n < 0:
+            raise RuntimeError("bfp8 plan: the lm_head top-k of this run is invalid (count -1)")
+        return ids[:n], sc[:n], am
+
     def quantize(self):
         check(load().bfp8_plan_quantize(self.handle, _stream()), "plan_quantize")
 

@@ -905,8 +905,8 @@ def test_sweep_plan_24_layers_and_lm_head(gpu, torch_mod, with_head):
             continue
         mant, exps = qk.synth_planes(65536, 1024, 99_999, 122, 128)
         y_ref, *_ = ol.gemv_neon(xl, mant, exps)
-        ids, sc, cnt = plan.topk_out
+        ids, sc, am = plan.topk_result()  # raises on an invalid (count -1) run
         ids_ref, sc_ref = ol.topk(y_ref, 40)
-        assert int(cnt[0].item()) == 40 and int(cnt[1].item()) == ol.argmax(y_ref)
+        assert ids.numel() == 40 and am == ol.argmax(y_ref)
         assert np.array_equal(ids.cpu().numpy(), ids_ref) and same_f32(sc.cpu().numpy(), sc_ref)
     plan.close()

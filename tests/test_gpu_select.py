@@ -105,6 +105,42 @@ def test_bfp8_lm_head_device_any_arguments(gpu, V, k):
     assert int(am.item()) == ol.argmax(y)
 
 
+@pytest.mark.parametrize("k", [40, 100])
+def test_top_k_on_a_second_stream_and_the_host_entry(gpu, k):
+    """Scratch is per stream: a device-level top-k queued on a second stream
+    (not waited for) and the host entry bfp8_lm_head_topk (the library's own
+    stream) right after it, then two device-level top-ks on two streams, each
+    over its own lm_head, all against the oracle.  k = 40 takes the fused
+    per-tile lists and the merge, k = 100 the scores and the selection."""
+    qk = gpu
+    import torch
+
+    V, H = 65536, 1024
+    kk = qk.Bfp8Kernels()
+    mats = [planes(V, H, 9100 + i) for i in range(3)]
+    refs = [ol.topk(ref_logits(x, mant, exps), k) for mant, exps, x in mats]
+    dms = [qk.DeviceMatrix.from_soa(mant, exps) for mant, exps, _ in mats]
+    xq = [qk.quantize(torch.from_numpy(x).cuda()) for _, _, x in mats]
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    say("two streams", V, H, k)
+    for rep in range(3):
+        with torch.cuda.stream(s2):
+            d0 = qk.lm_head_topk(dms[0], xq[0][2], xq[0][1], k)
+        mant, exps, x = mats[1]
+        ids_h, sc_h = kk.lm_head_topk(x, mant, exps, V, H, k)  # the library's stream, while s2 runs
+        with torch.cuda.stream(s1):
+            d1 = qk.lm_head_topk(dms[2], xq[2][2], xq[2][1], k)
+        with torch.cuda.stream(s2):
+            d2 = qk.lm_head_topk(dms[0], xq[0][2], xq[0][1], k)
+        torch.cuda.synchronize()
+        assert np.array_equal(ids_h, refs[1][0]) and same_f32(sc_h, refs[1][1]), rep
+        for (ids, sc, cnt, _), (ids_ref, sc_ref) in ((d0, refs[0]), (d1, refs[2]), (d2, refs[0])):
+            n = int(cnt.item())
+            assert n == ids_ref.size, rep
+            assert np.array_equal(ids.cpu().numpy()[:n], ids_ref) and same_f32(sc.cpu().numpy()[:n], sc_ref), rep
+
+
 @pytest.mark.parametrize("case", ["odd_vocab", "k100", "k4160"])
 def test_plan_with_a_general_lm_head(gpu, case):
     """A sweep plan whose lm_head item is outside the fused launch's range runs

@@ -64,3 +64,42 @@ def test_no_alloc_lm_head_matches_the_allocating_entry(gpu):
                                            xsp.data_ptr(), xs.data_ptr(), big.mant.data_ptr(), big.exps.data_ptr(),
                                            262146, 64, 4, None)
     assert rc == qk.BFP8_EINVAL and b"262144" in lib.bfp8_last_error()
+
+
+def test_no_alloc_lm_head_allocates_nothing(gpu):
+    """On a stream the library has never seen (the allocating entry would
+    reserve that stream's scratch there; HIP has used it once), a call of the
+    no-alloc entry leaves the device's free memory exactly as it was, and its
+    result is the oracle's."""
+    qk = gpu
+    import torch
+
+    lib = qk.load()
+    V, H, k = 65536, 1024, 40
+    r = np.random.default_rng(13)
+    mant = r.integers(-128, 128, size=(V, H), dtype=np.int8)
+    exps = r.integers(120, 131, size=(V, H // 64), dtype=np.uint8)
+    x = r.standard_normal(H).astype(F32)
+    dm = qk.DeviceMatrix.from_soa(mant, exps)
+    _, xs, xsp = qk.quantize(torch.from_numpy(x).cuda())
+    ids = torch.full((k,), -7, dtype=torch.int32, device="cuda")
+    sc = torch.zeros(k, dtype=torch.float32, device="cuda")
+    cnt = torch.full((2,), -7, dtype=torch.int32, device="cuda")
+    fresh = torch.cuda.Stream()
+    with torch.cuda.stream(fresh):  # HIP's own first use of the stream, outside the measured call
+        ids.fill_(-7)
+    torch.cuda.synchronize()
+    say("no-alloc lm_head free memory", V, H, k)
+    free0 = torch.cuda.mem_get_info()[0]
+    rc = lib.bfp8_dev_lm_head_topk_noalloc(ids.data_ptr(), sc.data_ptr(), cnt.data_ptr(), cnt.data_ptr() + 4,
+                                           xsp.data_ptr(), xs.data_ptr(), dm.mant.data_ptr(), dm.exps.data_ptr(),
+                                           V, H, k, fresh.cuda_stream)
+    qk.check(rc, "bfp8_dev_lm_head_topk_noalloc")
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info()[0] == free0
+    y = ol.gemv_neon(x, mant, exps)[0]
+    ids_ref, sc_ref = ol.topk(y, k)
+    n = int(cnt[0].item())
+    assert n == k and int(cnt[1].item()) == ol.argmax(y)
+    assert np.array_equal(ids.cpu().numpy()[:n], ids_ref)
+    assert np.array_equal(sc.cpu().numpy()[:n].view(np.uint32), sc_ref.view(np.uint32))
