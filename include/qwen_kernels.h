@@ -250,6 +250,16 @@ const char* bfp8_last_error(void);
 /* Drops every cached device copy of weights and forward parameters (and
  * the forward's device states, resident ones included). */
 void bfp8_cache_clear(void);
+/* Device bytes the library holds (caches, workspaces, per-stream scratch). */
+size_t bfp8_device_bytes(void);
+/* No counterpart in the reference; a testing aid for callers that must rehearse
+ * a full device: the library's device allocations beyond `bytes` in total then
+ * fail as a full device's would (0 lifts the limit).  A weight or bf16 table
+ * that would be cached is then uploaded per call instead (the result is the
+ * same); an entry point that still cannot allocate returns its error code, or,
+ * without an error channel (bfp8_gemv and the other void entry points),
+ * aborts. */
+void bfp8_debug_device_limit(size_t bytes);
 
 /* ---- 3. device-level symbols ------------------------------------------------ */
 

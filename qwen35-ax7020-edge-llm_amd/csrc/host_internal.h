@@ -52,21 +52,41 @@ struct ProfScope {
 };
 
 // ---- device buffers -------------------------------------------------------------------
+// Bytes the library's DevBufs hold on the device, and a limit on them (0:
+// none) that bfp8_debug_device_limit sets to rehearse a full device.
+inline size_t g_dev_bytes = 0;
+inline size_t g_dev_limit = 0;
+
 struct DevBuf {
     void* p = nullptr;
     size_t n = 0;
+    // BFP8_ENOMEM when the device cannot hold `bytes` more (the buffer is then
+    // empty and HIP's last-error state clear, so that the next launch check
+    // does not report this failure).
     int reserve(size_t bytes) {
         if (bytes <= n) return BFP8_OK;
-        if (p) HIP_OK(hipFree(p));
-        p = nullptr;
-        n = 0;
-        size_t want = std::max<size_t>(bytes, 256);
-        HIP_OK(hipMalloc(&p, want));
+        release();
+        const size_t want = std::max<size_t>(bytes, 256);
+        if (g_dev_limit && g_dev_bytes + want > g_dev_limit) {
+            set_error("device memory: %zu more bytes exceed the limit of %zu", want, g_dev_limit);
+            return BFP8_ENOMEM;
+        }
+        const hipError_t e = hipMalloc(&p, want);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            p = nullptr;
+            set_error("hipMalloc(%zu): %s", want, hipGetErrorString(e));
+            return e == hipErrorOutOfMemory ? BFP8_ENOMEM : BFP8_EHIP;
+        }
         n = want;
+        g_dev_bytes += n;
         return BFP8_OK;
     }
     void release() {
-        if (p) (void)hipFree(p);
+        if (p) {
+            (void)hipFree(p);
+            g_dev_bytes -= n;
+        }
         p = nullptr;
         n = 0;
     }

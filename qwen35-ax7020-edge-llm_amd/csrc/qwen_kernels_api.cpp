@@ -156,8 +156,8 @@ int weights_cached(const int8_t* mant, const uint8_t* exps, int M, int K, bool f
     HIP_OK(hipMemcpyAsync(g.soa_m.p, mant, mbytes, hipMemcpyHostToDevice, g.stream));
     HIP_OK(hipMemcpyAsync(g.soa_e.p, exps, ebytes, hipMemcpyHostToDevice, g.stream));
     const size_t gm = bfp8_gpu_mant_bytes(M, K), ge = bfp8_gpu_exps_bytes(M, K);
-    const bool cacheable = g.cache_bytes + gm + ge <= kCacheLimit &&
-                           (force || (range_readonly_cached(mant, mbytes) && range_readonly_cached(exps, ebytes)));
+    bool cacheable = g.cache_bytes + gm + ge <= kCacheLimit &&
+                     (force || (range_readonly_cached(mant, mbytes) && range_readonly_cached(exps, ebytes)));
     if (force && !cacheable) {
         set_error("device weight cache full (%zu bytes)", g.cache_bytes);
         return BFP8_EINVAL;
@@ -166,8 +166,17 @@ int weights_cached(const int8_t* mant, const uint8_t* exps, int M, int K, bool f
     DevBuf* de = &g.gpu_e;
     CachedWeights cw;
     if (cacheable) {
-        dm = &cw.mant;
-        de = &cw.exps;
+        if ((rc = cw.mant.reserve(gm)) || (rc = cw.exps.reserve(ge))) {
+            // the device holds no further cached copy: a preload fails, any
+            // other call converts into the per-call buffers (recoverable)
+            cw.mant.release();
+            cw.exps.release();
+            if (force) return rc;
+            cacheable = false;
+        } else {
+            dm = &cw.mant;
+            de = &cw.exps;
+        }
     }
     if ((rc = dm->reserve(gm)) || (rc = de->reserve(ge))) return rc;
     HIP_OK(bfp8_launch_pack(dm->as<uint8_t>(), de->as<uint8_t>(), g.soa_m.as<int8_t>(),
@@ -214,8 +223,17 @@ int bf16_table_cached(const uint16_t* table, int vocab, int hidden, bool force, 
     if (bf16_table_lookup(table, vocab, hidden, out, tiled)) return BFP8_OK;
     const bool tile = bf16_tiled_ok(hidden);
     const size_t kept = tile ? bf16_tiled_elems(vocab, hidden) * 2 : bytes;
-    const bool cacheable = g.cache_bytes + kept <= kCacheLimit && (force || range_readonly_cached(table, bytes));
+    bool cacheable = g.cache_bytes + kept <= kCacheLimit && (force || range_readonly_cached(table, bytes));
     int rc;
+    Bf16Table fresh;
+    if (cacheable) {
+        // (the tile layout is converted from a row-major upload in bf16_ws)
+        if ((rc = fresh.buf.reserve(kept)) || (tile && (rc = g.bf16_ws.reserve(bytes)))) {
+            fresh.buf.release();   // no room for another cached table: a preload
+            if (force) return rc;  // fails, any other call uploads per call
+            cacheable = false;
+        }
+    }
     if (!cacheable) {
         if ((rc = g.bf16_ws.reserve(bytes))) return rc;
         HIP_OK(hipMemcpyAsync(g.bf16_ws.p, table, bytes, hipMemcpyHostToDevice, g.stream));
@@ -223,13 +241,7 @@ int bf16_table_cached(const uint16_t* table, int vocab, int hidden, bool force, 
         *tiled = 0;
         return BFP8_OK;
     }
-    Bf16Table fresh;
-    if ((rc = fresh.buf.reserve(kept))) return rc;
     if (tile) {
-        if ((rc = g.bf16_ws.reserve(bytes))) {
-            fresh.buf.release();
-            return rc;
-        }
         HIP_OK(hipMemcpyAsync(g.bf16_ws.p, table, bytes, hipMemcpyHostToDevice, g.stream));
         HIP_OK(bf16_launch_tile_table(fresh.buf.as<uint16_t>(), g.bf16_ws.as<uint16_t>(), vocab, hidden, g.stream));
         fresh.tiled = 1;
@@ -815,6 +827,16 @@ void bfp8_cache_clear(void) {
     g.cache.clear();
     g.cache_bytes = 0;
     g.writable.clear();
+}
+
+void bfp8_debug_device_limit(size_t bytes) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    g_dev_limit = bytes;
+}
+
+size_t bfp8_device_bytes(void) {
+    std::lock_guard<std::mutex> lk(g.mu);
+    return g_dev_bytes;
 }
 
 void qwen_prof_enable(int on) { g_prof_on = on; }

@@ -149,6 +149,10 @@ def bind(lib: ctypes.CDLL) -> ctypes.CDLL:
     lib.bfp8_gpu_ready.restype = ctypes.c_int
     lib.bfp8_cache_clear.argtypes = []
     lib.bfp8_cache_clear.restype = None
+    lib.bfp8_device_bytes.argtypes = []
+    lib.bfp8_device_bytes.restype = ctypes.c_size_t
+    lib.bfp8_debug_device_limit.argtypes = [ctypes.c_size_t]
+    lib.bfp8_debug_device_limit.restype = None
     # device level
     for name in ("bfp8_dev_mant_bytes", "bfp8_dev_exps_bytes"):
         getattr(lib, name).argtypes = [i, i]
