@@ -184,7 +184,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="sweep",
                     choices=["sweep", "layers", "lm_head", "lm_head_plain", "gemv", "down", "batch16", "lm_head_bf16",
-                             "host_gemv",
+                             "host_gemv", "select",
                              "forward_token"])
     ap.add_argument("--rotate-gb", type=float, default=1.0, help="rotating weight copies totalling >= this")
     ap.add_argument("--bf16-layout", choices=["tiles", "rows"], default="tiles",
@@ -219,6 +219,8 @@ def main():
         return bench_forward_token(args, qk, torch, np)
     if args.workload == "host_gemv":
         return bench_host_gemv(args, qk, torch, np)
+    if args.workload == "select":
+        return bench_select(args, qk, torch, np)
 
     items = workload_items(args.workload)
     per_copy = sum(wbytes(M, K) for _, M, K, *_ in items)
@@ -462,6 +464,54 @@ def bench_batch16(args, qk, torch, np):
         out["cpu_baseline"] = cpu_baseline([("batch16", M, K, 124, 130, 0)], batch=B,
                                            nbytes=wbytes(M, K) + B * 4 * K + B * 4 * M)
     print(json.dumps(out), flush=True)
+
+
+def bench_select(args, qk, torch, np):
+    """k above 64 at the 65536 x 1024 lm_head (bfp8_dev_lm_head_topk): the
+    scores (the plain GEMV into the stream's scratch), then the selection --
+    16 blocks of 4096 keys sorted in LDS, each block's first min(k, 4096)
+    keys ranked against every block's -- for k = 65, 200 and vocab + 50.
+    Per k: the call, and the GEMV alone on the same inputs (the difference is
+    the selection's)."""
+    V, H = 65536, 1024
+    lib = qk.load()
+    dm = qk.DeviceMatrix.synth(V, H, 777, 122, 128)
+    x = torch.from_numpy(qk.synth_normal(H, 778)).cuda()
+    _, xs, xsp = qk.quantize(x)
+    y = torch.empty(V, dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream()
+    s = stream.cuda_stream
+    ev = lambda: torch.cuda.Event(enable_timing=True)
+
+    def timed(fn):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        a, b = ev(), ev()
+        a.record(stream)
+        for _ in range(args.steps):
+            fn()
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) * 1e3 / args.steps
+
+    gemv_us = timed(lambda: qk.check(lib.bfp8_dev_gemv(y.data_ptr(), xsp.data_ptr(), xs.data_ptr(), dm.mant.data_ptr(),
+                                                       dm.exps.data_ptr(), V, H, None, s)))
+    per_k = {}
+    for k in (65, 200, V + 50):
+        kk = min(k, V)
+        ids = torch.empty(kk, dtype=torch.int32, device="cuda")
+        sc = torch.empty(kk, dtype=torch.float32, device="cuda")
+        cnt = torch.empty(2, dtype=torch.int32, device="cuda")
+        us = timed(lambda: qk.check(lib.bfp8_dev_lm_head_topk(ids.data_ptr(), sc.data_ptr(), cnt.data_ptr(),
+                                                               cnt.data_ptr() + 4, xsp.data_ptr(), xs.data_ptr(),
+                                                               dm.mant.data_ptr(), dm.exps.data_ptr(), V, H, k, s)))
+        per_k[str(k)] = {"us_per_call": round(us, 2), "selection_us": round(us - gemv_us, 2)}
+    print(json.dumps({"metric": "lm_head top-k above 64: us per call", "value": per_k["200"]["us_per_call"],
+                      "unit": "us", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+                      "higher_is_better": False,
+                      "config": {"workload": "select", "vocab": V, "hidden": H, "k": [65, 200, V + 50]},
+                      "gemv_alone_us": round(gemv_us, 2), "per_k": per_k}), flush=True)
 
 
 def bench_lm_head_bf16(args, qk, torch, np):

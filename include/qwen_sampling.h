@@ -22,7 +22,8 @@ extern "C" {
  * added), sorted by (score desc, id asc) among scores above -FLT_MAX.
  * Returns min(k, vocab_size) candidates or fewer; 0 on invalid arguments
  * (here also a vocabulary above 2^28 rows).  k <= 64 runs fused into the
- * scoring launch, larger k through the scores and a sort of their keys. */
+ * scoring launch, larger k through the scores and a multi-workgroup
+ * selection of their keys (include/qwen_kernels.h). */
 int lm_head_topk(const float* h, const uint16_t* embed_table, int vocab_size, int hidden_dim, int k, int* out_ids,
                  float* out_scores);
 

@@ -79,6 +79,12 @@ struct Bfp8TileRef {
 #define BFP8_TOPK_MAX 64
 #define BFP8_TOPK_MAX_TILES 4096
 #define BFP8_SELECT_MAX (1 << 28)  // entries the sort-based selection and the sampler take
+#define BFP8_SELECT_BLOCK 2048       // keys per LDS-sorted block of the selection
+#define BFP8_SELECT_RANK_MAX (1 << 20)  // entries the block-sort + rank selection takes
+// Scratch of bfp8_launch_select_sort: the n keys, then a count per block.
+constexpr size_t bfp8_select_scratch_bytes(long long n) {
+    return ((size_t)n * 8 + (size_t)((n + BFP8_SELECT_BLOCK - 1) / BFP8_SELECT_BLOCK) * 4 + 255) & ~(size_t)255;
+}
 #define BF16_HEAD_MAX_HIDDEN 4096  // hidden size of the bf16 lm_head (LDS copy of h)
 #define BFP8_STREAM_WG_PER_CU 4
 // Row tiles up to which a GEMV (or a plan's GEMVs) runs one tile per
@@ -222,7 +228,7 @@ hipError_t bf16_launch_tile_table(uint16_t* dst, const uint16_t* src, int vocab,
 #define BFP8_NOALLOC_MAX_VOCAB 262144
 #define BFP8_NOALLOC_PARTIALS_BYTES ((size_t)(BFP8_NOALLOC_MAX_VOCAB / 64) * BFP8_TOPK_MAX * 8)
 #define BFP8_NOALLOC_LOGITS_BYTES ((size_t)BFP8_NOALLOC_MAX_VOCAB * 4)
-#define BFP8_NOALLOC_KEYS_BYTES ((size_t)BFP8_NOALLOC_MAX_VOCAB * 8)
+#define BFP8_NOALLOC_KEYS_BYTES bfp8_select_scratch_bytes(BFP8_NOALLOC_MAX_VOCAB)
 // Device address of the scratch on the current device (looked up once per
 // device with hipGetSymbolAddress, then cached).
 hipError_t bfp8_noalloc_setup(void** out);
@@ -231,8 +237,10 @@ hipError_t bfp8_noalloc_setup(void** out);
 // Per-tile top-`topk` partials ([ntiles(n)][topk] keys) of logits[0, n), for
 // bfp8_launch_topk_merge (topk <= BFP8_TOPK_MAX).
 hipError_t bfp8_launch_select_partials(const float* logits, int n, int topk, uint64_t* partials, hipStream_t s);
-// The kk best of logits[0, n) by sorting all n keys (keys: n entries of
-// scratch): ids / scores [kk], count, argmax as the merge writes them.
+// The kk best of logits[0, n) (kk > BFP8_TOPK_MAX): 4096-key blocks sorted
+// in LDS, then ranked (n <= BFP8_SELECT_RANK_MAX), else all n keys sorted by
+// one workgroup; keys: bfp8_select_scratch_bytes(n) of scratch.  ids /
+// scores [kk], count, argmax as the merge writes them.
 hipError_t bfp8_launch_select_sort(const float* logits, int n, int kk, uint64_t* keys, int* ids, float* scores,
                                    int* count, int* argmax, hipStream_t s);
 hipError_t bfp8_launch_sample(const Bfp8SampleArgs& a, hipStream_t s);

@@ -263,7 +263,8 @@ int bf16_table_for(const uint16_t* table, int vocab, int hidden, const uint16_t*
 StreamScratch& scratch_for(hipStream_t s) { return g.scratch[s]; }
 
 // Selection with the caller's scratch: partials (bfp8_ntiles(n) * kk keys)
-// when kk <= BFP8_TOPK_MAX, else keys (n keys).  Allocates nothing.
+// when kk <= BFP8_TOPK_MAX, else keys (bfp8_select_scratch_bytes(n)).
+// Allocates nothing.
 int select_topk_raw(const float* logits, int n, int kk, int* ids, float* scores, int* count, int* argmax,
                     uint64_t* partials, uint64_t* keys, hipStream_t s) {
     if (kk <= BFP8_TOPK_MAX) {
@@ -288,7 +289,7 @@ int select_topk_bufs(const float* logits, int n, int kk, int* ids, float* scores
     int rc;
     if (kk <= BFP8_TOPK_MAX) {
         if ((rc = partials.reserve((size_t)bfp8_ntiles(n) * kk * 8))) return rc;
-    } else if ((rc = keys.reserve((size_t)n * 8))) {
+    } else if ((rc = keys.reserve(bfp8_select_scratch_bytes(n)))) {
         return rc;
     }
     return select_topk_raw(logits, n, kk, ids, scores, count, argmax, partials.as<uint64_t>(), keys.as<uint64_t>(), s);
@@ -1286,7 +1287,7 @@ void* bfp8_plan_create(const bfp8_plan_item* items, int n) {
             if (kk <= BFP8_TOPK_MAX)
                 rc = rc ? rc : p->gen_partials.reserve((size_t)bfp8_ntiles(it.M) * kk * 8);
             else
-                rc = rc ? rc : p->gen_keys.reserve((size_t)it.M * 8);
+                rc = rc ? rc : p->gen_keys.reserve(bfp8_select_scratch_bytes(it.M));
             p->items[i].topk = 0;
             p->items[i].y = p->logits.as<float>();
         }

@@ -4,8 +4,14 @@
 //   * per-tile top-k partials of a logits vector (k <= 64), merged by the
 //     stand-alone merge kernel of bfp8_ftz.hip: odd vocabularies, hidden
 //     sizes the fused launches do not take;
-//   * a full sort of the (score desc, id asc) keys for k > 64
-//     (04/qwen_sampling.c:283-353 returns min(k, vocab) entries for any k);
+//   * for k > 64 (04/qwen_sampling.c:283-353 returns min(k, vocab) entries
+//     for any k) the (score desc, id asc) keys sorted in 2048-key blocks in
+//     LDS and registers, one workgroup each, then each block's first
+//     min(k, 2048) keys ranked against every block's (one bisection in LDS per
+//     candidate and block; keys are unique, so a key's rank is the count of
+//     keys above it).  At 65536 keys: 13.8 us of block sorts, then 5.5 us
+//     (k = 65) to 49 us (all keys) of ranking.  Beyond 2^20 keys one workgroup
+//     sorts them all in global memory (about 2 ms at 65536 keys);
 //   * sample_from_topk (04/qwen_sampling.c:384-529) for any candidate count.
 //
 // Compiled with IEEE f32 subnormals and -ffp-contract=off: the sampler
@@ -20,6 +26,14 @@
 namespace {
 
 constexpr int kSortThreads = 1024;
+constexpr int kSelBlock = BFP8_SELECT_BLOCK;  // keys per LDS-sorted block
+constexpr int kSelLog = __builtin_ctz(kSelBlock);
+constexpr int kBlkThreads = 1024;                        // block sort: threads
+constexpr int kBlkKeys = kSelBlock / kBlkThreads;        // keys per thread (key r * 1024 + thread)
+constexpr int kBlkPairs = (kSelBlock / 2 + kBlkThreads - 1) / kBlkThreads;  // LDS compare-exchanges per thread, step
+constexpr int kRankParts = (kSelBlock + 1023) / 1024;  // rank kernel: workgroups (1024 candidates) per block
+constexpr int kRankTab = 8192;                         // keys of the rank kernel's LDS tables per batch
+static_assert(kSelBlock == 1 << kSelLog && kSelBlock >= 1024 && kSelBlock <= 8192, "block size");
 
 // In-place sort of keys[0, n) into descending order by one workgroup.  The
 // bitonic network in its one-direction form: at every stage of size s, element
@@ -70,9 +84,188 @@ __device__ void block_sort_desc(uint64_t* keys, int n) {
     }
 }
 
+// The kSelBlock keys v (thread t holds keys r * 1024 + t) sorted descending
+// into LDS by the workgroup's 1024 threads: the one-direction bitonic network
+// of block_sort_desc.  A step whose partner (key index ^ mask) is in the same
+// wavefront runs in registers (a lane exchange, the larger key to the lower
+// index); the others run on LDS, one pair or more per thread and step.  Of
+// the 66 steps of 2048 keys, 15 go through LDS.
+__device__ void block_sort_regs(uint64_t (&v)[kBlkKeys], uint64_t* lds) {
+    const int tid = threadIdx.x;
+    bool in_lds = false;
+#pragma unroll
+    for (int ls = 1; ls <= kSelLog; ++ls) {
+#pragma unroll
+        for (int lj = ls - 1; lj >= 0; --lj) {
+            const int j = 1 << lj, size = 1 << ls;
+            const bool mirror = lj == ls - 1;
+            const int mask = mirror ? size - 1 : j;  // partner = index ^ mask
+            if (mask < 64) {
+                if (in_lds) {
+                    __syncthreads();
+#pragma unroll
+                    for (int r = 0; r < kBlkKeys; ++r) v[r] = lds[r * kBlkThreads + tid];
+                    in_lds = false;
+                }
+                const bool lower = (tid & (mirror ? size >> 1 : j)) == 0;  // index below its partner's
+#pragma unroll
+                for (int r = 0; r < kBlkKeys; ++r) {
+                    const uint64_t o = xor_lane(v[r], mask);
+                    v[r] = ((o > v[r]) == lower) ? o : v[r];
+                }
+            } else {
+                if (!in_lds) {
+#pragma unroll
+                    for (int r = 0; r < kBlkKeys; ++r) lds[r * kBlkThreads + tid] = v[r];
+                    in_lds = true;
+                }
+                __syncthreads();
+#pragma unroll
+                for (int r = 0; r < kBlkPairs; ++r) {
+                    const int i = tid + r * kBlkThreads;  // pair 0 .. kSelBlock / 2 - 1
+                    const int blk = i >> lj, off = i & (j - 1);
+                    const int a = mirror ? blk * size + off : blk * 2 * j + off;
+                    const int b = mirror ? blk * size + size - 1 - off : a + j;
+                    if (i >= kSelBlock / 2) continue;
+                    const uint64_t ka = lds[a], kb = lds[b];
+                    if (kb > ka) {
+                        lds[a] = kb;
+                        lds[b] = ka;
+                    }
+                }
+            }
+        }
+    }
+    if (!in_lds) {
+#pragma unroll
+        for (int r = 0; r < kBlkKeys; ++r) lds[r * kBlkThreads + tid] = v[r];
+    }
+    __syncthreads();
+}
+
 }  // namespace
 
 // ---- top-k over a logits vector ------------------------------------------------------------
+// Block b of the keys of logits[0, n) (kSelBlock rows; the last one
+// shorter) sorted descending in LDS and stored over keys[kSelBlock b, ...
+// + len); its count of candidates (nonzero keys) into valid[b].
+extern "C" __global__ __launch_bounds__(kBlkThreads) void bfp8_select_block_sort_kernel(
+    const float* __restrict__ logits, int n, uint64_t* __restrict__ keys, uint32_t* __restrict__ valid) {
+    __shared__ uint64_t s[kSelBlock];
+    __shared__ uint32_t nv;
+    const int base = blockIdx.x * kSelBlock, len = min(kSelBlock, n - base);
+    const int tid = threadIdx.x;
+    if (tid == 0) nv = 0;
+    uint32_t mine = 0;
+    uint64_t v[kBlkKeys];
+#pragma unroll
+    for (int r = 0; r < kBlkKeys; ++r) {
+        const int i = tid + r * kBlkThreads;
+        v[r] = i < len ? topk_key(logits[base + i], base + i) : 0ull;
+        mine += v[r] != 0;
+    }
+    __syncthreads();
+    if (mine) atomicAdd(&nv, mine);
+    block_sort_regs(v, s);
+    for (int i = tid; i < len; i += kBlkThreads) keys[base + i] = s[i];
+    if (tid == 0) valid[blockIdx.x] = nv;
+}
+
+// The kk best keys by rank: workgroup (b, part) takes positions part*1024 +
+// t of sorted block b below min(kk, len_b) as candidates; a candidate's rank
+// is the number of keys above it in every block's first min(kk, len) keys
+// (the blocks' prefixes go through LDS in batches of whole tables; every
+// (candidate, table) pair is one bisection; a key with kk or more keys above
+// it in one prefix is out whatever the rest).  Rank < kk: written at its rank.  Workgroup 0
+// writes the count (min(kk, candidates)), fills the places past it with
+// -1 / 0, and the argmax when there is no candidate; the rank-0 key writes
+// it otherwise (04/qwen_kernels_opt.c:402-403, :483-490).
+extern "C" __global__ __launch_bounds__(kSortThreads) void bfp8_select_rank_kernel(
+    const uint64_t* __restrict__ keys, const uint32_t* __restrict__ valid, int n, int kk, int* __restrict__ ids,
+    float* __restrict__ scores, int* __restrict__ count, int* __restrict__ argmax) {
+    __shared__ uint64_t tab[kRankTab];
+    __shared__ uint64_t cand[kSortThreads];
+    __shared__ int crank[kSortThreads];
+    __shared__ uint32_t red[kSortThreads / 64];
+    const int nblk = (n + kSelBlock - 1) >> kSelLog;
+    const int b = blockIdx.x / kRankParts, part = blockIdx.x % kRankParts;
+    const int tid = threadIdx.x;
+    const int m = min(kk, kSelBlock);  // prefix length of a whole block
+    if (blockIdx.x == 0) {
+        uint32_t v = 0;
+        for (int i = tid; i < nblk; i += kSortThreads) v += valid[i];
+        for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+        if ((tid & 63) == 0) red[tid >> 6] = v;
+        __syncthreads();
+        v = 0;
+#pragma unroll
+        for (int w = 0; w < kSortThreads / 64; ++w) v += red[w];
+        const int cnt = (int)min((uint32_t)kk, v);
+        for (int i = cnt + tid; i < kk; i += kSortThreads) {
+            ids[i] = -1;
+            scores[i] = 0.0f;
+        }
+        if (tid == 0) {
+            *count = cnt;
+            if (v == 0) *argmax = 0;
+        }
+    }
+    const int len_b = min(kSelBlock, n - (b << kSelLog));
+    const int ncand = min(m, len_b) - part * kSortThreads;  // this workgroup's candidates
+    if (ncand <= 0) return;
+    const int nc = min(ncand, kSortThreads);
+    const int pos = part * kSortThreads + tid;
+    const uint64_t key = tid < nc ? keys[(size_t)(b << kSelLog) + pos] : 0ull;
+    if (tid < nc) {
+        cand[tid] = key;
+        crank[tid] = 0;
+    }
+    const int per_batch = kRankTab / m;
+    int top = 1;  // the largest power of two <= m
+    while (2 * top <= m) top *= 2;
+    for (int b0 = 0; b0 < nblk; b0 += per_batch) {
+        const int nt = min(per_batch, nblk - b0);
+        // every load of the batch goes out before any is stored
+        uint64_t v[kRankTab / kSortThreads];
+#pragma unroll
+        for (int r = 0; r < kRankTab / kSortThreads; ++r) {
+            const int i = tid + r * kSortThreads;
+            const int t = i / m, e = i - t * m, b2 = b0 + t;
+            v[r] = i < nt * m && e < n - (b2 << kSelLog) ? keys[(size_t)(b2 << kSelLog) + e] : 0ull;  // past the block: 0
+        }
+        __syncthreads();  // the previous batch's searches are done
+#pragma unroll
+        for (int r = 0; r < kRankTab / kSortThreads; ++r) {
+            const int i = tid + r * kSortThreads;
+            if (i < nt * m) tab[i] = v[r];
+        }
+        __syncthreads();
+        // one (candidate, table) pair per thread at a time: the keys above the
+        // candidate in the table (descending, unique; 0s last) by a
+        // bisection of fixed steps, added to the candidate's rank in LDS
+        for (int w = tid; w < nc * nt; w += kSortThreads) {
+            const int t = w / nc, c = w - t * nc;
+            const uint64_t ck = cand[c];
+            if (!ck) continue;
+            const uint64_t* T = tab + t * m;
+            int at = 0;
+            for (int step = top; step > 0; step >>= 1) {
+                const int q = at + step;  // T[q - 1] > key: at least q keys above
+                if (q <= m && T[q - 1] > ck) at = q;
+            }
+            if (at) atomicAdd(&crank[c], at);
+        }
+    }
+    __syncthreads();
+    if (key) {
+        const int rank = crank[tid];
+        if (rank < kk) {
+            ids[rank] = key_id(key);
+            scores[rank] = key_score(key);
+            if (rank == 0) *argmax = key_score(key) > -1e30f ? key_id(key) : 0;
+        }
+    }
+}
 // keys[i] = the (score desc, id asc) key of logits[i] (0: not a candidate).
 extern "C" __global__ __launch_bounds__(256) void bfp8_select_keys_kernel(const float* __restrict__ logits, int n,
                                                                           uint64_t* __restrict__ keys) {
@@ -284,6 +477,17 @@ hipError_t bfp8_launch_select_partials(const float* logits, int n, int topk, uin
 hipError_t bfp8_launch_select_sort(const float* logits, int n, int kk, uint64_t* keys, int* ids, float* scores,
                                    int* count, int* argmax, hipStream_t s) {
     if (n <= 0 || kk < 1 || kk > n || n > BFP8_SELECT_MAX) return hipErrorInvalidValue;
+    if (n <= BFP8_SELECT_RANK_MAX) {
+        const int nblk = (n + kSelBlock - 1) / kSelBlock;
+        uint32_t* valid = reinterpret_cast<uint32_t*>(keys + n);
+        hipLaunchKernelGGL(bfp8_select_block_sort_kernel, dim3(nblk), dim3(kBlkThreads), 0, s, logits, n, keys,
+                           valid);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(bfp8_select_rank_kernel, dim3(nblk * kRankParts), dim3(kSortThreads), 0, s, keys, valid,
+                           n, kk, ids, scores, count, argmax);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(bfp8_select_keys_kernel, dim3(select_grid(n, 256)), dim3(256), 0, s, logits, n, keys);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;

@@ -105,6 +105,31 @@ def test_bfp8_lm_head_device_any_arguments(gpu, V, k):
     assert int(am.item()) == ol.argmax(y)
 
 
+@pytest.mark.parametrize("k,ties", [(65, False), (200, False), (65586, False), (200, True), (65586, True)])
+def test_k_above_64_at_the_full_vocabulary(gpu, k, ties):
+    """k = 65, 200 and vocab + 50 over 65536 rows (bfp8_dev_lm_head_topk: the
+    scores, then the selection of 4096-key blocks sorted in LDS and ranked
+    against each other): ids and scores bit-exact against the oracle, the
+    count and argmax too; with mantissas in {-1, 0, 1} many scores are equal
+    and ids ascend among them."""
+    qk = gpu
+    import torch
+
+    V, H = 65536, 1024
+    mant, exps, x = planes(V, H, 6500 + k + ties, *((-1, 2) if ties else (-128, 128)))
+    y = ref_logits(x, mant, exps)
+    dm = qk.DeviceMatrix.from_soa(mant, exps)
+    _, xs, xsp = qk.quantize(torch.from_numpy(x).cuda())
+    say("k above 64 at 65536 rows", k, ties)
+    ids, sc, cnt, am = qk.lm_head_topk(dm, xsp, xs, k)
+    torch.cuda.synchronize()
+    ids_ref, sc_ref = ol.topk(y, k)
+    n = int(cnt.item())
+    assert n == ids_ref.size == min(k, V)
+    assert np.array_equal(ids.cpu().numpy()[:n], ids_ref) and same_f32(sc.cpu().numpy()[:n], sc_ref)
+    assert int(am.item()) == ol.argmax(y)
+
+
 @pytest.mark.parametrize("k", [40, 100])
 def test_top_k_on_a_second_stream_and_the_host_entry(gpu, k):
     """Scratch is per stream: a device-level top-k queued on a second stream
