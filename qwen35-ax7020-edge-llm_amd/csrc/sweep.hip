@@ -387,6 +387,20 @@ __device__ __forceinline__ void finish_unit(const Ctx& C, const Unit& U, const f
     __builtin_amdgcn_wave_barrier();
 }
 
+// B_start: a workgroup barrier that waits for this wavefront's LDS operations
+// only.  __syncthreads() would first wait for the control wavefront's loads
+// to LDS (a release covers them: vmcnt(0)), and the streaming wavefronts
+// would issue their first weight loads only when the table and the
+// activation are in, ~2 us into the launch; so the LDS words initialized
+// before it are what it publishes, and those loads are still in flight when
+// the weight loads go out.
+__device__ __forceinline__ void barrier_start() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // ---- the two roles -----------------------------------------------------------------------------
 // The control wavefront, unit by unit: between barriers B_j (the start of
 // unit j) and B_j+1 it takes unit j + 1 (the ticket overlaps finishing unit
@@ -413,7 +427,7 @@ __device__ void control_role(const Ctx& C, const Bfp8SweepGemv* gemvs, SweepLds&
     const bool head0 = C.ns > 0 && C.head_ntiles > 0;
     Unit U = head0 ? head_unit(C, 0) : no_unit();
     if (head0) issue_x(U, xin, lane);
-    __syncthreads();  // B_start
+    barrier_start();  // B_start
     wait_vm_all();
     if (!head0) {
         // published before its activation is read: the streaming wavefronts
@@ -458,7 +472,7 @@ __device__ void stream_role(const Ctx& C, int q, SweepLds& L, const uint32_t* xi
     // the first unit's chunks 0 and 1 go out before its activation is in
     // LDS (after the control wavefront's first loads: B_start); an lm_head
     // tile is known without the control wavefront
-    __syncthreads();  // B_start
+    barrier_start();  // B_start
     const bool head0 = C.ns > 0 && C.head_ntiles > 0;
     U = head0 ? head_unit(C, 0) : await_unit(L, 0);
     issue_chunk(c[0], U, 0, vw, ve);
