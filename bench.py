@@ -7,23 +7,24 @@ weight sweep at batch 1 -- per layer gate 3584x1024, up 3584x1024, down
 the 65536x1024 lm_head with fused greedy argmax + top-40.  Mantissas uniform
 in [-127, 127], exponents uniform in [124, 130] ([122, 128] for the lm_head),
 a fresh N(0,1) activation per GEMV (silu(a)*b with 1% +-20 outliers for the
-down projection).  One step = two persistent streaming launches: the
-lm_head's 1024 tiles (that launch also quantizes every activation: the
-lm_head's in each workgroup, the others one block per wavefront), then the
-other 120 GEMVs' tiles, whose workgroup 0 first merges the lm_head top-k;
-weights resident in HBM.  Plans without an lm_head quantize in a launch of
-their own first.  Weight copies rotate (2 sweeps = 1.08 GB) so the 256 MB
+down projection).  One step = one persistent launch (bfp8_sweep_kernel, 3
+five-wavefront workgroups per CU): each workgroup streams the lm_head's
+tiles dealt to it, then takes the other 120 GEMVs' tiles from ticket
+queues, quantizing every unit's activation itself; the last workgroup
+merges the lm_head's per-tile top-k lists as they are published.  Weights
+resident in HBM.  Weight copies rotate (2 sweeps = 1.08 GB) so the 256 MB
 Infinity Cache cannot serve repeats.
 
-roofline: the launch that moves the most bytes (the 120-GEMV launch for the
-sweep), timed alone with HIP events on its stream; its algorithmic bytes =
+roofline: the launch that moves the most bytes (for the sweep, its one
+launch), timed alone with HIP events on its stream; its algorithmic bytes =
 weights + int16 activations (2 B/element) + f32 block scales + f32 outputs.
 
 value = algorithmic bytes per sweep (weights once + f32 x in + f32 y out; the
 fused lm_head writes no logits) / wall time per step, in GB/s.
 
 Extra workloads for the per-config numbers: --workload lm_head (65536x1024
-fused top-40), gemv (3584x1024), down (1024x3584), batch16 (B=16 x 3584x1024),
+fused top-40), gemv (3584x1024), down (1024x3584), batch16 (B=16 x 3584x1024 and
+65536x1024), select (top-k above 64 at the lm_head),
 lm_head_bf16 (the reference's bf16 tied-embedding lm_head, top-64),
 forward_token (the reference's forward_token_c: 24 layers at the model's
 shapes with distinct synthetic weights + bf16 lm_head argmax, per token).
@@ -50,7 +51,8 @@ PKG = ROOT / "qwen35-ax7020-edge-llm_amd"
 sys.path.insert(0, str(PKG))
 
 PEAK_HBM_GBPS = 8000.0
-PEAK_VALU_INT_TOPS = 157.3  # v_dot4_i32_i8 with two passes per int16 activation (see bench_batch16)
+PEAK_MFMA_I8_TOPS = 5000.0  # dense int8 MFMA, MI355X (the batch kernel's integer part)
+VALU_LANE_OPS = 256 * 4 * 16 * 2.4e9  # 32-bit VALU lane operations per second, no packed math
 LAYER = [("gate", 3584, 1024), ("up", 3584, 1024), ("down", 1024, 3584), ("in_proj", 6144, 1024),
          ("out_proj", 1024, 2048)]
 N_LAYERS = 24
@@ -395,10 +397,16 @@ def bench_batch16(args, qk, torch, np):
     batch kernel (int8 MFMA for the exact residue sums, the float epilogue on
     the VALU).  roofline: HBM, with the kernel's algorithmic bytes (weights +
     int16 activations + f32 block scales + f32 outputs) over its time between
-    HIP events.  int_tops / valu_frac: algorithmic int-ops (2 per weight per
-    vector) against 157.3 TOP/s, the rate of v_dot4_i32_i8 on 256 CUs x 64
-    lanes x 8 int-ops x 2.4 GHz with two passes per int16 activation -- the
-    roof of a dot-product (non-MFMA) batch kernel."""
+    HIP events.  Its two floors beside it: hbm_floor_us (those bytes at
+    8 TB/s) and epilogue_floor_us, the float epilogue on the VALU at its
+    least -- per row, vector, block and residue an integer combine of the
+    two int8 parts' sums, a conversion, a multiply and an add (the
+    reference's order, no contraction), 4 lane-operations at 256 CUs x 4
+    SIMDs x 16 lanes x 2.4 GHz.  binding_floor_us is the larger, and
+    frac_of_binding_floor its ratio to the time.  mfma_tops: the int8 MFMA
+    operations (2 per weight, vector and activation part) per second, against
+    the 5.0 POP/s dense int8 peak.  3584 x 1024 is latency-bound (112 tiles:
+    both floors are under 1 us)."""
     B = 16
     lib = qk.load()
     s = torch.cuda.current_stream()
@@ -435,11 +443,17 @@ def bench_batch16(args, qk, torch, np):
             raise RuntimeError(f"bfp8_dev_gemv_batch failed: {set(rcs)}")
         us = a.elapsed_time(b) * 1e3 / args.steps
         gbs = (per_copy + B * 4 * K + B * 4 * M) / (us * 1e-6) / 1e9
-        tops = 2.0 * M * K * B / (us * 1e-6) / 1e12
+        mfma_tops = 2.0 * 2 * M * K * B / (us * 1e-6) / 1e12
         kbytes = per_copy + B * (2 * K + 4 * (K // 64)) + B * 4 * M
         kgbs = kbytes / (us * 1e-6) / 1e9
-        shapes.append({"M": M, "K": K, "B": B, "us": round(us, 3), "GBps": round(gbs, 2), "int_tops": round(tops, 3),
-                       "valu_frac": round(tops / PEAK_VALU_INT_TOPS, 4), "rotating_copies": copies,
+        hbm_floor = kbytes / (PEAK_HBM_GBPS * 1e9) * 1e6
+        epi_floor = 4.0 * M * B * (K // 64) * 4 / VALU_LANE_OPS * 1e6
+        floor = max(hbm_floor, epi_floor)
+        shapes.append({"M": M, "K": K, "B": B, "us": round(us, 3), "GBps": round(gbs, 2),
+                       "mfma_tops": round(mfma_tops, 3), "mfma_frac": round(mfma_tops / PEAK_MFMA_I8_TOPS, 4),
+                       "hbm_floor_us": round(hbm_floor, 3), "epilogue_floor_us": round(epi_floor, 3),
+                       "binding_floor_us": round(floor, 3), "frac_of_binding_floor": round(floor / us, 4),
+                       "rotating_copies": copies,
                        "roofline": {"bound": "hbm", "achieved": round(kgbs, 2), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                                     "frac": round(kgbs / PEAK_HBM_GBPS, 4), "algorithmic_bytes": kbytes,
                                     "traffic": read_traffic("batch16", f"bfp8_gemv_batch_mfma_kernel@{M}x{K}")}})
@@ -453,7 +467,8 @@ def bench_batch16(args, qk, torch, np):
     first = shapes[0]
     out = {"metric": "BFP8 GEMV B=16 achieved GB/s and int Tops/s", "value": first["GBps"],
            "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-           "us_per_step": first["us"], "int_tops": first["int_tops"], "valu_frac": first["valu_frac"],
+           "us_per_step": first["us"], "mfma_tops": first["mfma_tops"],
+           "epilogue_floor_us": first["epilogue_floor_us"], "frac_of_binding_floor": first["frac_of_binding_floor"],
            "higher_is_better": True,
            "dtype": "int8xint16->int32, f32 epilogue", "data": "synthetic",
            "config": {"workload": "batch16", "M": first["M"], "K": first["K"], "B": B},
@@ -469,8 +484,9 @@ def bench_batch16(args, qk, torch, np):
 def bench_select(args, qk, torch, np):
     """k above 64 at the 65536 x 1024 lm_head (bfp8_dev_lm_head_topk): the
     scores (the plain GEMV into the stream's scratch), then the selection --
-    16 blocks of 4096 keys sorted in LDS, each block's first min(k, 4096)
-    keys ranked against every block's -- for k = 65, 200 and vocab + 50.
+    32 blocks of 2048 keys sorted in LDS and registers, each block's first
+    min(k, 2048) keys ranked against every block's -- for k = 65, 200 and
+    vocab + 50.
     Per k: the call, and the GEMV alone on the same inputs (the difference is
     the selection's)."""
     V, H = 65536, 1024
