@@ -226,7 +226,11 @@ __device__ __forceinline__ void mf_group(MfState<kRes>& st, MfLds& L, const MfLo
 
 // kHalves: halves of a tile per workgroup (2: both, workgroup per tile; 1:
 // workgroup per 32-row half, twice the workgroups for GEMVs with few tiles).
-template <int kRes, int kHalves>
+// kDepth: weight-load groups in flight per wavefront (2: one group computed
+// while the next loads; kMfChunk / kMfGroup: a chunk's every weight load
+// issued at once, for GEMVs with too few tiles to fill the memory system
+// otherwise).
+template <int kRes, int kHalves, int kDepth>
 __global__ __launch_bounds__(64 * kHalves * (4 / kRes)) __attribute__((amdgpu_waves_per_eu(4))) void bfp8_gemv_batch_mfma_kernel(
     float* __restrict__ Y, const uint32_t* __restrict__ xsplit, const float* __restrict__ xscale,
     const uint8_t* __restrict__ mant, const uint8_t* __restrict__ exps, int M, int K, int B) {
@@ -255,16 +259,17 @@ __global__ __launch_bounds__(64 * kHalves * (4 / kRes)) __attribute__((amdgpu_wa
     constexpr int NT = 64 * kHalves * (4 / kRes);
     MfStaged<NT> S0;
     mf_stage_load<NT>(S0, xsplit, xscale, nb, B, 0, min(kMfChunk, nb));
-    MfLoads<kRes> A, Bq;
-    mf_issue<kRes>(A, wrs, ers, wv, ev, 0);
-    mf_issue<kRes>(Bq, wrs, ers, wv, ev, 1);
+    MfLoads<kRes> ld[kDepth];
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) mf_issue<kRes>(ld[d], wrs, ers, wv, ev, d);
     mf_stage_store<NT>(L, S0);
-    for (int gi = 0; gi < ng; gi += 2) {
-        // two load sets in alternating roles: the next group is always in flight
-        mf_group<kRes, NT>(st, L, A, gi, nb, xsplit, xscale, B, q0, lane);
-        mf_issue<kRes>(A, wrs, ers, wv, ev, gi + 2);
-        if (gi + 1 < ng) mf_group<kRes, NT>(st, L, Bq, gi + 1, nb, xsplit, xscale, B, q0, lane);
-        mf_issue<kRes>(Bq, wrs, ers, wv, ev, gi + 3);
+    for (int gi = 0; gi < ng; gi += kDepth) {
+        // kDepth load sets in turn: set d holds group gi + d, then gi + d + kDepth
+#pragma unroll
+        for (int d = 0; d < kDepth; ++d) {
+            if (gi + d < ng) mf_group<kRes, NT>(st, L, ld[d], gi + d, nb, xsplit, xscale, B, q0, lane);
+            mf_issue<kRes>(ld[d], wrs, ers, wv, ev, gi + d + kDepth);
+        }
     }
     float (&fs)[kRes][8] = st.fs;
 
@@ -309,10 +314,10 @@ hipError_t bfp8_launch_gemv_batch_mfma(float* Y, const uint32_t* xsplit, const f
     // few tiles: one residue per wavefront and a workgroup per 32-row half
     // (8 wavefronts per tile over two CUs) so that more run
     if (nt < 512)
-        hipLaunchKernelGGL((bfp8_gemv_batch_mfma_kernel<1, 1>), dim3(2 * nt), dim3(256), 0, s, Y, xsplit, xscale, mant,
-                           exps, M, K, B);
+        hipLaunchKernelGGL((bfp8_gemv_batch_mfma_kernel<1, 1, kMfChunk / kMfGroup>), dim3(2 * nt), dim3(256), 0, s, Y,
+                           xsplit, xscale, mant, exps, M, K, B);
     else
-        hipLaunchKernelGGL((bfp8_gemv_batch_mfma_kernel<2, 2>), dim3(nt), dim3(256), 0, s, Y, xsplit, xscale, mant,
+        hipLaunchKernelGGL((bfp8_gemv_batch_mfma_kernel<2, 2, 2>), dim3(nt), dim3(256), 0, s, Y, xsplit, xscale, mant,
                            exps, M, K, B);
     return hipGetLastError();
 }
