@@ -169,8 +169,9 @@ struct Bfp8SweepArgs {
     int ticket0;           // the queue unit the first ticket of sub-queue 0 stands for
     int nqueues;           // sub-queues (1, or up to BFP8_SWEEP_QUEUES with 8 nqueues <= the grid): sub-queue
                            // s holds units ticket0 + s + nqueues t, taken by workgroups (w / 8) mod nqueues = s
-    uint32_t* counters;    // BFP8_SWEEP_QUEUES tickets-taken counters, then the finished-workgroup count
-                           // (BFP8_SWEEP_CTR_STRIDE words apart; zero between launches)
+    uint32_t* counters;    // this launch's BFP8_SWEEP_QUEUES tickets-taken counters (BFP8_SWEEP_CTR_STRIDE
+                           // words apart), zero when it starts
+    uint32_t* counters_next;  // the other set (the previous launch's): zeroed by this launch for the next
     // the lm_head (head_ntiles > 0): workgroup w < grid - 1 takes its tiles w, w + grid - 1, ...
     // first; the last workgroup merges their top-k lists
     const uint8_t* head_mant;
@@ -190,7 +191,8 @@ struct Bfp8SweepArgs {
 #define BFP8_SWEEP_WG_PER_CU 3
 #define BFP8_SWEEP_QUEUES 64
 #define BFP8_SWEEP_CTR_STRIDE 1024  // words (4 KiB apart: counters in different memory channels)
-#define BFP8_SWEEP_CTR_BYTES ((BFP8_SWEEP_QUEUES + 1) * BFP8_SWEEP_CTR_STRIDE * 4)
+// Two counter sets: launches of a plan take them in turn.
+#define BFP8_SWEEP_CTR_BYTES (2 * BFP8_SWEEP_QUEUES * BFP8_SWEEP_CTR_STRIDE * 4)
 // Units of a sweep launch have an even number of 4-block chunks (nb % 8 == 0,
 // 8 <= nb <= 64): their chunks alternate between two register buffers.
 #define BFP8_SWEEP_MIN_NB 8

@@ -1123,6 +1123,7 @@ struct Plan {
     bool sweep = false;
     DevBuf s_gemvs, s_counters;
     int s_nwg = 0, s_ngemv = 0, s_nunits = 0;
+    uint32_t s_launches = 0;       // of the single launch: its counter set is s_launches % 2
     uint32_t epoch = 0;            // of the last launch; the partials start zeroed (epoch 0)
 };
 
@@ -1441,7 +1442,12 @@ int bfp8_plan_launch(void* plan, int stage, void* stream) {
         a.gemvs = p->s_gemvs.as<Bfp8SweepGemv>();
         a.ngemv = p->s_ngemv;
         a.nunits = p->s_nunits;
-        a.counters = p->s_counters.as<uint32_t>();
+        {
+            uint32_t* sets = p->s_counters.as<uint32_t>();
+            const int cur = (int)(p->s_launches & 1u);  // counted below once the launch is made
+            a.counters = sets + cur * BFP8_SWEEP_QUEUES * BFP8_SWEEP_CTR_STRIDE;
+            a.counters_next = sets + (1 - cur) * BFP8_SWEEP_QUEUES * BFP8_SWEEP_CTR_STRIDE;
+        }
         a.nqueues = sweep_queues(p->s_nwg);
         if (p->topk_desc >= 0) {
             const Bfp8GemvDesc& hd = p->hdesc[p->topk_desc];
@@ -1465,6 +1471,7 @@ int bfp8_plan_launch(void* plan, int stage, void* stream) {
         p->epoch = p->epoch % 16383u + 1u;
         a.epoch = p->epoch;
         HIP_OK(bfp8_launch_sweep(a, p->s_nwg, s));
+        ++p->s_launches;
         return BFP8_OK;
     }
     if (stage == 0) {

@@ -34,9 +34,10 @@
 //     dispatched to the 8 XCDs in turn, so each sub-queue is shared by
 //     workgroups of every XCD and of several dispatch slots of a CU: the
 //     memory system serves XCDs and slots at different rates, and sub-queues
-//     tied to one XCD ended up to 15 us apart.  The counters are reset by the
-//     last workgroup to finish, so a launch leaves them as it found them
-//     (zero).
+//     tied to one XCD ended up to 15 us apart.  A plan's launches take two
+//     counter sets in turn: a launch starts with its set at zero and zeroes
+//     the other (the previous launch's, which ended before it began) for the
+//     next, so no workgroup waits at its end for a count of finished ones.
 //   * The lm_head's tiles publish their top-k lists as epoch-tagged keys
 //     (topk_merge.h: one agent-scope atomic 64-bit store per key) and the last
 //     workgroup of the grid only merges them, from the start of the launch:
@@ -537,6 +538,11 @@ extern "C" __global__ __launch_bounds__(kThreads) void bfp8_sweep_kernel(Bfp8Swe
     else
         C.ns = C.wg < a.nunits ? 1 : 0;
 
+    // the other counter set, for the next launch: the last workgroup's fifth
+    // wavefront (idle in the merging workgroup), one lane per counter
+    if (C.wg == C.nwg - 1 && wave == kStreamWaves && C.lane < a.nqueues)
+        __hip_atomic_store(a.counters_next + C.lane * BFP8_SWEEP_CTR_STRIDE, 0u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
     if (head && C.wg == C.nwg - 1) {
         // the merging workgroup: four wavefronts merge the lm_head's lists as
         // they are published (the fifth ends here; a barrier waits only for
@@ -550,19 +556,6 @@ extern "C" __global__ __launch_bounds__(kThreads) void bfp8_sweep_kernel(Bfp8Swe
         return;
     } else {
         stream_role(C, wave, L, xin);
-    }
-    // the last workgroup to finish leaves the counters at zero for the next
-    // launch (a workgroup's tickets were all taken before its streaming
-    // wavefronts passed their last barrier)
-    if (threadIdx.x == 0) {
-        uint32_t* done = a.counters + BFP8_SWEEP_QUEUES * BFP8_SWEEP_CTR_STRIDE;
-        const uint32_t d = __hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (d == (uint32_t)C.nwg - 1u) {
-            for (int i = 0; i < a.nqueues; ++i)
-                __hip_atomic_store(a.counters + i * BFP8_SWEEP_CTR_STRIDE, 0u, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
     }
 }
 

@@ -866,7 +866,9 @@ def test_sweep_plan_24_layers_and_lm_head(gpu, torch_mod, with_head):
     """The full synthetic decode sweep in one plan: 24 x {gate, up, down, in, out}
     plus the fused lm_head (or without it: every tile from the queue), in the
     single launch, every output bit-exact, three runs in a row (the second
-    with new activations written in place)."""
+    with new activations written in place; the runs take the plan's two
+    ticket-counter sets in turn, so the third depends on the second having
+    zeroed the first's)."""
     qk, torch = gpu, torch_mod
     shapes = [(3584, 1024), (3584, 1024), (1024, 3584), (6144, 1024), (1024, 2048)]
     items, refs = [], []
