@@ -50,7 +50,7 @@ def test_profiles_hold_the_traffic_the_bench_reports():
         return bench.wbytes(M, K) + B * (2 * K + 4 * (K // 64)) + B * 4 * M
 
     cases = [
-        ("sweep", "bfp8_gemv_grouped_merge_kernel", bench.kernel_bytes(items("sweep", lm=False))),
+        ("sweep", "bfp8_sweep_kernel", bench.metric_bytes(items("sweep"))),  # the single launch
         ("lm_head", "bfp8_gemv_head_kernel", bench.kernel_bytes(items("lm_head", lm=True))),
         ("gemv", "rt_rows_gemv_kernel", bench.kernel_bytes(items("gemv"))),
         ("down", "rt_rows_gemv_kernel", bench.kernel_bytes(items("down"))),
