@@ -34,7 +34,9 @@
 // residues; the wavefronts of a half combine their fs_q into y at the end
 // through LDS.  GEMVs with many tiles: a workgroup per tile, 2 residues per
 // wavefront.  GEMVs with few tiles: a workgroup per half, 1 residue per
-// wavefront, so that more wavefronts run on more CUs.
+// wavefront, every weight load of a chunk in flight at once, and (more than
+// 8 vectors) a workgroup per half of the vectors too, so that more
+// wavefronts, each with a shorter epilogue chain, run on more CUs.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -84,7 +86,9 @@ struct MfStaged {
 // 16 bytes of xsplit = one part of one residue (both k halves): item
 // ((u * 4 + q) * 2 + p) * 16 + v, vectors fastest, so the LDS stores of
 // consecutive threads are consecutive
-template <int NT>
+// kVH: -1 every vector, else only vectors 8 kVH .. 8 kVH + 7 (the others
+// staged as zeros: their MFMA rows are computed and not used).
+template <int NT, int kVH>
 __device__ __forceinline__ void mf_stage_load(MfStaged<NT>& S, const uint32_t* __restrict__ xsplit,
                                               const float* __restrict__ xscale, int nb, int B, int c0, int nbc) {
 #pragma unroll
@@ -92,14 +96,15 @@ __device__ __forceinline__ void mf_stage_load(MfStaged<NT>& S, const uint32_t* _
         const int i = threadIdx.x + j * NT;
         const int v = i % kMfVec, p = (i / kMfVec) % 2, q = (i / (2 * kMfVec)) % 4, u = i / (8 * kMfVec);
         S.val[j] = u32x4{0u, 0u, 0u, 0u};
-        if (v < B && u < nbc)
+        if (v < B && (kVH < 0 || (v >> 3) == kVH) && u < nbc)
             S.val[j] = *reinterpret_cast<const u32x4*>(
                 xsplit + ((size_t)v * nb + c0 + u) * BFP8_XSPLIT_WORDS_PER_BLOCK + q * 8 + p * 4);
     }
 #pragma unroll
     for (int j = 0; j < MfStaged<NT>::kScaleRounds; ++j) {
         const int i = threadIdx.x + j * NT, v = i % kMfVec, u = i / kMfVec;
-        S.xs[j] = (i < kMfScales && v < B && u < nbc) ? xscale[(size_t)v * nb + c0 + u] : 0.0f;
+        S.xs[j] = (i < kMfScales && v < B && (kVH < 0 || (v >> 3) == kVH) && u < nbc) ? xscale[(size_t)v * nb + c0 + u]
+                                                                                        : 0.0f;
     }
 }
 
@@ -136,9 +141,18 @@ __device__ __forceinline__ void mf_stage_store(MfLds& L, const MfStaged<NT>& S) 
     __syncthreads();
 }
 
-template <int kRes>
+// A lane's result slots: register i of the MFMA result (and i + 8, the low
+// parts) is vector 8(i/4) + 4*kh + i%4 of the lane's row; every vector: slots
+// i = 0..7; vector half kVH: slots i = 4 kVH .. 4 kVH + 3.
+template <int kVH>
+struct MfSlots {
+    static constexpr int n = kVH < 0 ? 8 : 4;
+    static constexpr int i0 = kVH < 0 ? 0 : 4 * kVH;
+};
+
+template <int kRes, int kVH>
 struct MfState {
-    float fs[kRes][8];  // [residue of the group][i]: vector 8(i/4) + 4*kh + i%4, the lane's row
+    float fs[kRes][MfSlots<kVH>::n];  // [residue of the group][slot]
 };
 
 template <int kRes>
@@ -148,40 +162,45 @@ struct MfLoads {
 };
 
 // One block: an MFMA per residue of the group and the epilogue.
-template <int kRes>
-__device__ __forceinline__ void mf_block(MfState<kRes>& st, const MfLds& L, const uint64_t (&w)[kRes], uint32_t e,
+template <int kRes, int kVH>
+__device__ __forceinline__ void mf_block(MfState<kRes, kVH>& st, const MfLds& L, const uint64_t (&w)[kRes], uint32_t e,
                                          int u, int q0, int lane) {
+    constexpr int NS = MfSlots<kVH>::n, I0 = MfSlots<kVH>::i0;
     i32x16 d[kRes];
     const i32x16 zero = {};
 #pragma unroll
     for (int r = 0; r < kRes; ++r)
         d[r] = __builtin_amdgcn_mfma_i32_32x32x16_i8((long)L.xa[u][q0 + r][lane], (long)w[r], zero, 0, 0, 0);
     const int kh = lane >> 5;
-    const f32x4 xa = *reinterpret_cast<const f32x4*>(&L.xs[u][4 * kh]);
-    const f32x4 xb = *reinterpret_cast<const f32x4*>(&L.xs[u][8 + 4 * kh]);
-    const float xs[8] = {xa[0], xa[1], xa[2], xa[3], xb[0], xb[1], xb[2], xb[3]};
+    float xs[NS];
+#pragma unroll
+    for (int h = 0; h < NS / 4; ++h) {  // slots 4h..4h+3: vectors 8 (I0 / 4 + h) + 4 kh ..
+        const f32x4 x4 = *reinterpret_cast<const f32x4*>(&L.xs[u][8 * (I0 / 4 + h) + 4 * kh]);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) xs[4 * h + m] = x4[m];
+    }
     const float es = exp_scale_ftz(e);
     const int lo = L.lo[u], hi = L.hi[u];
     const bool one_product = (e < 8u) | ((uint32_t)((int)e - lo) <= (uint32_t)(hi - lo));
     if (__builtin_amdgcn_ballot_w64(!one_product) == 0) {
-        float c[8];
+        float c[NS];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) c[i] = es * xs[i];
+        for (int k = 0; k < NS; ++k) c[k] = es * xs[k];
 #pragma unroll
         for (int r = 0; r < kRes; ++r)
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int S = (int)((uint32_t)d[r][i] << 8) + d[r][i + 8];
-                st.fs[r][i] = st.fs[r][i] + (float)S * c[i];
+            for (int k = 0; k < NS; ++k) {
+                const int S = (int)((uint32_t)d[r][I0 + k] << 8) + d[r][I0 + k + 8];
+                st.fs[r][k] = st.fs[r][k] + (float)S * c[k];
             }
     } else {
 #pragma unroll
         for (int r = 0; r < kRes; ++r)
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int S = (int)((uint32_t)d[r][i] << 8) + d[r][i + 8];
+            for (int k = 0; k < NS; ++k) {
+                const int S = (int)((uint32_t)d[r][I0 + k] << 8) + d[r][I0 + k + 8];
                 const float t1 = (float)S * es;
-                st.fs[r][i] = st.fs[r][i] + t1 * xs[i];
+                st.fs[r][k] = st.fs[r][k] + t1 * xs[k];
             }
     }
 }
@@ -206,59 +225,56 @@ __device__ __forceinline__ void mf_issue(MfLoads<kRes>& ld, __amdgpu_buffer_rsrc
     ld.e = load_e(ers, ev + (gi * kMfGroup / 4) * 256, 0);
 }
 
-template <int kRes, int NT>
-__device__ __forceinline__ void mf_group(MfState<kRes>& st, MfLds& L, const MfLoads<kRes>& ld, int gi, int nb,
+template <int kRes, int NT, int kVH>
+__device__ __forceinline__ void mf_group(MfState<kRes, kVH>& st, MfLds& L, const MfLoads<kRes>& ld, int gi, int nb,
                                          const uint32_t* __restrict__ xsplit, const float* __restrict__ xscale, int B,
                                          int q0, int lane) {
     const int b0 = gi * kMfGroup;
     if (b0 % kMfChunk == 0 && b0 > 0) {  // the first chunk is staged before the loop
         __syncthreads();  // every wavefront is done with the previous chunk
         MfStaged<NT> S;
-        mf_stage_load<NT>(S, xsplit, xscale, nb, B, b0, min(kMfChunk, nb - b0));
+        mf_stage_load<NT, kVH>(S, xsplit, xscale, nb, B, b0, min(kMfChunk, nb - b0));
         mf_stage_store<NT>(L, S);
     }
 #pragma unroll
     for (int uu = 0; uu < kMfGroup; ++uu) {
         if (b0 + uu >= nb) break;
-        mf_block<kRes>(st, L, ld.w[uu], (ld.e >> (8 * ((b0 + uu) & 3))) & 0xffu, (b0 + uu) % kMfChunk, q0, lane);
+        mf_block<kRes, kVH>(st, L, ld.w[uu], (ld.e >> (8 * ((b0 + uu) & 3))) & 0xffu, (b0 + uu) % kMfChunk, q0, lane);
     }
 }
 
-// kHalves: halves of a tile per workgroup (2: both, workgroup per tile; 1:
-// workgroup per 32-row half, twice the workgroups for GEMVs with few tiles).
+// The work of one workgroup: tile t, its 32-row half s (kHalves == 1) or both
+// (kHalves == 2, wavefront w takes half w & 1), the residues of group grp,
+// the vectors of kVH (every vector, or one half of them).
 // kDepth: weight-load groups in flight per wavefront (2: one group computed
 // while the next loads; kMfChunk / kMfGroup: a chunk's every weight load
 // issued at once, for GEMVs with too few tiles to fill the memory system
 // otherwise).
-template <int kRes, int kHalves, int kDepth>
-__global__ __launch_bounds__(64 * kHalves * (4 / kRes)) __attribute__((amdgpu_waves_per_eu(4))) void bfp8_gemv_batch_mfma_kernel(
-    float* __restrict__ Y, const uint32_t* __restrict__ xsplit, const float* __restrict__ xscale,
-    const uint8_t* __restrict__ mant, const uint8_t* __restrict__ exps, int M, int K, int B) {
-    __shared__ MfLds L;
+template <int kRes, int kHalves, int kDepth, int kVH>
+__device__ __forceinline__ void mf_body(MfLds& L, float* __restrict__ Y, const uint32_t* __restrict__ xsplit,
+                                        const float* __restrict__ xscale, const uint8_t* __restrict__ mant,
+                                        const uint8_t* __restrict__ exps, int M, int K, int B, int t, int s, int grp) {
+    constexpr int NS = MfSlots<kVH>::n, I0 = MfSlots<kVH>::i0;
     const int lane = threadIdx.x & 63;
-    const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
-    // 32-row half, residue group
-    const int s = kHalves == 2 ? (w & 1) : (int)(blockIdx.x & 1), grp = kHalves == 2 ? (w >> 1) : w;
     const int q0 = grp * kRes;
     const int col = lane & 31, kh = lane >> 5;
-    const int t = kHalves == 2 ? (int)blockIdx.x : (int)(blockIdx.x >> 1);
     const int nb = K >> 6, nb4 = (nb + 3) >> 2;
     const __amdgpu_buffer_rsrc_t wrs = make_rsrc(mant + (size_t)t * nb * 4096u, (uint32_t)nb * 4096u);
     const __amdgpu_buffer_rsrc_t ers = make_rsrc(exps + (size_t)t * nb4 * 256u, (uint32_t)nb4 * 256u);
     const int wv = q0 * 1024 + (32 * s + col) * 16 + kh * 8;
     const int ev = (32 * s + col) * 4;
-    MfState<kRes> st;
+    MfState<kRes, kVH> st;
 #pragma unroll
     for (int r = 0; r < kRes; ++r)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) st.fs[r][i] = 0.0f;
+        for (int k = 0; k < NS; ++k) st.fs[r][k] = 0.0f;
     const int ng = (nb + kMfGroup - 1) / kMfGroup;
-    // the first chunk's activation loads go out first, then the first two
+    // the first chunk's activation loads go out first, then the first
     // weight groups: the staging then waits for its own loads only (a
     // wavefront's loads complete in the order issued)
     constexpr int NT = 64 * kHalves * (4 / kRes);
     MfStaged<NT> S0;
-    mf_stage_load<NT>(S0, xsplit, xscale, nb, B, 0, min(kMfChunk, nb));
+    mf_stage_load<NT, kVH>(S0, xsplit, xscale, nb, B, 0, min(kMfChunk, nb));
     MfLoads<kRes> ld[kDepth];
 #pragma unroll
     for (int d = 0; d < kDepth; ++d) mf_issue<kRes>(ld[d], wrs, ers, wv, ev, d);
@@ -267,39 +283,72 @@ __global__ __launch_bounds__(64 * kHalves * (4 / kRes)) __attribute__((amdgpu_wa
         // kDepth load sets in turn: set d holds group gi + d, then gi + d + kDepth
 #pragma unroll
         for (int d = 0; d < kDepth; ++d) {
-            if (gi + d < ng) mf_group<kRes, NT>(st, L, ld[d], gi + d, nb, xsplit, xscale, B, q0, lane);
+            if (gi + d < ng) mf_group<kRes, NT, kVH>(st, L, ld[d], gi + d, nb, xsplit, xscale, B, q0, lane);
             mf_issue<kRes>(ld[d], wrs, ers, wv, ev, gi + d + kDepth);
         }
     }
-    float (&fs)[kRes][8] = st.fs;
+    float (&fs)[kRes][NS] = st.fs;
 
     // y = (fs_0 + fs_2) + (fs_1 + fs_3): the other residue groups of the half
     // hand their sums to group 0 through the (no longer needed) staging area
     __syncthreads();
-    float* xch = reinterpret_cast<float*>(&L.xa[0][0][0]);  // [group - 1][half][residue][i][lane]
+    float* xch = reinterpret_cast<float*>(&L.xa[0][0][0]);  // [group - 1][half][residue][slot][lane]
     if (grp > 0) {
 #pragma unroll
         for (int r = 0; r < kRes; ++r)
 #pragma unroll
-            for (int i = 0; i < 8; ++i) xch[((((grp - 1) * 2 + s) * kRes + r) * 8 + i) * 64 + lane] = fs[r][i];
+            for (int k = 0; k < NS; ++k) xch[((((grp - 1) * 2 + s) * kRes + r) * NS + k) * 64 + lane] = fs[r][k];
     }
     __syncthreads();
     if (grp == 0) {
         const int row = t * 64 + 32 * s + col;
         const int pair_rows = M & ~1;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int k = 0; k < NS; ++k) {
             float f[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int gq = q / kRes, rq = q % kRes;
-                f[q] = gq == 0 ? fs[rq][i] : xch[((((gq - 1) * 2 + s) * kRes + rq) * 8 + i) * 64 + lane];
+                f[q] = gq == 0 ? fs[rq][k] : xch[((((gq - 1) * 2 + s) * kRes + rq) * NS + k) * 64 + lane];
             }
+            const int i = I0 + k;
             const int v = 8 * (i / 4) + 4 * kh + (i % 4);
             const float y = (f[0] + f[2]) + (f[1] + f[3]);
             if (v < B && row < pair_rows) Y[(size_t)v * M + row] = y;
         }
     }
+}
+
+// kHalves: halves of a tile per workgroup (2: both, workgroup per tile; 1:
+// workgroup per 32-row half, twice the workgroups for GEMVs with few tiles).
+// kSplit: 1, every vector in each workgroup; 2, a workgroup per half of the
+// vectors, each wavefront then finishing 4 of the 8 result slots of its
+// lanes -- half the epilogue per wavefront, on twice the wavefronts, for
+// GEMVs whose wavefronts are too few to hide the epilogue's latencies.  The
+// two workgroups of a unit are blocks 16a + x and 16a + 8 + x (x < 8), which
+// go to the same XCD (blocks are dealt to the 8 XCDs in turn), so the second
+// reads the unit's weights from that XCD's L2; unit 8a + x, blocks past the
+// last unit exit at once.
+template <int kRes, int kHalves, int kDepth, int kSplit>
+__global__ __launch_bounds__(64 * kHalves * (4 / kRes)) __attribute__((amdgpu_waves_per_eu(kSplit == 2 ? 2 : 4))) void
+bfp8_gemv_batch_mfma_kernel(float* __restrict__ Y, const uint32_t* __restrict__ xsplit,
+                            const float* __restrict__ xscale, const uint8_t* __restrict__ mant,
+                            const uint8_t* __restrict__ exps, int M, int K, int B) {
+    __shared__ MfLds L;
+    const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int b = (int)blockIdx.x;
+    const int bid = kSplit == 2 ? 8 * (b >> 4) + (b & 7) : b;
+    const int nunits = kHalves == 2 ? bfp8_ntiles(M) : 2 * bfp8_ntiles(M);
+    if (kSplit == 2 && bid >= nunits) return;  // the grid's last 16 blocks may hold fewer units
+    // 32-row half, residue group, tile
+    const int s = kHalves == 2 ? (w & 1) : (bid & 1), grp = kHalves == 2 ? (w >> 1) : w;
+    const int t = kHalves == 2 ? bid : (bid >> 1);
+    if (kSplit == 1)
+        mf_body<kRes, kHalves, kDepth, -1>(L, Y, xsplit, xscale, mant, exps, M, K, B, t, s, grp);
+    else if (((b >> 3) & 1) == 0)
+        mf_body<kRes, kHalves, kDepth, 0>(L, Y, xsplit, xscale, mant, exps, M, K, B, t, s, grp);
+    else
+        mf_body<kRes, kHalves, kDepth, 1>(L, Y, xsplit, xscale, mant, exps, M, K, B, t, s, grp);
 }
 
 }  // namespace
@@ -313,11 +362,14 @@ hipError_t bfp8_launch_gemv_batch_mfma(float* Y, const uint32_t* xsplit, const f
     if (B < 1 || B > kMfVec || K < 64) return hipErrorInvalidValue;
     // few tiles: one residue per wavefront and a workgroup per 32-row half
     // (8 wavefronts per tile over two CUs) so that more run
-    if (nt < 512)
-        hipLaunchKernelGGL((bfp8_gemv_batch_mfma_kernel<1, 1, kMfChunk / kMfGroup>), dim3(2 * nt), dim3(256), 0, s, Y,
-                           xsplit, xscale, mant, exps, M, K, B);
+    if (nt < 512 && B > 8)  // and a workgroup per half of the vectors: 2 nt units, 16 blocks per 8
+        hipLaunchKernelGGL((bfp8_gemv_batch_mfma_kernel<1, 1, kMfChunk / kMfGroup, 2>), dim3(16 * ((2 * nt + 7) / 8)),
+                           dim3(256), 0, s, Y, xsplit, xscale, mant, exps, M, K, B);
+    else if (nt < 512)
+        hipLaunchKernelGGL((bfp8_gemv_batch_mfma_kernel<1, 1, kMfChunk / kMfGroup, 1>), dim3(2 * nt), dim3(256), 0, s,
+                           Y, xsplit, xscale, mant, exps, M, K, B);
     else
-        hipLaunchKernelGGL((bfp8_gemv_batch_mfma_kernel<2, 2, 2>), dim3(nt), dim3(256), 0, s, Y, xsplit, xscale, mant,
-                           exps, M, K, B);
+        hipLaunchKernelGGL((bfp8_gemv_batch_mfma_kernel<2, 2, 2, 1>), dim3(nt), dim3(256), 0, s, Y, xsplit, xscale,
+                           mant, exps, M, K, B);
     return hipGetLastError();
 }
