@@ -105,6 +105,8 @@ hipError_t bfp8_launch_gemv_wide_grouped(const Bfp8GemvDesc* descs_dev, const Bf
                                          int max_nb, hipStream_t s);
 // Stand-alone final top-k merge of partials an earlier launch wrote.
 hipError_t bfp8_launch_topk_merge(const Bfp8GemvDesc& d, hipStream_t s);
+// Name of the stand-alone merge kernel bfp8_launch_topk_merge runs for an M-row lm_head.
+const char* bfp8_topk_merge_kernel_name(int M);
 // Persistent grouped launch: workgroup w walks tiles_dev[wg_off_dev[w] ..
 // wg_off_dev[w+1]); nwg <= bfp8_stream_grid().  merge_desc >= 0: workgroup 0
 // first merges the top-k partials of descs_dev[merge_desc] (written by an

@@ -1547,7 +1547,7 @@ const char* bfp8_plan_kernel_name(void* plan, int stage) {
         if (p->rest.wide) return "bfp8_gemv_wide_grouped_kernel";
         if (fold) return "bfp8_gemv_grouped_merge_kernel";
         if (p->rest.nwg > 0) return "bfp8_gemv_grouped_kernel";
-        return p->topk_desc >= 0 ? "bfp8_topk_merge_kernel" : "";
+        return p->topk_desc >= 0 ? bfp8_topk_merge_kernel_name(p->hdesc[p->topk_desc].M) : "";
     }
     if (stage == 2) {
         if (!p->odd_items.empty()) return "bfp8_tail_row_kernel";

@@ -582,7 +582,7 @@ def test_rows_kernel_quantizes_special_blocks(gpu, torch_mod, M, K, inf):
     plan.close()
 
 
-@pytest.mark.parametrize("shape", ["alone", "alone_65536", "alone_ragged_2049_tiles", "alone_k1",
+@pytest.mark.parametrize("shape", ["alone", "alone_65536", "alone_1536_tiles", "alone_ragged_2049_tiles", "alone_k1",
                                    "with_small_gemv", "ragged_2049_tiles", "queue_gemv", "queue_ragged_2049_tiles",
                                    "queue_k1", "queue_small_vocab"])
 def test_plan_lm_head_merge_paths(gpu, torch_mod, shape):
@@ -590,14 +590,15 @@ def test_plan_lm_head_merge_paths(gpu, torch_mod, shape):
     launch (with a 2048 x 1024 GEMV: the 2049-tile vocabulary gives some
     workgroups three lm_head tiles, a 64-tile one leaves most workgroups to
     start from the queue, and k = 1), as the stand-alone merge kernel after
-    the per-tile lists (a lone lm_head: 256, 1024 and a ragged 2049 tiles, and
+    the per-tile lists (a lone lm_head: 256 and 1024 tiles, 1536 in the wide
+    form that reads eight passes of list heads, a ragged 2049 tiles, and
     k = 1), or folded into workgroup 0 of the second launch (another GEMV too
     narrow for the single launch, here 128 x 256); a 2049-tile ragged
     vocabulary takes several passes over the list heads.  Later runs use new
     activations written in place: every activation is quantized again (no
     stale records)."""
     qk, torch = gpu, torch_mod
-    V, H, k = {"alone": (16384, 1024, 64), "alone_65536": (65536, 1024, 40),
+    V, H, k = {"alone": (16384, 1024, 64), "alone_65536": (65536, 1024, 40), "alone_1536_tiles": (98304, 1024, 40),
                "alone_ragged_2049_tiles": (131074, 1024, 40), "alone_k1": (65536, 1024, 1),
                "with_small_gemv": (65536, 1024, 40), "ragged_2049_tiles": (131074, 1024, 40),
                "queue_gemv": (65536, 1024, 40), "queue_ragged_2049_tiles": (131074, 1024, 40),
@@ -614,8 +615,9 @@ def test_plan_lm_head_merge_paths(gpu, torch_mod, shape):
         items.append({"mat": qk.DeviceMatrix.synth(SM, SK, sseed, 124, 130), "x": torch.from_numpy(xs).cuda(),
                       "y": torch.empty(SM, dtype=torch.float32, device="cuda")})
     plan = qk.SweepPlan(items)
-    if shape.startswith("alone"):  # per-tile lists, then the merge kernel
-        assert plan.kernel_name(0) == "bfp8_gemv_head_kernel" and plan.kernel_name(1) == "bfp8_topk_merge_kernel"
+    if shape.startswith("alone"):  # per-tile lists, then the merge kernel (its wide form past 1024 lists)
+        merge = "bfp8_topk_merge_kernel" if V <= 65536 else "bfp8_topk_merge_wide_kernel"
+        assert plan.kernel_name(0) == "bfp8_gemv_head_kernel" and plan.kernel_name(1) == merge
     elif shape.startswith("queue"):
         assert plan.kernel_name(0) == "bfp8_sweep_kernel"
     else:
