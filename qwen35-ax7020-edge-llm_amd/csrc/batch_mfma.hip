@@ -50,19 +50,23 @@ typedef int i32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kMfVec = 16;    // vectors (the MFMA's rows are vector x part)
-constexpr int kMfChunk = 16;  // blocks of split activations staged in LDS at a time
-constexpr int kMfGroup = 2;   // blocks per weight-load group
+constexpr int kMfVec = 16;   // vectors (the MFMA's rows are vector x part)
+constexpr int kMfGroup = 2;  // blocks per weight-load group
 
+// CH: blocks of split activations staged in LDS at a time (16: the whole K of
+// the configured shapes in one staging; 8: half the LDS and the staging
+// registers, for the kernel whose occupancy they limit).
+template <int CH>
 struct MfLds {
     // A operands: [block][residue][k half][part][vector], 8 bytes each: the
     // 64 lanes of one (block, residue) read 512 contiguous bytes
-    uint64_t xa[kMfChunk][4][64];
-    float xs[kMfChunk][kMfVec];      // [block][vector] block scales
-    int lo[kMfChunk], hi[kMfChunk];  // per block: e range of the one-product epilogue
+    uint64_t xa[CH][4][64];
+    float xs[CH][kMfVec];      // [block][vector] block scales
+    int lo[CH], hi[CH];        // per block: e range of the one-product epilogue
+    // the end's exchange: 3 residue groups x 2 halves x 8 values x 64 lanes at most
+    static_assert(CH * 4 * 64 * sizeof(uint64_t) >= 3 * 2 * 8 * 64 * sizeof(float),
+                  "the fs exchange fits in the staging area");
 };
-// the end's exchange: 3 residue groups x 2 halves x 8 values x 64 lanes at most
-static_assert(sizeof(MfLds::xa) >= 3 * 2 * 8 * 64 * sizeof(float), "the fs exchange fits in the staging area");
 
 // Staging of blocks c0 .. c0+nbc-1 of the B split activations and scales
 // (vectors >= B and blocks >= nbc as zeros) into LDS, with each block's
@@ -72,14 +76,13 @@ static_assert(sizeof(MfLds::xa) >= 3 * 2 * 8 * 64 * sizeof(float), "the fs excha
 // so that a caller can issue other loads between them: mf_stage_load issues
 // every load of the NT threads (one round trip to L2 for all of them),
 // mf_stage_store waits for them, writes LDS and synchronizes the workgroup.
-constexpr int kMfItems = kMfChunk * 4 * 2 * kMfVec;  // 16-byte pieces of split activations
-constexpr int kMfScales = kMfChunk * kMfVec;
-
-template <int NT>
+template <int NT, int CH>
 struct MfStaged {
-    static_assert(kMfItems % NT == 0, "whole staging rounds");
-    static constexpr int kScaleRounds = (kMfScales + NT - 1) / NT;
-    u32x4 val[kMfItems / NT];
+    static constexpr int kItems = CH * 4 * 2 * kMfVec;  // 16-byte pieces of split activations
+    static constexpr int kScales = CH * kMfVec;
+    static_assert(kItems % NT == 0, "whole staging rounds");
+    static constexpr int kScaleRounds = (kScales + NT - 1) / NT;
+    u32x4 val[kItems / NT];
     float xs[kScaleRounds];
 };
 
@@ -88,11 +91,11 @@ struct MfStaged {
 // consecutive threads are consecutive
 // kVH: -1 every vector, else only vectors 8 kVH .. 8 kVH + 7 (the others
 // staged as zeros: their MFMA rows are computed and not used).
-template <int NT, int kVH>
-__device__ __forceinline__ void mf_stage_load(MfStaged<NT>& S, const uint32_t* __restrict__ xsplit,
+template <int NT, int kVH, int CH>
+__device__ __forceinline__ void mf_stage_load(MfStaged<NT, CH>& S, const uint32_t* __restrict__ xsplit,
                                               const float* __restrict__ xscale, int nb, int B, int c0, int nbc) {
 #pragma unroll
-    for (int j = 0; j < kMfItems / NT; ++j) {
+    for (int j = 0; j < MfStaged<NT, CH>::kItems / NT; ++j) {
         const int i = threadIdx.x + j * NT;
         const int v = i % kMfVec, p = (i / kMfVec) % 2, q = (i / (2 * kMfVec)) % 4, u = i / (8 * kMfVec);
         S.val[j] = u32x4{0u, 0u, 0u, 0u};
@@ -101,26 +104,26 @@ __device__ __forceinline__ void mf_stage_load(MfStaged<NT>& S, const uint32_t* _
                 xsplit + ((size_t)v * nb + c0 + u) * BFP8_XSPLIT_WORDS_PER_BLOCK + q * 8 + p * 4);
     }
 #pragma unroll
-    for (int j = 0; j < MfStaged<NT>::kScaleRounds; ++j) {
+    for (int j = 0; j < MfStaged<NT, CH>::kScaleRounds; ++j) {
         const int i = threadIdx.x + j * NT, v = i % kMfVec, u = i / kMfVec;
-        S.xs[j] = (i < kMfScales && v < B && (kVH < 0 || (v >> 3) == kVH) && u < nbc) ? xscale[(size_t)v * nb + c0 + u]
+        S.xs[j] = (i < MfStaged<NT, CH>::kScales && v < B && (kVH < 0 || (v >> 3) == kVH) && u < nbc) ? xscale[(size_t)v * nb + c0 + u]
                                                                                         : 0.0f;
     }
 }
 
-template <int NT>
-__device__ __forceinline__ void mf_stage_store(MfLds& L, const MfStaged<NT>& S) {
+template <int NT, int CH>
+__device__ __forceinline__ void mf_stage_store(MfLds<CH>& L, const MfStaged<NT, CH>& S) {
 #pragma unroll
-    for (int j = 0; j < kMfItems / NT; ++j) {
+    for (int j = 0; j < MfStaged<NT, CH>::kItems / NT; ++j) {
         const int i = threadIdx.x + j * NT;
         const int v = i % kMfVec, p = (i / kMfVec) % 2, q = (i / (2 * kMfVec)) % 4, u = i / (8 * kMfVec);
         L.xa[u][q][p * 16 + v] = ((uint64_t)S.val[j].y << 32) | S.val[j].x;       // k half 0: bytes 0..7
         L.xa[u][q][32 + p * 16 + v] = ((uint64_t)S.val[j].w << 32) | S.val[j].z;  // k half 1: bytes 8..15
     }
 #pragma unroll
-    for (int j = 0; j < MfStaged<NT>::kScaleRounds; ++j) {
+    for (int j = 0; j < MfStaged<NT, CH>::kScaleRounds; ++j) {
         const int i = threadIdx.x + j * NT;
-        if (i < kMfScales) {  // whole wavefronts (kMfScales is a multiple of 64)
+        if (i < MfStaged<NT, CH>::kScales) {  // whole wavefronts (a multiple of 64)
             const int v = i % kMfVec, u = i / kMfVec;
             const float xs = S.xs[j];
             L.xs[u][v] = xs;
@@ -162,8 +165,8 @@ struct MfLoads {
 };
 
 // One block: an MFMA per residue of the group and the epilogue.
-template <int kRes, int kVH>
-__device__ __forceinline__ void mf_block(MfState<kRes, kVH>& st, const MfLds& L, const uint64_t (&w)[kRes], uint32_t e,
+template <int kRes, int kVH, int CH>
+__device__ __forceinline__ void mf_block(MfState<kRes, kVH>& st, const MfLds<CH>& L, const uint64_t (&w)[kRes], uint32_t e,
                                          int u, int q0, int lane) {
     constexpr int NS = MfSlots<kVH>::n, I0 = MfSlots<kVH>::i0;
     i32x16 d[kRes];
@@ -225,21 +228,21 @@ __device__ __forceinline__ void mf_issue(MfLoads<kRes>& ld, __amdgpu_buffer_rsrc
     ld.e = load_e(ers, ev + (gi * kMfGroup / 4) * 256, 0);
 }
 
-template <int kRes, int NT, int kVH>
-__device__ __forceinline__ void mf_group(MfState<kRes, kVH>& st, MfLds& L, const MfLoads<kRes>& ld, int gi, int nb,
+template <int kRes, int NT, int kVH, int CH>
+__device__ __forceinline__ void mf_group(MfState<kRes, kVH>& st, MfLds<CH>& L, const MfLoads<kRes>& ld, int gi, int nb,
                                          const uint32_t* __restrict__ xsplit, const float* __restrict__ xscale, int B,
                                          int q0, int lane) {
     const int b0 = gi * kMfGroup;
-    if (b0 % kMfChunk == 0 && b0 > 0) {  // the first chunk is staged before the loop
+    if (b0 % CH == 0 && b0 > 0) {  // the first chunk is staged before the loop
         __syncthreads();  // every wavefront is done with the previous chunk
-        MfStaged<NT> S;
-        mf_stage_load<NT, kVH>(S, xsplit, xscale, nb, B, b0, min(kMfChunk, nb - b0));
-        mf_stage_store<NT>(L, S);
+        MfStaged<NT, CH> S;
+        mf_stage_load<NT, kVH, CH>(S, xsplit, xscale, nb, B, b0, min(CH, nb - b0));
+        mf_stage_store<NT, CH>(L, S);
     }
 #pragma unroll
     for (int uu = 0; uu < kMfGroup; ++uu) {
         if (b0 + uu >= nb) break;
-        mf_block<kRes, kVH>(st, L, ld.w[uu], (ld.e >> (8 * ((b0 + uu) & 3))) & 0xffu, (b0 + uu) % kMfChunk, q0, lane);
+        mf_block<kRes, kVH, CH>(st, L, ld.w[uu], (ld.e >> (8 * ((b0 + uu) & 3))) & 0xffu, (b0 + uu) % CH, q0, lane);
     }
 }
 
@@ -247,11 +250,10 @@ __device__ __forceinline__ void mf_group(MfState<kRes, kVH>& st, MfLds& L, const
 // (kHalves == 2, wavefront w takes half w & 1), the residues of group grp,
 // the vectors of kVH (every vector, or one half of them).
 // kDepth: weight-load groups in flight per wavefront (2: one group computed
-// while the next loads; kMfChunk / kMfGroup: a chunk's every weight load
-// issued at once, for GEMVs with too few tiles to fill the memory system
-// otherwise).
-template <int kRes, int kHalves, int kDepth, int kVH>
-__device__ __forceinline__ void mf_body(MfLds& L, float* __restrict__ Y, const uint32_t* __restrict__ xsplit,
+// while the next loads; CH / kMfGroup: a chunk's every weight load issued at
+// once, for GEMVs with too few tiles to fill the memory system otherwise).
+template <int kRes, int kHalves, int kDepth, int kVH, int CH>
+__device__ __forceinline__ void mf_body(MfLds<CH>& L, float* __restrict__ Y, const uint32_t* __restrict__ xsplit,
                                         const float* __restrict__ xscale, const uint8_t* __restrict__ mant,
                                         const uint8_t* __restrict__ exps, int M, int K, int B, int t, int s, int grp) {
     constexpr int NS = MfSlots<kVH>::n, I0 = MfSlots<kVH>::i0;
@@ -273,17 +275,17 @@ __device__ __forceinline__ void mf_body(MfLds& L, float* __restrict__ Y, const u
     // weight groups: the staging then waits for its own loads only (a
     // wavefront's loads complete in the order issued)
     constexpr int NT = 64 * kHalves * (4 / kRes);
-    MfStaged<NT> S0;
-    mf_stage_load<NT, kVH>(S0, xsplit, xscale, nb, B, 0, min(kMfChunk, nb));
+    MfStaged<NT, CH> S0;
+    mf_stage_load<NT, kVH, CH>(S0, xsplit, xscale, nb, B, 0, min(CH, nb));
     MfLoads<kRes> ld[kDepth];
 #pragma unroll
     for (int d = 0; d < kDepth; ++d) mf_issue<kRes>(ld[d], wrs, ers, wv, ev, d);
-    mf_stage_store<NT>(L, S0);
+    mf_stage_store<NT, CH>(L, S0);
     for (int gi = 0; gi < ng; gi += kDepth) {
         // kDepth load sets in turn: set d holds group gi + d, then gi + d + kDepth
 #pragma unroll
         for (int d = 0; d < kDepth; ++d) {
-            if (gi + d < ng) mf_group<kRes, NT, kVH>(st, L, ld[d], gi + d, nb, xsplit, xscale, B, q0, lane);
+            if (gi + d < ng) mf_group<kRes, NT, kVH, CH>(st, L, ld[d], gi + d, nb, xsplit, xscale, B, q0, lane);
             mf_issue<kRes>(ld[d], wrs, ers, wv, ev, gi + d + kDepth);
         }
     }
@@ -329,12 +331,12 @@ __device__ __forceinline__ void mf_body(MfLds& L, float* __restrict__ Y, const u
 // go to the same XCD (blocks are dealt to the 8 XCDs in turn), so the second
 // reads the unit's weights from that XCD's L2; unit 8a + x, blocks past the
 // last unit exit at once.
-template <int kRes, int kHalves, int kDepth, int kSplit>
+template <int kRes, int kHalves, int kDepth, int kSplit, int CH>
 __global__ __launch_bounds__(64 * kHalves * (4 / kRes)) __attribute__((amdgpu_waves_per_eu(kSplit == 2 ? 2 : 4))) void
 bfp8_gemv_batch_mfma_kernel(float* __restrict__ Y, const uint32_t* __restrict__ xsplit,
                             const float* __restrict__ xscale, const uint8_t* __restrict__ mant,
                             const uint8_t* __restrict__ exps, int M, int K, int B) {
-    __shared__ MfLds L;
+    __shared__ MfLds<CH> L;
     const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int b = (int)blockIdx.x;
     const int bid = kSplit == 2 ? 8 * (b >> 4) + (b & 7) : b;
@@ -344,11 +346,11 @@ bfp8_gemv_batch_mfma_kernel(float* __restrict__ Y, const uint32_t* __restrict__ 
     const int s = kHalves == 2 ? (w & 1) : (bid & 1), grp = kHalves == 2 ? (w >> 1) : w;
     const int t = kHalves == 2 ? bid : (bid >> 1);
     if (kSplit == 1)
-        mf_body<kRes, kHalves, kDepth, -1>(L, Y, xsplit, xscale, mant, exps, M, K, B, t, s, grp);
+        mf_body<kRes, kHalves, kDepth, -1, CH>(L, Y, xsplit, xscale, mant, exps, M, K, B, t, s, grp);
     else if (((b >> 3) & 1) == 0)
-        mf_body<kRes, kHalves, kDepth, 0>(L, Y, xsplit, xscale, mant, exps, M, K, B, t, s, grp);
+        mf_body<kRes, kHalves, kDepth, 0, CH>(L, Y, xsplit, xscale, mant, exps, M, K, B, t, s, grp);
     else
-        mf_body<kRes, kHalves, kDepth, 1>(L, Y, xsplit, xscale, mant, exps, M, K, B, t, s, grp);
+        mf_body<kRes, kHalves, kDepth, 1, CH>(L, Y, xsplit, xscale, mant, exps, M, K, B, t, s, grp);
 }
 
 }  // namespace
@@ -362,14 +364,17 @@ hipError_t bfp8_launch_gemv_batch_mfma(float* Y, const uint32_t* xsplit, const f
     if (B < 1 || B > kMfVec || K < 64) return hipErrorInvalidValue;
     // few tiles: one residue per wavefront and a workgroup per 32-row half
     // (8 wavefronts per tile over two CUs) so that more run
+    // (few tiles: 16-block staging, all of a chunk's weight loads in flight;
+    // many tiles: 8-block staging, 17 KB of LDS and 110 VGPRs instead of 34 KB
+    // and 123: 17.9 against 18.5 us at 65536 x 1024, B = 16)
     if (nt < 512 && B > 8)  // and a workgroup per half of the vectors: 2 nt units, 16 blocks per 8
-        hipLaunchKernelGGL((bfp8_gemv_batch_mfma_kernel<1, 1, kMfChunk / kMfGroup, 2>), dim3(16 * ((2 * nt + 7) / 8)),
+        hipLaunchKernelGGL((bfp8_gemv_batch_mfma_kernel<1, 1, 16 / kMfGroup, 2, 16>), dim3(16 * ((2 * nt + 7) / 8)),
                            dim3(256), 0, s, Y, xsplit, xscale, mant, exps, M, K, B);
     else if (nt < 512)
-        hipLaunchKernelGGL((bfp8_gemv_batch_mfma_kernel<1, 1, kMfChunk / kMfGroup, 1>), dim3(2 * nt), dim3(256), 0, s,
+        hipLaunchKernelGGL((bfp8_gemv_batch_mfma_kernel<1, 1, 16 / kMfGroup, 1, 16>), dim3(2 * nt), dim3(256), 0, s,
                            Y, xsplit, xscale, mant, exps, M, K, B);
     else
-        hipLaunchKernelGGL((bfp8_gemv_batch_mfma_kernel<2, 2, 2, 1>), dim3(nt), dim3(256), 0, s, Y, xsplit, xscale,
+        hipLaunchKernelGGL((bfp8_gemv_batch_mfma_kernel<2, 2, 2, 1, 8>), dim3(nt), dim3(256), 0, s, Y, xsplit, xscale,
                            mant, exps, M, K, B);
     return hipGetLastError();
 }
