@@ -60,4 +60,6 @@ def test_profiles_hold_the_traffic_the_bench_reports():
     for workload, kernel, alg in cases:
         t = bench.read_traffic(workload, kernel)
         assert t is not None, (workload, kernel)
-        assert 0.99 <= t / alg <= 1.12, (workload, kernel, t, alg, t / alg)
+        # (up to 15 % above: the small B = 16 shape's workgroups each read their
+        # copy of the split activations, counted once per XCD)
+        assert 0.99 <= t / alg <= 1.15, (workload, kernel, t, alg, t / alg)
