@@ -408,7 +408,11 @@ int bfp8_dev_pack_rows(int8_t* mant_gpu, uint8_t* exps_gpu, const uint8_t* row_s
  * launch also quantizes every activation of the plan (else, and without an
  * lm_head, a quantize launch comes first).  A plan without an lm_head runs
  * one GEMV, or two reading the same x, 16 rows per workgroup, and other
- * plans of few row tiles one tile per 16-wavefront workgroup. */
+ * plans of few row tiles one tile per 16-wavefront workgroup.
+ *
+ * Runs of one plan must not overlap in time (queue them on one stream, or
+ * order them): the plan's workspaces, ticket counters and partial lists are
+ * its own. */
 typedef struct bfp8_plan_item {
     const float* x;
     float* y;
