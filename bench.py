@@ -391,6 +391,13 @@ def main():
         p.close()
 
 
+def batch_kernel(M, K):
+    """The kernel the library's batch launch picks for B = 16 (M rows, K
+    columns): a workgroup per four 64-row tiles from 512 tiles on while
+    K <= 1024, else the per-tile / per-half matrix-core kernel."""
+    return "bfp8_gemv_batch_cu_kernel" if (M + 63) // 64 >= 512 and K // 64 <= 16 else "bfp8_gemv_batch_mfma_kernel"
+
+
 def bench_batch16(args, qk, torch, np):
     """C4: B = 16 activation vectors against one weight matrix, weights read
     once per batch, at 3584 x 1024 and at 65536 x 1024, on the matrix-core
@@ -456,7 +463,7 @@ def bench_batch16(args, qk, torch, np):
                        "rotating_copies": copies,
                        "roofline": {"bound": "hbm", "achieved": round(kgbs, 2), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                                     "frac": round(kgbs / PEAK_HBM_GBPS, 4), "algorithmic_bytes": kbytes,
-                                    "traffic": read_traffic("batch16", f"bfp8_gemv_batch_mfma_kernel@{M}x{K}")}})
+                                    "traffic": read_traffic("batch16", f"{batch_kernel(M, K)}@{M}x{K}")}})
         del mats, X, Y
     # a copy of known size: the PMC counters' calibration kernel
     src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")

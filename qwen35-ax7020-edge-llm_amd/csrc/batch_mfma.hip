@@ -32,11 +32,13 @@
 // Work split: wavefront (s, g) takes a 64-row tile's 32-row half s and the
 // residues of group g (kRes residues per wavefront), keeping fs_q of its
 // residues; the wavefronts of a half combine their fs_q into y at the end
-// through LDS.  GEMVs with many tiles: a workgroup per tile, 2 residues per
-// wavefront.  GEMVs with few tiles: a workgroup per half, 1 residue per
-// wavefront, every weight load of a chunk in flight at once, and (more than
-// 8 vectors) a workgroup per half of the vectors too, so that more
-// wavefronts, each with a shorter epilogue chain, run on more CUs.
+// through LDS.  GEMVs with many tiles and K <= 1024: a workgroup per four
+// tiles, all 4 residues per wavefront (bfp8_gemv_batch_cu_kernel); with
+// larger K, a workgroup per tile, 2 residues per wavefront.  GEMVs with few
+// tiles: a workgroup per half, 1 residue per wavefront, every weight load of
+// a chunk in flight at once, and (more than 8 vectors) a workgroup per half
+// of the vectors too, so that more wavefronts, each with a shorter epilogue
+// chain, run on more CUs.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -111,7 +113,7 @@ __device__ __forceinline__ void mf_stage_load(MfStaged<NT, CH>& S, const uint32_
     }
 }
 
-template <int NT, int CH>
+template <int NT, int CH, bool kSync = true>
 __device__ __forceinline__ void mf_stage_store(MfLds<CH>& L, const MfStaged<NT, CH>& S) {
 #pragma unroll
     for (int j = 0; j < MfStaged<NT, CH>::kItems / NT; ++j) {
@@ -141,7 +143,7 @@ __device__ __forceinline__ void mf_stage_store(MfLds<CH>& L, const MfStaged<NT, 
             }
         }
     }
-    __syncthreads();
+    if (kSync) __syncthreads();
 }
 
 // A lane's result slots: register i of the MFMA result (and i + 8, the low
@@ -321,6 +323,159 @@ __device__ __forceinline__ void mf_body(MfLds<CH>& L, float* __restrict__ Y, con
     }
 }
 
+// ---- many tiles, K <= 1024: a workgroup per CU's four tiles ------------------
+// Eight wavefronts, two per SIMD; wavefront w takes tile 4 * blockIdx + w / 2,
+// its 32-row half w % 2, and all four residues, so that the per-block work
+// (exponent, one-product check, the eight scale products) is shared by 32
+// values per lane.  Its weights are 8 VGPRs per block (four residue slices,
+// 8 bytes per lane), loaded kAhead blocks ahead.  The batch's split
+// activations and scales of every block are staged into LDS once, by the
+// eight wavefronts together, with the first weight loads already in flight.
+// The two wavefronts of a SIMD run different tiles; the one issued first
+// would win every issue slot and leave the other to finish alone, so each
+// wavefront lowers its priority as it progresses (s_setprio 3 .. 0 over the
+// blocks): the one behind is served first.
+constexpr int kCuWaves = 8;
+constexpr int kCuMaxNb = 16;
+
+struct CuOps {
+    uint64_t a[4];  // MFMA A operands (split activations) per residue
+    f32x4 x0, x1;   // block scales of the lane's slots 0..3 and 4..7
+    int lo, hi;     // the block's one-product exponent range
+};
+
+// The epilogue of one block for the four residues (as mf_block's)
+__device__ __forceinline__ void cu_epilogue(float (&fs)[4][8], const i32x16 (&d)[4], const CuOps& o, uint32_t e) {
+    float xs[8];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        xs[m] = o.x0[m];
+        xs[4 + m] = o.x1[m];
+    }
+    const float es = exp_scale_ftz(e);
+    const bool one_product = (e < 8u) | ((uint32_t)((int)e - o.lo) <= (uint32_t)(o.hi - o.lo));
+    if (__builtin_amdgcn_ballot_w64(!one_product) == 0) {
+        float c[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) c[k] = es * xs[k];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int S = (int)((uint32_t)d[r][k] << 8) + d[r][k + 8];
+                fs[r][k] = fs[r][k] + (float)S * c[k];
+            }
+    } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int S = (int)((uint32_t)d[r][k] << 8) + d[r][k + 8];
+                const float t1 = (float)S * es;
+                fs[r][k] = fs[r][k] + t1 * xs[k];
+            }
+    }
+}
+
+// s_setprio takes an immediate: level 3 for blocks 0..4, 2 for 5..9, 1 for
+// 10..14, 0 after
+__device__ __forceinline__ void cu_priority(int u) {
+    const int level = u / 5;
+    if (level == 0)
+        __builtin_amdgcn_s_setprio(3);
+    else if (level == 1)
+        __builtin_amdgcn_s_setprio(2);
+    else if (level == 2)
+        __builtin_amdgcn_s_setprio(1);
+    else
+        __builtin_amdgcn_s_setprio(0);
+}
+
+template <int kAhead>
+__global__ __launch_bounds__(64 * kCuWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+bfp8_gemv_batch_cu_kernel(float* __restrict__ Y, const uint32_t* __restrict__ xsplit, const float* __restrict__ xscale,
+                          const uint8_t* __restrict__ mant, const uint8_t* __restrict__ exps, int M, int K, int B) {
+    static_assert(kAhead >= 1 && kAhead <= kCuMaxNb, "blocks in flight");
+    __shared__ MfLds<kCuMaxNb> L;
+    constexpr int NT = 64 * kCuWaves;
+    const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, col = lane & 31, kh = lane >> 5;
+    const int nb = K >> 6, nb4 = (nb + 3) >> 2;  // nb <= kCuMaxNb (host-checked)
+    const int t = (int)blockIdx.x * (kCuWaves / 2) + (w >> 1), s = w & 1;
+    const bool live = t < bfp8_ntiles(M);  // the last workgroup may hold fewer tiles
+    const int tt = live ? t : 0;
+    const __amdgpu_buffer_rsrc_t ers = make_rsrc(exps + (size_t)tt * nb4 * 256u, (uint32_t)nb4 * 256u);
+    uint32_t ev[kCuMaxNb / 4];
+#pragma unroll
+    for (int g = 0; g < kCuMaxNb / 4; ++g) ev[g] = load_e(ers, (32 * s + col) * 4 + g * 256, 0);
+    MfStaged<NT, kCuMaxNb> S0;
+    mf_stage_load<NT, -1, kCuMaxNb>(S0, xsplit, xscale, nb, B, 0, nb);
+    // residue q of block b for the lane's row and k half, through a buffer
+    // range starting at the block (the lane offset stays fixed); blocks past
+    // the tile, and wavefronts without a tile, have an empty range and read
+    // zeros without touching memory
+    const int wv = (32 * s + col) * 16 + kh * 8;
+    uint64_t wq[kCuMaxNb][4];
+    auto issue = [&](int b) {
+        const __amdgpu_buffer_rsrc_t rs =
+            make_rsrc(mant + ((size_t)tt * nb + b) * 4096u, live && b < nb ? (uint32_t)(nb - b) * 4096u : 0u);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const u32x2 v =
+                __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, wv + q * 1024, 0, kNonTemporal));
+            wq[b][q] = ((uint64_t)v.y << 32) | v.x;
+        }
+    };
+#pragma unroll
+    for (int b = 0; b < kAhead; ++b) issue(b);
+    mf_stage_store<NT, kCuMaxNb, false>(L, S0);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the staging is in LDS; the weight loads stay in flight
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (!live) return;
+
+    float fs[4][8];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) fs[r][k] = 0.0f;
+    const i32x16 zero = {};
+    // block u's LDS operands are read behind block u - 1's MFMAs
+    auto ops = [&](CuOps& o, int u) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) o.a[q] = L.xa[u][q][lane];
+        o.x0 = *reinterpret_cast<const f32x4*>(&L.xs[u][4 * kh]);
+        o.x1 = *reinterpret_cast<const f32x4*>(&L.xs[u][8 + 4 * kh]);
+        o.lo = L.lo[u];
+        o.hi = L.hi[u];
+    };
+    CuOps o[2];
+    ops(o[0], 0);
+#pragma unroll
+    for (int u = 0; u < kCuMaxNb; ++u) {
+        if (u + kAhead < kCuMaxNb) issue(u + kAhead);
+        if (u >= nb) continue;  // (uniform; the loads above read nothing past the tile)
+        cu_priority(u);
+        i32x16 d[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            d[r] = __builtin_amdgcn_mfma_i32_32x32x16_i8((long)o[u & 1].a[r], (long)wq[u][r], zero, 0, 0, 0);
+        if (u + 1 < kCuMaxNb && u + 1 < nb) ops(o[(u + 1) & 1], u + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        cu_epilogue(fs, d, o[u & 1], (ev[u >> 2] >> (8 * (u & 3))) & 0xffu);
+    }
+
+    const int row = t * 64 + 32 * s + col;
+    const int pair_rows = M & ~1;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int v = 8 * (k / 4) + 4 * kh + (k % 4);
+        const float y = (fs[0][k] + fs[2][k]) + (fs[1][k] + fs[3][k]);
+        if (v < B && row < pair_rows) Y[(size_t)v * M + row] = y;
+    }
+}
+
 // kHalves: halves of a tile per workgroup (2: both, workgroup per tile; 1:
 // workgroup per 32-row half, twice the workgroups for GEMVs with few tiles).
 // kSplit: 1, every vector in each workgroup; 2, a workgroup per half of the
@@ -363,16 +518,20 @@ hipError_t bfp8_launch_gemv_batch_mfma(float* Y, const uint32_t* xsplit, const f
     // (nb = K / 64 blocks; the split activation's stride is nb blocks)
     if (B < 1 || B > kMfVec || K < 64) return hipErrorInvalidValue;
     // few tiles: one residue per wavefront and a workgroup per 32-row half
-    // (8 wavefronts per tile over two CUs) so that more run
-    // (few tiles: 16-block staging, all of a chunk's weight loads in flight;
-    // many tiles: 8-block staging, 17 KB of LDS and 110 VGPRs instead of 34 KB
-    // and 123: 17.9 against 18.5 us at 65536 x 1024, B = 16)
+    // (8 wavefronts per tile over two CUs) so that more run, 16-block
+    // staging, all of a chunk's weight loads in flight.  Many tiles: a
+    // workgroup per four tiles, four residues per wavefront (K <= 1024; at
+    // 65536 x 1024, B = 16: 14.9-15.0 us against 18.4 for a workgroup per
+    // tile, on one box); beyond that, a workgroup per tile with 8-block staging.
     if (nt < 512 && B > 8)  // and a workgroup per half of the vectors: 2 nt units, 16 blocks per 8
         hipLaunchKernelGGL((bfp8_gemv_batch_mfma_kernel<1, 1, 16 / kMfGroup, 2, 16>), dim3(16 * ((2 * nt + 7) / 8)),
                            dim3(256), 0, s, Y, xsplit, xscale, mant, exps, M, K, B);
     else if (nt < 512)
         hipLaunchKernelGGL((bfp8_gemv_batch_mfma_kernel<1, 1, 16 / kMfGroup, 1, 16>), dim3(2 * nt), dim3(256), 0, s,
                            Y, xsplit, xscale, mant, exps, M, K, B);
+    else if ((K >> 6) <= kCuMaxNb)  // many tiles, K <= 1024: a workgroup per four tiles, two blocks ahead
+        hipLaunchKernelGGL((bfp8_gemv_batch_cu_kernel<2>), dim3((nt + kCuWaves / 2 - 1) / (kCuWaves / 2)),
+                           dim3(64 * kCuWaves), 0, s, Y, xsplit, xscale, mant, exps, M, K, B);
     else
         hipLaunchKernelGGL((bfp8_gemv_batch_mfma_kernel<2, 2, 2, 1, 8>), dim3(nt), dim3(256), 0, s, Y, xsplit, xscale,
                            mant, exps, M, K, B);

@@ -54,8 +54,8 @@ def test_profiles_hold_the_traffic_the_bench_reports():
         ("lm_head", "bfp8_gemv_head_kernel", bench.kernel_bytes(items("lm_head", lm=True))),
         ("gemv", "rt_rows_gemv_kernel", bench.kernel_bytes(items("gemv"))),
         ("down", "rt_rows_gemv_kernel", bench.kernel_bytes(items("down"))),
-        ("batch16", "bfp8_gemv_batch_mfma_kernel@3584x1024", batch_bytes(3584, 1024)),
-        ("batch16", "bfp8_gemv_batch_mfma_kernel@65536x1024", batch_bytes(65536, 1024)),
+        ("batch16", f"{bench.batch_kernel(3584, 1024)}@3584x1024", batch_bytes(3584, 1024)),
+        ("batch16", f"{bench.batch_kernel(65536, 1024)}@65536x1024", batch_bytes(65536, 1024)),
     ]
     for workload, kernel, alg in cases:
         t = bench.read_traffic(workload, kernel)
