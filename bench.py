@@ -393,9 +393,13 @@ def main():
 
 def batch_kernel(M, K):
     """The kernel the library's batch launch picks for B = 16 (M rows, K
-    columns): a workgroup per four 64-row tiles from 512 tiles on while
-    K <= 1024, else the per-tile / per-half matrix-core kernel."""
-    return "bfp8_gemv_batch_cu_kernel" if (M + 63) // 64 >= 512 and K // 64 <= 16 else "bfp8_gemv_batch_mfma_kernel"
+    columns) while K <= 1024: a workgroup per four 64-row tiles from 512
+    tiles on, below that a workgroup per half tile and half of the vectors
+    with each residue's blocks split over four wavefronts; with larger K the
+    per-tile / per-half matrix-core kernel."""
+    if K // 64 > 16:
+        return "bfp8_gemv_batch_mfma_kernel"
+    return "bfp8_gemv_batch_cu_kernel" if (M + 63) // 64 >= 512 else "bfp8_gemv_batch_split_kernel"
 
 
 def bench_batch16(args, qk, torch, np):

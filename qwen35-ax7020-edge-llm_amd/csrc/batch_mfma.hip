@@ -38,7 +38,8 @@
 // tiles: a workgroup per half, 1 residue per wavefront, every weight load of
 // a chunk in flight at once, and (more than 8 vectors) a workgroup per half
 // of the vectors too, so that more wavefronts, each with a shorter epilogue
-// chain, run on more CUs.
+// chain, run on more CUs; with K <= 1024 each residue's blocks are split
+// over four wavefronts besides (bfp8_gemv_batch_split_kernel).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -476,6 +477,155 @@ bfp8_gemv_batch_cu_kernel(float* __restrict__ Y, const uint32_t* __restrict__ xs
     }
 }
 
+// The block's terms float(S) * es * xs of the lane's four result slots of
+// vector half kVH (one product where es * xs is normal for the batch, as
+// mf_block's)
+template <int kVH>
+__device__ __forceinline__ void half_terms(float (&tv)[4], const i32x16& d, f32x4 x4, int lo, int hi, uint32_t e) {
+    constexpr int I0 = 4 * kVH;
+    const float es = exp_scale_ftz(e);
+    const bool one_product = (e < 8u) | ((uint32_t)((int)e - lo) <= (uint32_t)(hi - lo));
+    if (__builtin_amdgcn_ballot_w64(!one_product) == 0) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float c = es * x4[k];
+            const int S = (int)((uint32_t)d[I0 + k] << 8) + d[I0 + k + 8];
+            tv[k] = (float)S * c;
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int S = (int)((uint32_t)d[I0 + k] << 8) + d[I0 + k + 8];
+            const float t1 = (float)S * es;
+            tv[k] = t1 * x4[k];
+        }
+    }
+}
+// ---- few tiles, K <= 1024: a workgroup per 32-row half and half of the vectors,
+// the blocks split over four wavefronts per residue ---------------------------
+// Few tiles leave about one wavefront per SIMD with a workgroup of four
+// (one per residue), so a wavefront's chain of sixteen blocks (LDS read, MFMA,
+// epilogue, each waiting for the last) set the time.  Here wavefront (q, j)
+// computes residue q's terms float(S) * es * xs of blocks 4j .. 4j + 3 only,
+// each block's MFMA issued before the previous block's terms; the terms of
+// blocks 4 .. 15 go through LDS to wavefront (q, 0), which adds all sixteen in
+// block order (the reference's chain, unchanged).  All blocks run, also past
+// nb (K < 1024): their weights, activations and scales read as zeros, so each
+// adds an exact +0 to a sum that is never -0.
+constexpr int kSplitParts = 4;
+struct SplitLds {
+    MfLds<kCuMaxNb> a;
+    f32x4 t[kSplitParts - 1][4][4][64];     // [group - 1][residue][block of the group][lane]: the 4 slots
+    float xch[3][4][64];                     // residues 1..3: [residue - 1][slot][lane]
+};
+
+template <int kVH>
+__device__ __forceinline__ void split_body(SplitLds& L, float* __restrict__ Y, const uint32_t* __restrict__ xsplit,
+                                           const float* __restrict__ xscale, const uint8_t* __restrict__ mant,
+                                           const uint8_t* __restrict__ exps, int M, int K, int B, int t, int s, int q,
+                                           int j) {
+    constexpr int NT = 64 * 4 * kSplitParts;
+    const int lane = threadIdx.x & 63, col = lane & 31, kh = lane >> 5;
+    const int nb = K >> 6, nb4 = (nb + 3) >> 2;  // nb <= kCuMaxNb (host-checked)
+    const __amdgpu_buffer_rsrc_t ers = make_rsrc(exps + (size_t)t * nb4 * 256u, (uint32_t)nb4 * 256u);
+    const uint32_t ev = load_e(ers, (32 * s + col) * 4 + j * 256, 0);  // blocks 4j .. 4j + 3
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(mant + (size_t)t * nb * 4096u, (uint32_t)nb * 4096u);
+    const int wv = q * 1024 + (32 * s + col) * 16 + kh * 8;
+    uint64_t wq[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const u32x2 v = __builtin_bit_cast(
+            u32x2, __builtin_amdgcn_raw_buffer_load_b64(wrs, wv + (4 * j + i) * 4096, 0, kNonTemporal));
+        wq[i] = ((uint64_t)v.y << 32) | v.x;
+    }
+    // the staging of the half's split activations and scales (the workgroup's
+    // sixteen wavefronts together), the weight loads in flight
+    MfStaged<NT, kCuMaxNb> S0;
+    mf_stage_load<NT, kVH, kCuMaxNb>(S0, xsplit, xscale, nb, B, 0, nb);
+    mf_stage_store<NT, kCuMaxNb, false>(L.a, S0);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the staging is in LDS; the weight loads stay in flight
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    uint64_t a[4];
+    f32x4 x4[4];
+    int lo[4], hi[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int b = 4 * j + i;
+        a[i] = L.a.xa[b][q][lane];
+        x4[i] = *reinterpret_cast<const f32x4*>(&L.a.xs[b][8 * kVH + 4 * kh]);
+        lo[i] = L.a.lo[b];
+        hi[i] = L.a.hi[b];
+    }
+    const i32x16 zero = {};
+    float tv[4][4];
+    i32x16 d = __builtin_amdgcn_mfma_i32_32x32x16_i8((long)a[0], (long)wq[0], zero, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        i32x16 dn = zero;
+        if (i + 1 < 4) dn = __builtin_amdgcn_mfma_i32_32x32x16_i8((long)a[i + 1], (long)wq[i + 1], zero, 0, 0, 0);
+        half_terms<kVH>(tv[i], d, x4[i], lo[i], hi[i], (ev >> (8 * i)) & 0xffu);
+        d = dn;
+    }
+    if (j > 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) L.t[j - 1][q][i][lane] = f32x4{tv[i][0], tv[i][1], tv[i][2], tv[i][3]};
+    }
+    __syncthreads();
+    float fs[4];
+    if (j == 0) {
+        f32x4 tg[kSplitParts - 1][4];  // every read out first, then the chain
+#pragma unroll
+        for (int g = 0; g < kSplitParts - 1; ++g)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) tg[g][i] = L.t[g][q][i][lane];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            float f = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) f = f + tv[i][k];
+#pragma unroll
+            for (int g = 0; g < kSplitParts - 1; ++g)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) f = f + tg[g][i][k];
+            fs[k] = f;
+        }
+        if (q > 0) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) L.xch[q - 1][k][lane] = fs[k];
+        }
+    }
+    __syncthreads();
+    if (j == 0 && q == 0) {
+        const int row = t * 64 + 32 * s + col;
+        const int pair_rows = M & ~1;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float y = (fs[k] + L.xch[1][k][lane]) + (L.xch[0][k][lane] + L.xch[2][k][lane]);
+            const int v = 8 * kVH + 4 * kh + k;
+            if (v < B && row < pair_rows) Y[(size_t)v * M + row] = y;
+        }
+    }
+}
+
+// Blocks 16a + x and 16a + 8 + x (x < 8, the same XCD, so the second reads
+// the weights from its L2) take unit 8a + x's two vector halves; unit =
+// (tile, 32-row half); blocks past the last unit exit.
+__global__ __launch_bounds__(64 * 4 * kSplitParts) void bfp8_gemv_batch_split_kernel(
+    float* __restrict__ Y, const uint32_t* __restrict__ xsplit, const float* __restrict__ xscale,
+    const uint8_t* __restrict__ mant, const uint8_t* __restrict__ exps, int M, int K, int B) {
+    __shared__ SplitLds L;
+    const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int b = (int)blockIdx.x;
+    const int unit = 8 * (b >> 4) + (b & 7);
+    if (unit >= 2 * bfp8_ntiles(M)) return;  // the whole workgroup: no barrier is left waiting
+    if (((b >> 3) & 1) == 0)
+        split_body<0>(L, Y, xsplit, xscale, mant, exps, M, K, B, unit >> 1, unit & 1, w & 3, w >> 2);
+    else
+        split_body<1>(L, Y, xsplit, xscale, mant, exps, M, K, B, unit >> 1, unit & 1, w & 3, w >> 2);
+}
+
 // kHalves: halves of a tile per workgroup (2: both, workgroup per tile; 1:
 // workgroup per 32-row half, twice the workgroups for GEMVs with few tiles).
 // kSplit: 1, every vector in each workgroup; 2, a workgroup per half of the
@@ -517,13 +667,18 @@ hipError_t bfp8_launch_gemv_batch_mfma(float* Y, const uint32_t* xsplit, const f
     // a ragged K drops its last K % 64 elements, as every other GEMV path does
     // (nb = K / 64 blocks; the split activation's stride is nb blocks)
     if (B < 1 || B > kMfVec || K < 64) return hipErrorInvalidValue;
-    // few tiles: one residue per wavefront and a workgroup per 32-row half
-    // (8 wavefronts per tile over two CUs) so that more run, 16-block
-    // staging, all of a chunk's weight loads in flight.  Many tiles: a
+    // few tiles: a workgroup per 32-row half (and, above 8 vectors, per half
+    // of the vectors) so that more run; with K <= 1024 and above 8 vectors
+    // the blocks are split over four wavefronts per residue (3584 x 1024,
+    // B = 16: 5.5-5.7 us against 6.5-6.8 on one box), else one residue per
+    // wavefront, 16-block staging, all of a chunk's weight loads in flight.  Many tiles: a
     // workgroup per four tiles, four residues per wavefront (K <= 1024; at
     // 65536 x 1024, B = 16: 14.9-15.0 us against 18.4 for a workgroup per
     // tile, on one box); beyond that, a workgroup per tile with 8-block staging.
-    if (nt < 512 && B > 8)  // and a workgroup per half of the vectors: 2 nt units, 16 blocks per 8
+    if (nt < 512 && B > 8 && (K >> 6) <= kCuMaxNb)  // four wavefronts per residue, a workgroup per half of the vectors
+        hipLaunchKernelGGL(bfp8_gemv_batch_split_kernel, dim3(16 * ((2 * nt + 7) / 8)), dim3(64 * 4 * kSplitParts), 0, s,
+                           Y, xsplit, xscale, mant, exps, M, K, B);
+    else if (nt < 512 && B > 8)  // and a workgroup per half of the vectors: 2 nt units, 16 blocks per 8
         hipLaunchKernelGGL((bfp8_gemv_batch_mfma_kernel<1, 1, 16 / kMfGroup, 2, 16>), dim3(16 * ((2 * nt + 7) / 8)),
                            dim3(256), 0, s, Y, xsplit, xscale, mant, exps, M, K, B);
     else if (nt < 512)

@@ -811,7 +811,8 @@ def test_batch16_matches_sixteen_single_calls(gpu, torch_mod, M):
         assert same_f32(Y[b], y_ref), (b, mismatch(Y[b], y_ref))
 
 
-@pytest.mark.parametrize("B,M,K", [(8, 131, 512), (11, 64, 4096), (16, 1000, 1088), (16, 32769, 960), (9, 33000, 64)])
+@pytest.mark.parametrize("B,M,K", [(8, 131, 512), (11, 64, 4096), (16, 1000, 1088), (12, 1000, 960), (16, 32769, 960),
+                                   (9, 33000, 64)])
 def test_batch_scale_edges(gpu, torch_mod, B, M, K):
     """Batches of 8-16 vectors (the matrix-core kernels) whose block scales
     span the float range: every exponent byte 0-255 across rows and blocks,
@@ -839,7 +840,7 @@ def test_batch_scale_edges(gpu, torch_mod, B, M, K):
         assert same_f32(Y[b], y_ref), (B, M, K, b, mismatch(Y[b], y_ref))
 
 
-@pytest.mark.parametrize("B,M,K", [(8, 200, 1000), (16, 1000, 1105), (12, 3584, 4095), (8, 40000, 1000)])
+@pytest.mark.parametrize("B,M,K", [(8, 200, 1000), (16, 1000, 1105), (12, 3584, 4095), (8, 40000, 1000), (13, 301, 1000)])
 def test_batch_ragged_k(gpu, torch_mod, B, M, K):
     """Batches of 8-16 vectors (the matrix-core kernel) with K not a multiple
     of 64: the trailing K % 64 elements are dropped, as in the single-vector
