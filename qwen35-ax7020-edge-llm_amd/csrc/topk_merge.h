@@ -284,7 +284,8 @@ __device__ __forceinline__ void list_offer(const KF& kf, const uint64_t* list, i
 // >= T, so at least kk keys are >= T when every t_w is valid, and T = 0 admits
 // every valid key otherwise: the kk best keys are always among the keys
 // >= T.  Lists are sorted descending, so a list's candidates are a prefix.
-// The candidates are gathered in LDS and ranked (select_rank_write).
+// The candidates are gathered in LDS (one LDS atomic per wavefront for its
+// slots) and ranked (select_rank_write).
 // Returns false (uniformly) when there are more than kSelCap candidates or
 // more lists than the form covers; the caller then runs the tree merge.
 // Random scores give ~100 candidates at kk = 40 over 1,024 lists; tables of
@@ -330,16 +331,23 @@ __device__ __forceinline__ bool topk_select(const TopkArgs& d, const KF& kf, Mer
     for (int v = 0; v < W; ++v) ts = L.tw[v] < ts ? L.tw[v] : ts;
     const uint64_t T = (uint64_t)ts << 32;
     auto above = [&](uint64_t k) { return key_valid(k) && k >= T; };
-    int total = 0;
+    // slots: one LDS atomic per wavefront; within it, pass p's candidates
+    // after those of passes < p, in lane order (ballots and lane counts; a
+    // per-lane atomic was serialized lane by lane)
+    int slot[PASSES];
+    int wtotal = 0;
 #pragma unroll
-    for (int p = 0; p < PASSES; ++p) total += above(e[p]) ? 1 : 0;
-    int off = total ? atomicAdd(&L.ncand, total) : 0;
+    for (int p = 0; p < PASSES; ++p) {
+        const uint64_t mk = __builtin_amdgcn_ballot_w64(above(e[p]));
+        slot[p] = wtotal + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mk >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mk, 0u));
+        wtotal += (int)__popcll(mk);
+    }
+    int wbase = 0;
+    if (lane == 0 && wtotal > 0) wbase = atomicAdd(&L.ncand, wtotal);
+    wbase = __builtin_amdgcn_readfirstlane(wbase);
 #pragma unroll
     for (int p = 0; p < PASSES; ++p)
-        if (above(e[p])) {
-            if (off < kSelCap) L.cand[off] = e[p];
-            ++off;
-        }
+        if (above(e[p]) && wbase + slot[p] < kSelCap) L.cand[wbase + slot[p]] = e[p];
     if (KEEP) {  // lane 3 of a quad holds entry 3: the list goes on above T (rare)
 #pragma unroll
         for (int p = 0; p < PASSES; ++p)
