@@ -156,16 +156,16 @@ extern "C" __global__ __launch_bounds__(kBlkThreads) void bfp8_select_block_sort
     const int base = blockIdx.x * kSelBlock, len = min(kSelBlock, n - base);
     const int tid = threadIdx.x;
     if (tid == 0) nv = 0;
-    uint32_t mine = 0;
+    uint32_t mine = 0;  // the wavefront's valid keys (ballots; one LDS atomic per wavefront)
     uint64_t v[kBlkKeys];
 #pragma unroll
     for (int r = 0; r < kBlkKeys; ++r) {
         const int i = tid + r * kBlkThreads;
         v[r] = i < len ? topk_key(logits[base + i], base + i) : 0ull;
-        mine += v[r] != 0;
+        mine += (uint32_t)__popcll(__builtin_amdgcn_ballot_w64(v[r] != 0));
     }
     __syncthreads();
-    if (mine) atomicAdd(&nv, mine);
+    if ((tid & 63) == 0 && mine) atomicAdd(&nv, mine);
     block_sort_regs(v, s);
     for (int i = tid; i < len; i += kBlkThreads) keys[base + i] = s[i];
     if (tid == 0) valid[blockIdx.x] = nv;
@@ -300,14 +300,17 @@ extern "C" __global__ __launch_bounds__(kSortThreads) void bfp8_select_sort_kern
     __shared__ int cnt;
     if (threadIdx.x == 0) cnt = 0;
     __syncthreads();
-    int mine = 0;
-    for (int i = threadIdx.x; i < kk; i += blockDim.x) {
-        const uint64_t k = keys[i];
-        ids[i] = k ? key_id(k) : -1;
-        scores[i] = k ? key_score(k) : 0.0f;
-        mine += k != 0;
+    int mine = 0;  // the wavefront's valid keys (ballots; one LDS atomic per wavefront)
+    for (int i0 = threadIdx.x & ~63; i0 < kk; i0 += blockDim.x) {  // wavefront-uniform trip count
+        const int i = i0 + (int)(threadIdx.x & 63);
+        const uint64_t k = i < kk ? keys[i] : 0ull;
+        if (i < kk) {
+            ids[i] = k ? key_id(k) : -1;
+            scores[i] = k ? key_score(k) : 0.0f;
+        }
+        mine += (int)__popcll(__builtin_amdgcn_ballot_w64(k != 0));
     }
-    if (mine) atomicAdd(&cnt, mine);
+    if ((threadIdx.x & 63) == 0 && mine) atomicAdd(&cnt, mine);
     __syncthreads();
     if (threadIdx.x == 0) {
         const uint64_t k = keys[0];
