@@ -182,8 +182,11 @@ def cpu_baseline(items, seconds=10.0, single_seconds=6.0, batch=1, nbytes=None):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    # (200 timed steps: the wall clock's fixed cost around the loop, the first
+    # launch's latency and the final synchronization, ~15-25 us and now and
+    # then ~120 us with host jitter, spread over 200 steps instead of 50)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="sweep",
                     choices=["sweep", "layers", "lm_head", "lm_head_plain", "gemv", "down", "batch16", "lm_head_bf16",
                              "host_gemv", "select",
