@@ -529,6 +529,11 @@ __device__ __forceinline__ void split_body(SplitLds& L, float* __restrict__ Y, c
     const int nb = K >> 6, nb4 = (nb + 3) >> 2;  // nb <= kCuMaxNb (host-checked)
     const __amdgpu_buffer_rsrc_t ers = make_rsrc(exps + (size_t)t * nb4 * 256u, (uint32_t)nb4 * 256u);
     const uint32_t ev = load_e(ers, (32 * s + col) * 4 + j * 256, 0);  // blocks 4j .. 4j + 3
+    // the staging of the half's split activations and scales (the workgroup's
+    // sixteen wavefronts together), its loads issued before the weights' so
+    // that the staging waits for them alone (loads complete in issue order)
+    MfStaged<NT, kCuMaxNb> S0;
+    mf_stage_load<NT, kVH, kCuMaxNb>(S0, xsplit, xscale, nb, B, 0, nb);
     const __amdgpu_buffer_rsrc_t wrs = make_rsrc(mant + (size_t)t * nb * 4096u, (uint32_t)nb * 4096u);
     const int wv = q * 1024 + (32 * s + col) * 16 + kh * 8;
     uint64_t wq[4];
@@ -538,10 +543,6 @@ __device__ __forceinline__ void split_body(SplitLds& L, float* __restrict__ Y, c
             u32x2, __builtin_amdgcn_raw_buffer_load_b64(wrs, wv + (4 * j + i) * 4096, 0, kNonTemporal));
         wq[i] = ((uint64_t)v.y << 32) | v.x;
     }
-    // the staging of the half's split activations and scales (the workgroup's
-    // sixteen wavefronts together), the weight loads in flight
-    MfStaged<NT, kCuMaxNb> S0;
-    mf_stage_load<NT, kVH, kCuMaxNb>(S0, xsplit, xscale, nb, B, 0, nb);
     mf_stage_store<NT, kCuMaxNb, false>(L.a, S0);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the staging is in LDS; the weight loads stay in flight
