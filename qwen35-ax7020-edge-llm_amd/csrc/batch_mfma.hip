@@ -405,12 +405,15 @@ bfp8_gemv_batch_cu_kernel(float* __restrict__ Y, const uint32_t* __restrict__ xs
     const int t = (int)blockIdx.x * (kCuWaves / 2) + (w >> 1), s = w & 1;
     const bool live = t < bfp8_ntiles(M);  // the last workgroup may hold fewer tiles
     const int tt = live ? t : 0;
+    // the staging's loads first (from L2), then the row's exponents and the
+    // weights (from HBM): a wavefront's loads complete in issue order, so the
+    // staging then waits for its own round trip only
+    MfStaged<NT, kCuMaxNb> S0;
+    mf_stage_load<NT, -1, kCuMaxNb>(S0, xsplit, xscale, nb, B, 0, nb);
     const __amdgpu_buffer_rsrc_t ers = make_rsrc(exps + (size_t)tt * nb4 * 256u, (uint32_t)nb4 * 256u);
     uint32_t ev[kCuMaxNb / 4];
 #pragma unroll
     for (int g = 0; g < kCuMaxNb / 4; ++g) ev[g] = load_e(ers, (32 * s + col) * 4 + g * 256, 0);
-    MfStaged<NT, kCuMaxNb> S0;
-    mf_stage_load<NT, -1, kCuMaxNb>(S0, xsplit, xscale, nb, B, 0, nb);
     // residue q of block b for the lane's row and k half, through a buffer
     // range starting at the block (the lane offset stays fixed); blocks past
     // the tile, and wavefronts without a tile, have an empty range and read
@@ -527,13 +530,14 @@ __device__ __forceinline__ void split_body(SplitLds& L, float* __restrict__ Y, c
     constexpr int NT = 64 * 4 * kSplitParts;
     const int lane = threadIdx.x & 63, col = lane & 31, kh = lane >> 5;
     const int nb = K >> 6, nb4 = (nb + 3) >> 2;  // nb <= kCuMaxNb (host-checked)
-    const __amdgpu_buffer_rsrc_t ers = make_rsrc(exps + (size_t)t * nb4 * 256u, (uint32_t)nb4 * 256u);
-    const uint32_t ev = load_e(ers, (32 * s + col) * 4 + j * 256, 0);  // blocks 4j .. 4j + 3
     // the staging of the half's split activations and scales (the workgroup's
-    // sixteen wavefronts together), its loads issued before the weights' so
-    // that the staging waits for them alone (loads complete in issue order)
+    // sixteen wavefronts together), its loads issued before the exponents'
+    // and the weights' so that the staging waits for them alone (loads
+    // complete in issue order)
     MfStaged<NT, kCuMaxNb> S0;
     mf_stage_load<NT, kVH, kCuMaxNb>(S0, xsplit, xscale, nb, B, 0, nb);
+    const __amdgpu_buffer_rsrc_t ers = make_rsrc(exps + (size_t)t * nb4 * 256u, (uint32_t)nb4 * 256u);
+    const uint32_t ev = load_e(ers, (32 * s + col) * 4 + j * 256, 0);  // blocks 4j .. 4j + 3
     const __amdgpu_buffer_rsrc_t wrs = make_rsrc(mant + (size_t)t * nb * 4096u, (uint32_t)nb * 4096u);
     const int wv = q * 1024 + (32 * s + col) * 16 + kh * 8;
     uint64_t wq[4];
