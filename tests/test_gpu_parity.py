@@ -812,7 +812,7 @@ def test_batch16_matches_sixteen_single_calls(gpu, torch_mod, M):
 
 
 @pytest.mark.parametrize("B,M,K", [(8, 131, 512), (11, 64, 4096), (16, 1000, 1088), (12, 1000, 960), (16, 32769, 960),
-                                   (9, 33000, 64)])
+                                   (9, 33000, 64), (12, 500, 64), (10, 3, 128)])
 def test_batch_scale_edges(gpu, torch_mod, B, M, K):
     """Batches of 8-16 vectors (the matrix-core kernels) whose block scales
     span the float range: every exponent byte 0-255 across rows and blocks,
