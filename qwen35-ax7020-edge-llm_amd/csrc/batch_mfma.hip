@@ -331,7 +331,10 @@ __device__ __forceinline__ void mf_body(MfLds<CH>& L, float* __restrict__ Y, con
 // values per lane.  Its weights are 8 VGPRs per block (four residue slices,
 // 8 bytes per lane), loaded kAhead blocks ahead.  The batch's split
 // activations and scales of every block are staged into LDS once, by the
-// eight wavefronts together, with the first weight loads already in flight.
+// eight wavefronts together.  The staging's loads go out first, then the row
+// exponents, then the first blocks' weights: a wavefront's vector loads
+// complete in issue order, so the L2-resident staging never waits behind the
+// HBM round trip, and the weights are in flight during the LDS stores.
 // The two wavefronts of a SIMD run different tiles; the one issued first
 // would win every issue slot and leave the other to finish alone, so each
 // wavefront lowers its priority as it progresses (s_setprio 3 .. 0 over the
