@@ -179,6 +179,32 @@ def cpu_baseline(items, seconds=10.0, single_seconds=6.0, batch=1, nbytes=None):
     return out
 
 
+def read_probe_same_bytes(lib, qk, torch, stream, nbytes, steps):
+    """The read-bandwidth probe (`bfp8_read_probe_kernel`) over nbytes, as one
+    launch reads them: windows of nbytes rotating through >= 1 GiB (so none is
+    served from the 256 MB last-level cache), `steps` back-to-back launches
+    between one event pair.  A streaming read of that size with its ramp-up and
+    tail: what one launch of the kernel's bytes can reach here, beside the
+    8 TB/s peak."""
+    n = (nbytes + 15) // 16 * 16
+    nwin = max(2, -(-(1 << 30) // n))
+    buf = torch.empty(nwin * n, dtype=torch.uint8, device="cuda")
+    buf.fill_(1)
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    base = buf.data_ptr()
+    for i in range(2):
+        qk.check(lib.bfp8_dev_read_probe(base + (i % nwin) * n, n, sink.data_ptr(), stream.cuda_stream))
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for i in range(steps):
+        qk.check(lib.bfp8_dev_read_probe(base + (i % nwin) * n, n, sink.data_ptr(), stream.cuda_stream))
+    b.record(stream)
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) * 1e3 / steps
+    del buf
+    return {"bytes": n, "avg_us": round(us, 3), "GBps": round(n / (us * 1e-6) / 1e9, 1)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -355,6 +381,7 @@ def main():
     qk.check(lib.bfp8_dev_copy_probe(cpy.data_ptr(), buf.data_ptr(), cpy.numel(), stream.cuda_stream))
     torch.cuda.synchronize()
     del buf, cpy
+    same = read_probe_same_bytes(lib, qk, torch, stream, dom["bytes"], args.steps)
 
     traffic = read_traffic(args.workload, dom["name"])
     result = {
@@ -385,6 +412,8 @@ def main():
                      "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": traffic},
         "hbm_read_ceiling_GBps": round(ceiling, 1),
         "frac_of_measured_ceiling": round(achieved / ceiling, 4),
+        "read_probe_same_bytes": same,
+        "frac_of_same_bytes_probe": round(achieved / same["GBps"], 4),
     }
     if not args.no_cpu:
         print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
@@ -504,6 +533,8 @@ def bench_batch16(args, qk, torch, np):
         hbm_floor = kbytes / (PEAK_HBM_GBPS * 1e9) * 1e6
         epi_floor = 4.0 * M * B * (K // 64) * 4 / VALU_LANE_OPS * 1e6
         floor = max(hbm_floor, epi_floor)
+        del mats, X, Y
+        same = read_probe_same_bytes(lib, qk, torch, s, kbytes, args.steps)
         shapes.append({"M": M, "K": K, "B": B, "us": round(us, 3), "timing": timing,
                        "us_eager_calls": round(us_eager, 3), "us_graph": round(us_graph, 3),
                        "GBps": round(gbs, 2),
@@ -513,8 +544,9 @@ def bench_batch16(args, qk, torch, np):
                        "rotating_copies": copies,
                        "roofline": {"bound": "hbm", "achieved": round(kgbs, 2), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                                     "frac": round(kgbs / PEAK_HBM_GBPS, 4), "algorithmic_bytes": kbytes,
-                                    "traffic": read_traffic("batch16", f"{batch_kernel(M, K)}@{M}x{K}")}})
-        del mats, X, Y
+                                    "traffic": read_traffic("batch16", f"{batch_kernel(M, K)}@{M}x{K}")},
+                       "read_probe_same_bytes": same,
+                       "frac_of_same_bytes_probe": round(kgbs / same["GBps"], 4)})
     # a copy of known size: the PMC counters' calibration kernel
     src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
     cpy = torch.empty_like(src)

@@ -473,13 +473,15 @@ bfp8_gemv_batch_cu_kernel(float* __restrict__ Y, const uint32_t* __restrict__ xs
         cu_epilogue(fs, d, o[u & 1], (ev[u >> 2] >> (8 * (u & 3))) & 0xffu);
     }
 
+    // non-temporal stores: every wavefront writes its 2 KiB at its end, and
+    // these leave the launch's last write burst sooner
     const int row = t * 64 + 32 * s + col;
     const int pair_rows = M & ~1;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
         const int v = 8 * (k / 4) + 4 * kh + (k % 4);
         const float y = (fs[0][k] + fs[2][k]) + (fs[1][k] + fs[3][k]);
-        if (v < B && row < pair_rows) Y[(size_t)v * M + row] = y;
+        if (v < B && row < pair_rows) __builtin_nontemporal_store(y, Y + (size_t)v * M + row);
     }
 }
 
@@ -612,7 +614,7 @@ __device__ __forceinline__ void split_body(SplitLds& L, float* __restrict__ Y, c
         for (int k = 0; k < 4; ++k) {
             const float y = (fs[k] + L.xch[1][k][lane]) + (L.xch[0][k][lane] + L.xch[2][k][lane]);
             const int v = 8 * kVH + 4 * kh + k;
-            if (v < B && row < pair_rows) Y[(size_t)v * M + row] = y;
+            if (v < B && row < pair_rows) __builtin_nontemporal_store(y, Y + (size_t)v * M + row);  // as the cu kernel's
         }
     }
 }
