@@ -501,16 +501,17 @@ __device__ __forceinline__ void head_reduce(HeadTile& T, const Bfp8HeadArgs& a, 
     __syncthreads();  // L.red and L.keys are reused by the next tile
 }
 
-// The lm_head activation, and this wavefront's quantization task (a record
-// and its 64 floats), are loaded and waited for before any weight goes out:
-// a workgroup's loads queue behind the weights already requested on its CU,
-// so a load issued after them returned only when those had drained (2-3 us
-// into the launch), and the tile could not be reduced before.  The record
-// comes in by a vector load (one 8-byte word per lane) and readlanes, not by
-// scalar loads: those count on the counter that the LDS barrier below waits
-// for, and under the weight streams they returned late.  Then the weights,
-// with nothing but the arguments before them, and the task is quantized with
-// the activation while they stream.
+// The tile's first kHeadDepth blocks of weights go out first, with nothing
+// but the arguments before them; then the lm_head activation and this
+// wavefront's quantization task (a record and its 64 floats), which are
+// waited for (with those weights: a wavefront's loads complete in issue
+// order) before the activation is quantized.  The weights cannot be reduced
+// before the activation is in either way; issued first, they stream during
+// the activation's round trip instead of after it (13.08-13.22 -> 12.94-13.02
+// us for the 65536 x 1024 launch, three interleaved pairs on one box).  The
+// record comes in by a vector load (one 8-byte word per lane) and readlanes,
+// not by scalar loads: those count on the counter that the LDS barrier below
+// waits for, and under the weight streams they returned late.
 extern "C" __global__ __launch_bounds__(256) void bfp8_gemv_head_kernel(Bfp8HeadArgs a) {
     __shared__ HeadLds L;
     const int q = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
@@ -518,7 +519,13 @@ extern "C" __global__ __launch_bounds__(256) void bfp8_gemv_head_kernel(Bfp8Head
     const int nb = a.K >> 6;  // 1 .. BFP8_HEAD_MAX_NB (host-checked)
     const int wid = (int)blockIdx.x * kWaves + q, nw = (int)gridDim.x * kWaves;
 
-    // 0. the lm_head activation: block 4q + lane / 16, elements 4 (lane % 16)
+    // 0. the first weights (the tile's exponents and kHeadDepth blocks)
+    HeadTile T;
+    int t = blockIdx.x;
+    head_issue(T, a, t, nb, q, lane);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // the lm_head activation: block 4q + lane / 16, elements 4 (lane % 16)
     // + j (blocks past nb read block nb - 1 and are never stored); this
     // wavefront's task record, one 8-byte word per lane 0..5; then its element
     static_assert(BFP8_HEAD_MAX_NB == 4 * kWaves, "one block per row of 16 lanes");
@@ -530,7 +537,7 @@ extern "C" __global__ __launch_bounds__(256) void bfp8_gemv_head_kernel(Bfp8Head
     const int ti = min(wid, max(a.ntasks - 1, 0));
     typedef const __attribute__((address_space(1))) uint64_t* g_u64_ptr;
     const uint64_t tw = ((g_u64_ptr)(a.qtasks + ti))[min(lane, 5)];
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the activation and the record are in
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the activation and the record are in (the first weights too)
     __builtin_amdgcn_sched_barrier(0);
     Bfp8HeadTask task;
     {
@@ -553,13 +560,9 @@ extern "C" __global__ __launch_bounds__(256) void bfp8_gemv_head_kernel(Bfp8Head
     }
     // (a global-address-space pointer: a flat load would count on both counters)
     const float tv = ((const __attribute__((address_space(1))) float*)task.x)[lane];
-    HeadTile T;
-    int t = blockIdx.x;
-    head_issue(T, a, t, nb, q, lane);
-    __builtin_amdgcn_sched_barrier(0);
 
-    // 1. the lm_head activation, quantized into LDS while the weights are in
-    // flight: one block per row of 16 lanes, four blocks per wavefront
+    // 1. the lm_head activation, quantized into LDS: one block per row of 16
+    // lanes, four blocks per wavefront
     // (hb passed through an opaque move: left visible, the compiler derived the
     // scale's address from the record's with a 64-bit multiply-add whose
     // unused high half sat in a register a weight load targets, which made the
@@ -567,8 +570,8 @@ extern "C" __global__ __launch_bounds__(256) void bfp8_gemv_head_kernel(Bfp8Head
     int hbs;
     asm("v_mov_b32 %0, %1" : "=v"(hbs) : "v"(hb));
     bfp8_quant4_store_lds(hv, hi, &L.xsc[hbs], &L.xs[hb * 32], hb < nb);
-    // this wavefront's quantization task now too (its element came in with the
-    // activation), so that its stores go out while the weights stream
+    // this wavefront's quantization task now too (its element is the one load
+    // issued after the wait), so that its stores go out before the tile
     if (wid < a.ntasks) quantize_task(task, tv, lane, L.rec[q]);
     __syncthreads();
 
